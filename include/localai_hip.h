@@ -1,0 +1,121 @@
+/*
+ * localai_hip.h -- C ABI of liblocalai_hip.so, the MI355X (gfx950) quantized
+ * matvec / GEMM / MoE library.
+ *
+ * Two groups of entry points:
+ *
+ *  1. The reference's ten legacy exports, same names, argument order and
+ *     meaning as engine/native_quant.cpp:705-768 (bound by ctypes in
+ *     engine/native_quant.py:77-94). Host pointers in, host results out; the
+ *     work runs on the GPU. `threads` is accepted and ignored.
+ *
+ *  2. Device-pointer entry points (prefix localai_hip_). Every pointer named
+ *     *_dev is a device address, `stream` is a hipStream_t (NULL = the legacy
+ *     default stream). They return 0 on success or a LOCALAI_E* status; the
+ *     message of the last failure on the calling thread is available from
+ *     localai_hip_last_error(). Nothing throws across this boundary.
+ *
+ * Weights live on the device in a repacked, lane-interleaved form held by an
+ * opaque localai_qmat handle, created from GGML bytes (host or device).
+ */
+#ifndef LOCALAI_HIP_H
+#define LOCALAI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LOCALAI_OK 0
+#define LOCALAI_EARG 1      /* bad argument (size, shape, null pointer) */
+#define LOCALAI_ETYPE 2     /* GGML type not supported by this entry point */
+#define LOCALAI_EHIP 3      /* HIP runtime error */
+#define LOCALAI_ENOMEM 4    /* device allocation failed */
+#define LOCALAI_ESTATE 5    /* library not initialised / no device */
+
+typedef struct localai_qmat localai_qmat;
+
+/* ---- library state ------------------------------------------------------ */
+
+/* ABI version (major*100 + minor). */
+int localai_hip_version(void);
+
+/* Select the HIP device used by this thread's calls; idempotent. */
+int localai_hip_init(int device);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *localai_hip_last_error(void);
+
+/* Status of the last legacy (void-returning) call on this thread. */
+int localai_hip_last_status(void);
+
+/* (values per block, bytes per block) of a GGML type; engine/dequant.py:12-17.
+ * Returns LOCALAI_ETYPE for types engine/dequant.py rejects. */
+int localai_hip_block_layout(int ggml_type, int *values_per_block, int *bytes_per_block);
+
+/* ---- dequantisation (engine/dequant.py:27-167) -------------------------- */
+
+/* Decode n_values of GGML type `ggml_type` from raw_dev (GGML bytes) to fp32.
+ * All ten engine/dequant.py types. Bit-exact with the reference decoders. */
+int localai_hip_dequant(int ggml_type, const void *raw_dev, int64_t n_values,
+                        float *out_dev, void *stream);
+
+/* ---- device-resident weight matrices ------------------------------------ */
+
+/* Upload + repack a [batch, rows, cols] GGML tensor (batch = 1 for a plain
+ * matrix, = experts for a 3-D expert tensor, engine/zaya.py:139-150).
+ * `src_is_device` says whether ggml_bytes is a device address. Types:
+ * Q4_0, Q8_0, Q4_K, Q5_K, Q6_K (the reference's native types,
+ * engine/native_quant.py:104). cols must be a multiple of the block size. */
+int localai_hip_qmat_create(int ggml_type, int64_t rows, int64_t cols, int64_t batch,
+                            const void *ggml_bytes, int src_is_device, void *stream,
+                            localai_qmat **out);
+int localai_hip_qmat_destroy(localai_qmat *m);
+
+/* Device bytes held by the handle (repacked form). */
+int64_t localai_hip_qmat_device_bytes(const localai_qmat *m);
+
+/* Write the GGML bytes back out (inverse of the repack) to out_dev. */
+int localai_hip_qmat_unpack(const localai_qmat *m, void *out_dev, void *stream);
+
+/* Dequantise expert `expert` of a handle to fp32 [rows, cols]. */
+int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out_dev,
+                             void *stream);
+
+/* y[t, r] = sum_c W_e[r, c] * x[t, c] for t < ntok (small-batch decode matvec;
+ * ntok in 1..8 per launch, larger counts are processed in passes).
+ * x_dev is [ntok, cols] fp32 row-major, y_dev is [ntok, rows] fp32.
+ * fp32 products of exactly decoded weights, fp32 accumulation. */
+int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x_dev,
+                       float *y_dev, int ntok, void *stream);
+
+/* ---- host weight registration for the legacy exports -------------------- */
+
+/* Declare [host, host+nbytes) immutable (e.g. a GGUF mmap). Legacy calls whose
+ * `raw` lies inside a registered range reuse a cached device copy instead of
+ * uploading the bytes on every call. */
+int localai_hip_register_host(const void *host, size_t nbytes);
+int localai_hip_unregister_host(const void *host);
+/* Drop every cached device copy. */
+int localai_hip_cache_clear(void);
+
+/* ---- legacy exports: engine/native_quant.cpp:705-768 --------------------- */
+/* out[rows] = W @ x.  engine/native_quant.cpp:705-738 */
+void localai_q8_0_matvec(const uint8_t *raw, const float *x, float *out, int rows, int cols, int threads);
+void localai_q4_0_matvec(const uint8_t *raw, const float *x, float *out, int rows, int cols, int threads);
+void localai_q4k_matvec(const uint8_t *raw, const float *x, float *out, int rows, int cols, int threads);
+void localai_q5k_matvec(const uint8_t *raw, const float *x, float *out, int rows, int cols, int threads);
+void localai_q6k_matvec(const uint8_t *raw, const float *x, float *out, int rows, int cols, int threads);
+/* out[rows, tokens] = W @ vectors^T (vectors [tokens, cols]).  engine/native_quant.cpp:744-768 */
+void localai_q8_0_matmul(const uint8_t *raw, const float *vectors, float *out, int rows, int cols, int tokens, int threads);
+void localai_q4_0_matmul(const uint8_t *raw, const float *vectors, float *out, int rows, int cols, int tokens, int threads);
+void localai_q4k_matmul(const uint8_t *raw, const float *vectors, float *out, int rows, int cols, int tokens, int threads);
+void localai_q5k_matmul(const uint8_t *raw, const float *vectors, float *out, int rows, int cols, int tokens, int threads);
+void localai_q6k_matmul(const uint8_t *raw, const float *vectors, float *out, int rows, int cols, int tokens, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LOCALAI_HIP_H */

@@ -1,0 +1,63 @@
+"""Build liblocalai_hip.so (gfx950) from localai_amd/csrc with hipcc.
+
+    python -m localai_amd.build            # compile every source, link the .so
+
+Every source is compiled on each call (the objects go to localai_amd/_build/,
+the library to localai_amd/liblocalai_hip.so). Packed-fp32 instruction
+selection is disabled for all device code.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / 'csrc'
+BUILD = PKG / '_build'
+LIB = PKG / 'liblocalai_hip.so'
+ARCH = os.environ.get('LOCALAI_HIP_ARCH', 'gfx950')
+
+HIPCC = shutil.which('hipcc') or '/opt/rocm/bin/hipcc'
+COMMON = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
+          '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+          '-Wno-unused-result', '-I', str(CSRC), '-I', str(PKG.parent / 'include')]
+
+
+def sources():
+    return sorted(list(CSRC.glob('*.hip')) + list(CSRC.glob('*.cpp')))
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD / (src.name + '.o')
+    cmd = [HIPCC, *COMMON, '-c', str(src), '-o', str(obj)]
+    if src.suffix == '.cpp':
+        cmd[1:1] = ['-x', 'hip']
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f'hipcc failed for {src.name}:\n{r.stderr[-6000:]}')
+    return obj
+
+
+def build(verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    srcs = sources()
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB.with_suffix('.so.tmp')
+    cmd = [HIPCC, '-shared', f'--offload-arch={ARCH}', '-o', str(tmp), *map(str, objs)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f'link failed:\n{r.stderr[-6000:]}')
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f'built {LIB}')
+    return LIB
+
+
+if __name__ == '__main__':
+    build(verbose=True)
+    sys.exit(0)

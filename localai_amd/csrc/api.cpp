@@ -1,0 +1,208 @@
+// extern "C" entry points: library state, errors, weight handles, dequant, matvec.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "internal.h"
+
+namespace lq {
+
+static thread_local std::string g_error;
+static thread_local int g_legacy_status = LOCALAI_OK;
+static int g_device = -1;
+static std::mutex g_init_mu;
+
+int fail(int status, const std::string &msg) {
+    g_error = msg;
+    return status;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    g_error = std::string(what) + ": " + hipGetErrorString(e);
+    return e == hipErrorOutOfMemory ? LOCALAI_ENOMEM : LOCALAI_EHIP;
+}
+
+void clear_error() { g_error.clear(); }
+void set_legacy_status(int status) { g_legacy_status = status; }
+
+int ensure_device() {
+    int dev;
+    {
+        std::lock_guard<std::mutex> lk(g_init_mu);
+        if (g_device < 0) {
+            int n = 0;
+            hipError_t e = hipGetDeviceCount(&n);
+            if (e != hipSuccess || n < 1) return fail(LOCALAI_ESTATE, "no HIP device available");
+            const char *env = getenv("LOCALAI_HIP_DEVICE");
+            g_device = env ? atoi(env) : 0;
+            if (g_device < 0 || g_device >= n) return fail(LOCALAI_ESTATE, "LOCALAI_HIP_DEVICE out of range");
+        }
+        dev = g_device;
+    }
+    int cur = -1;
+    LQ_HIP(hipGetDevice(&cur));
+    if (cur != dev) LQ_HIP(hipSetDevice(dev));
+    return LOCALAI_OK;
+}
+
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" {
+
+int localai_hip_version(void) { return 100; }
+
+const char *localai_hip_last_error(void) { return g_error.c_str(); }
+
+int localai_hip_last_status(void) { return g_legacy_status; }
+
+int localai_hip_init(int device) {
+    clear_error();
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n < 1) return fail(LOCALAI_ESTATE, "no HIP device available");
+    if (device < 0 || device >= n) return fail(LOCALAI_EARG, "device index out of range");
+    {
+        std::lock_guard<std::mutex> lk(g_init_mu);
+        g_device = device;
+    }
+    LQ_HIP(hipSetDevice(device));
+    return LOCALAI_OK;
+}
+
+int localai_hip_block_layout(int t, int *vpb, int *bpb) {
+    clear_error();
+    if (lq_block_values(t) == 0) return fail(LOCALAI_ETYPE, "unsupported GGML type");
+    if (vpb) *vpb = lq_block_values(t);
+    if (bpb) *bpb = lq_block_bytes(t);
+    return LOCALAI_OK;
+}
+
+int localai_hip_dequant(int t, const void *raw, int64_t n, float *out, void *stream) {
+    clear_error();
+    int bv = lq_block_values(t);
+    if (bv == 0) return fail(LOCALAI_ETYPE, "unsupported GGML type");
+    if (n < 0 || n % bv) return fail(LOCALAI_EARG, "value count is not a multiple of the block size");
+    if (n > 0 && (!raw || !out)) return fail(LOCALAI_EARG, "null pointer");
+    if (int st = ensure_device()) return st;
+    return launch_dequant_ggml(t, raw, n, out, (hipStream_t)stream);
+}
+
+int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, const void *src,
+                            int src_is_device, void *stream, localai_qmat **out) {
+    clear_error();
+    if (!out) return fail(LOCALAI_EARG, "null output handle");
+    *out = nullptr;
+    if (!lq_repackable(t)) return fail(LOCALAI_ETYPE, "qmat: type must be Q4_0, Q8_0, Q4_K, Q5_K or Q6_K");
+    int bv = lq_block_values(t);
+    if (rows < 1 || cols < bv || cols % bv || batch < 1)
+        return fail(LOCALAI_EARG, "qmat: rows >= 1, batch >= 1 and cols a positive multiple of the block size");
+    if (!src) return fail(LOCALAI_EARG, "qmat: null source");
+    if (int st = ensure_device()) return st;
+    hipStream_t s = (hipStream_t)stream;
+    lq_geom g = lq_make_geom(t, rows, cols, batch);
+    localai_qmat *m = new localai_qmat;
+    m->g = g;
+    m->data = nullptr;
+    m->partial = nullptr;
+    m->counter = nullptr;
+    hipGetDevice(&m->device);
+    size_t nbytes = (size_t)(g.matrix_bytes * batch);
+    hipError_t e = hipMalloc(&m->data, nbytes);
+    if (e != hipSuccess) { delete m; return hip_fail(e, "hipMalloc(qmat)"); }
+    const GemvPlan plan = gemv_plan(g);
+    if (plan.ksplit > 1) {
+        e = hipMalloc(&m->partial, (size_t)plan.ksplit * 8 * g.tiles * 64 * sizeof(float));
+        if (e == hipSuccess) e = hipMalloc(&m->counter, (size_t)g.tiles * sizeof(uint32_t));
+        if (e == hipSuccess) e = hipMemset(m->counter, 0, (size_t)g.tiles * sizeof(uint32_t));
+        if (e != hipSuccess) {
+            hipFree(m->partial); hipFree(m->counter); hipFree(m->data);
+            delete m;
+            return hip_fail(e, "hipMalloc(qmat split-K scratch)");
+        }
+    }
+    const uint8_t *dsrc = (const uint8_t *)src;
+    void *staging = nullptr;
+    size_t gbytes = (size_t)(g.ggml_matrix_bytes * batch);
+    if (!src_is_device) {
+        e = hipMalloc(&staging, gbytes);
+        if (e == hipSuccess) e = hipMemcpyAsync(staging, src, gbytes, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) {
+            if (staging) hipFree(staging);
+            hipFree(m->data); hipFree(m->partial); hipFree(m->counter);
+            delete m;
+            return hip_fail(e, "qmat upload");
+        }
+        dsrc = (const uint8_t *)staging;
+    }
+    int st = launch_repack(g, dsrc, m->data, 0, s);
+    if (staging) {
+        hipError_t e2 = hipStreamSynchronize(s);
+        hipFree(staging);
+        if (st == LOCALAI_OK && e2 != hipSuccess) st = hip_fail(e2, "qmat repack");
+    }
+    if (st != LOCALAI_OK) {
+        hipFree(m->data); hipFree(m->partial); hipFree(m->counter);
+        delete m;
+        return st;
+    }
+    *out = m;
+    return LOCALAI_OK;
+}
+
+int localai_hip_qmat_destroy(localai_qmat *m) {
+    clear_error();
+    if (!m) return LOCALAI_OK;
+    hipFree(m->data);
+    hipFree(m->partial);
+    hipFree(m->counter);
+    delete m;
+    return LOCALAI_OK;
+}
+
+int64_t localai_hip_qmat_device_bytes(const localai_qmat *m) {
+    return m ? m->g.matrix_bytes * m->g.batch : 0;
+}
+
+int localai_hip_qmat_unpack(const localai_qmat *m, void *out, void *stream) {
+    clear_error();
+    if (!m || !out) return fail(LOCALAI_EARG, "null pointer");
+    if (int st = ensure_device()) return st;
+    return launch_repack(m->g, m->data, (uint8_t *)out, 1, (hipStream_t)stream);
+}
+
+int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out, void *stream) {
+    clear_error();
+    if (!m || !out) return fail(LOCALAI_EARG, "null pointer");
+    if (expert < 0 || expert >= m->g.batch) return fail(LOCALAI_EARG, "expert index out of range");
+    if (int st = ensure_device()) return st;
+    hipStream_t s = (hipStream_t)stream;
+    lq_geom one = m->g;
+    one.batch = 1;
+    void *tmp = nullptr;
+    LQ_HIP(hipMalloc(&tmp, (size_t)one.ggml_matrix_bytes));
+    int st = launch_repack(one, m->data + expert * m->g.matrix_bytes, (uint8_t *)tmp, 1, s);
+    if (st == LOCALAI_OK) st = launch_dequant_ggml(m->g.type, tmp, one.rows * one.cols, out, s);
+    hipError_t e = hipStreamSynchronize(s);
+    hipFree(tmp);
+    if (st == LOCALAI_OK && e != hipSuccess) st = hip_fail(e, "qmat dequant");
+    return st;
+}
+
+int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x, float *y, int ntok,
+                       void *stream) {
+    clear_error();
+    if (!m || !x || !y) return fail(LOCALAI_EARG, "null pointer");
+    if (expert < 0 || expert >= m->g.batch) return fail(LOCALAI_EARG, "expert index out of range");
+    if (ntok < 1) return fail(LOCALAI_EARG, "ntok must be >= 1");
+    if (int st = ensure_device()) return st;
+    lq_geom one = m->g;
+    one.batch = 1;
+    return launch_matvec(one, m->data + expert * m->g.matrix_bytes, x, m->g.cols, y, m->g.rows, ntok,
+                         m->partial, m->counter, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// Device-side helpers shared by the kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qformat.h"
+
+namespace lq {
+
+// IEEE binary16 -> binary32, exact for every input (subnormals, inf, NaN);
+// same values as half_to_float, engine/native_quant.cpp:12-33.
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffffu));
+    return (float)h;
+}
+
+// Byte i of a dword as float: each maps to one v_cvt_f32_ubyte{0..3}.
+__device__ __forceinline__ float ubyte0(uint32_t v) { return (float)(v & 0xffu); }
+__device__ __forceinline__ float ubyte1(uint32_t v) { return (float)((v >> 8) & 0xffu); }
+__device__ __forceinline__ float ubyte2(uint32_t v) { return (float)((v >> 16) & 0xffu); }
+__device__ __forceinline__ float ubyte3(uint32_t v) { return (float)(v >> 24); }
+
+// A constant the compiler cannot see through (materialised in an SGPR). Used
+// for nibble masks: with a visible constant mask the compiler narrows each
+// byte conversion into a bitfield extract plus ubyte0 conversion (two
+// instructions per value instead of one).
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    uint32_t r;
+    asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t u4_get(const uint4 &v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Sum over aligned groups of G consecutive lanes (G = 2..64); every lane of a
+// group receives the group sum. Butterfly over lane xor masks 1, 2, ..., G/2.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int m = 1; m < G; m <<= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+template <int G>
+__device__ __forceinline__ double group_sum_f64(double v) {
+#pragma unroll
+    for (int m = 1; m < G; m <<= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+__device__ __forceinline__ float uniform_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ int wave_id() {
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+
+}  // namespace lq

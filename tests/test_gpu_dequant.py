@@ -1,0 +1,82 @@
+"""GPU dequant parity: bit-exact against the oracle (and the reference golden
+decodes) for every GGML type of engine/dequant.py; repack round trips."""
+import numpy as np
+import pytest
+
+from oracle import quant
+from tests.gpu_util import bits, random_ggml
+
+pytestmark = pytest.mark.gpu
+
+ALL_TYPES = (0, 1, 2, 3, 6, 7, 8, 12, 13, 14)
+REPACK_TYPES = (2, 8, 12, 13, 14)
+
+
+@pytest.mark.parametrize('t', ALL_TYPES)
+@pytest.mark.parametrize('nblocks', (1, 3, 37))
+def test_dequant_bit_exact(t, nblocks):
+    from localai_amd import dequant
+    rng = np.random.default_rng(100 + t * 7 + nblocks)
+    block, _ = quant.block_layout(t)
+    n = block * nblocks * (64 if block == 1 else 1)
+    raw = random_ggml(rng, t, n)
+    got = dequant.dequantize(raw, t, (n,))
+    ref = quant.dequantize(raw, t, (n,))
+    np.testing.assert_array_equal(bits(got), bits(ref))
+
+
+@pytest.mark.parametrize('t', (2, 3, 6, 7, 8, 12, 13, 14))
+def test_dequant_subnormal_zero_and_extreme_scales(t):
+    from localai_amd import dequant
+    rng = np.random.default_rng(200 + t)
+    block, _ = quant.block_layout(t)
+    scales = [0.0, -0.0, 6e-8, 3e-6, -6.1e-5, 1.0, 65504.0, -2.0, 0.03125]
+    raw = random_ggml(rng, t, block * 64, scales=scales)
+    got = dequant.dequantize(raw, t, (64, block))
+    ref = quant.dequantize(raw, t, (64, block))
+    np.testing.assert_array_equal(bits(got), bits(ref))
+
+
+@pytest.mark.parametrize('t', (8, 2, 13, 12, 14))
+def test_dequant_matches_reference_golden_decode(golden, t):
+    from localai_amd import dequant
+    block, bpb = quant.block_layout(t)
+    want = golden[f'decode_{t}']
+    raw = golden[f'raw_{t}'].tobytes()[:want.shape[0] * (512 // block) * bpb]
+    np.testing.assert_array_equal(dequant.dequantize(raw, t, want.shape), want)
+
+
+def test_dequant_full_size_q4_k_ffn():
+    """14336 x 4096 Q4_K (the Llama-3-8B ffn_gate shape), bit-exact."""
+    from localai_amd import dequant, synth
+    rng = np.random.default_rng(1)
+    raw = synth.quant_tensor(rng, 12, 14336, 4096)
+    got = dequant.dequantize(raw, 12, (14336, 4096))
+    ref = quant.dequantize(raw, 12, (14336, 4096))
+    np.testing.assert_array_equal(bits(got), bits(ref))
+
+
+def test_dequant_empty_and_errors():
+    from localai_amd import dequant
+    assert dequant.dequantize(b'', 12, (0,)).shape == (0,)
+    with pytest.raises(NotImplementedError):
+        dequant.dequantize(b'\x00' * 32, 99, (16,))
+    with pytest.raises(ValueError):
+        dequant.dequantize(b'\x00' * 144, 12, (100,))
+
+
+@pytest.mark.parametrize('t', REPACK_TYPES)
+@pytest.mark.parametrize('rows,cols,batch', [(1, 256, 1), (100, 512, 3), (64, 2048, 2), (130, 768, 1)])
+def test_repack_round_trip_and_expert_dequant(t, rows, cols, batch):
+    from localai_amd import device
+    rng = np.random.default_rng(300 + t + rows)
+    raw = random_ggml(rng, t, batch * rows * cols)
+    q = device.QMat.from_ggml(raw, t, rows, cols, batch)
+    back = q.unpack().cpu().numpy().tobytes()
+    assert back == raw
+    per = len(raw) // batch
+    for e in range(batch):
+        got = q.dequant(e).cpu().numpy()
+        want = quant.dequantize(raw[e * per:(e + 1) * per], t, (rows, cols))
+        np.testing.assert_array_equal(bits(got), bits(want))
+    q.close()

@@ -1,0 +1,247 @@
+"""GPU decode-matvec parity against the fp64 oracle (exactly decoded weights),
+the reference's golden outputs and the reference's own test tolerances.
+
+Tolerance: fp32 accumulation of exact products gives errors of order 1e-6 of
+the output scale; the gate is the north-star max-rel 1e-3 (normwise:
+max|y - y_ref| / max|y_ref|) plus an elementwise check at the reference
+test suite's tolerances."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import quant
+from tests.conftest import normwise_rel
+from tests.gpu_util import random_ggml
+
+pytestmark = pytest.mark.gpu
+
+TYPES = (2, 8, 12, 13, 14)
+MAX_REL = 1e-3
+
+
+def gpu_matvec(raw, t, rows, cols, x):
+    from localai_amd import device
+    q = device.QMat.from_ggml(raw, t, rows, cols)
+    y = q.matvec(device.to_device_f32(x)).cpu().numpy()
+    q.close()
+    return y
+
+
+@pytest.mark.parametrize('t', TYPES)
+def test_golden_cases(golden, t):
+    """The reference test-suite cases (300 x 512, tests/test_dequant.py:119-230)."""
+    raw, x = golden[f'raw_{t}'].tobytes(), golden[f'x_{t}']
+    got = gpu_matvec(raw, t, 300, 512, x)
+    exact = quant.matvec_exact(raw, t, 300, 512, x)
+    assert normwise_rel(got, exact) < 1e-5
+    np.testing.assert_allclose(got, exact, rtol=2e-5, atol=2e-4)
+    if t in (2, 8, 14):   # reference kernels that are exact up to rounding: same tolerance vs AVX2
+        rtol, atol = (2e-5, 2e-4) if t == 8 else (2e-4, 2e-3)
+        np.testing.assert_allclose(got, golden[f'matvec_{t}'], rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize('t', TYPES)
+@pytest.mark.parametrize('rows', (1, 63, 64, 65, 300, 1000))
+def test_ragged_rows(t, rows):
+    rng = np.random.default_rng(rows * 31 + t)
+    block, _ = quant.block_layout(t)
+    cols = 512 if block == 256 else 96
+    raw = random_ggml(rng, t, rows * cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = gpu_matvec(raw, t, rows, cols, x)
+    assert normwise_rel(got, quant.matvec_exact(raw, t, rows, cols, x)) < 1e-5
+
+
+@pytest.mark.parametrize('t', TYPES)
+@pytest.mark.parametrize('nblocks', (1, 2, 7, 17, 56))
+def test_k_lengths(t, nblocks):
+    rng = np.random.default_rng(nblocks * 13 + t)
+    block, _ = quant.block_layout(t)
+    cols = block * nblocks
+    raw = random_ggml(rng, t, 70 * cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = gpu_matvec(raw, t, 70, cols, x)
+    assert normwise_rel(got, quant.matvec_exact(raw, t, 70, cols, x)) < 1e-5
+
+
+@pytest.mark.parametrize('t', (12, 14, 8))
+@pytest.mark.parametrize('ntok', (1, 2, 3, 5, 8, 11))
+def test_multi_vector(t, ntok):
+    from localai_amd import device
+    rng = np.random.default_rng(ntok + t)
+    rows, cols = 200, 1024
+    raw = random_ggml(rng, t, rows * cols)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    q = device.QMat.from_ggml(raw, t, rows, cols)
+    got = q.matvec(device.to_device_f32(x)).cpu().numpy()
+    want = quant.matmul_exact(raw, t, rows, cols, x)
+    assert got.shape == (ntok, rows)
+    assert normwise_rel(got, want) < 1e-5
+
+
+@pytest.mark.parametrize('name,t,rows,cols', [
+    ('ffn_gate', 12, 14336, 4096), ('ffn_down', 14, 4096, 14336), ('attn_v', 14, 1024, 4096),
+    ('attn_k', 12, 1024, 4096)])
+def test_llama3_8b_shapes(name, t, rows, cols):
+    from localai_amd import synth
+    rng = np.random.default_rng(11)
+    raw = synth.quant_tensor(rng, t, rows, cols)
+    x = synth.activations(rng, cols)
+    got = gpu_matvec(raw, t, rows, cols, x)
+    err = normwise_rel(got, quant.matvec_exact(raw, t, rows, cols, x))
+    assert err < MAX_REL
+    assert err < 1e-5, f'{name}: {err}'
+
+
+def test_expert_slices_of_a_3d_tensor():
+    """[E, rows, cols] tensor; expert e is the byte slice of engine/zaya.py:144-150."""
+    from localai_amd import device
+    rng = np.random.default_rng(5)
+    E, rows, cols = 4, 96, 512
+    raw = random_ggml(rng, 14, E * rows * cols)
+    q = device.QMat.from_ggml(raw, 14, rows, cols, batch=E)
+    x = rng.standard_normal(cols).astype(np.float32)
+    per = len(raw) // E
+    for e in range(E):
+        got = q.matvec(device.to_device_f32(x), expert=e).cpu().numpy()
+        want = quant.matvec_exact(raw[e * per:(e + 1) * per], 14, rows, cols, x)
+        assert normwise_rel(got, want) < 1e-5
+
+
+# -------------------------------------------- drop-in Python API (native_quant)
+
+def test_native_quant_mirror_contract():
+    from localai_amd import native_quant as nq
+    assert nq.get_native() is not None
+    rng = np.random.default_rng(9)
+    raw = random_ggml(rng, 12, 300 * 512)
+    x = rng.standard_normal(512).astype(np.float32)
+    y = nq.matvec(raw, x, 300, 512, 12)
+    assert y.dtype == np.float32 and y.shape == (300,)
+    assert normwise_rel(y, quant.matvec_exact(raw, 12, 300, 512, x)) < 1e-5
+    # unsupported type / misaligned cols -> None (engine/native_quant.py:104-111)
+    assert nq.matvec(raw, x, 300, 512, 3) is None
+    assert nq.matvec(raw, x[:100], 300, 100, 12) is None
+    # size mismatch -> ValueError (engine/native_quant.py:115-116)
+    with pytest.raises(ValueError):
+        nq.matvec(raw[:-144], x, 300, 512, 12)
+    with pytest.raises(ValueError):
+        nq.matvec(raw, x[:256], 300, 512, 12)
+    v = rng.standard_normal((5, 512)).astype(np.float32)
+    m = nq.matmul(raw, v, 300, 512, 12)
+    assert m.shape == (5, 300)
+    assert normwise_rel(m, quant.matmul_exact(raw, 12, 300, 512, v)) < 1e-5
+    with pytest.raises(ValueError):
+        nq.matmul(raw, v[:, :256], 300, 512, 12)
+
+
+def test_native_quant_cache_reuses_immutable_weights():
+    from localai_amd import native_quant as nq
+    rng = np.random.default_rng(10)
+    raw = random_ggml(rng, 14, 128 * 512)   # bytes: immutable
+    x = rng.standard_normal(512).astype(np.float32)
+    nq.clear_cache()
+    y1 = nq.matvec(raw, x, 128, 512, 14)
+    assert len(nq._cache) == 1
+    y2 = nq.matvec(raw, x, 128, 512, 14)
+    assert len(nq._cache) == 1
+    np.testing.assert_array_equal(y1, y2)
+    mutable = bytearray(raw)               # writable: never cached
+    y3 = nq.matvec(mutable, x, 128, 512, 14)
+    np.testing.assert_array_equal(y1, y3)
+    assert len(nq._cache) == 1
+    mutable[208:210] = np.float16(0.0).tobytes()   # change the scale of block 0 of row 0
+    y4 = nq.matvec(mutable, x, 128, 512, 14)
+    assert y4[0] != y1[0]
+    nq.clear_cache()
+
+
+# ------------------------------------------------------ legacy C exports
+
+
+def _legacy(lib, name, raw, x, rows, cols, tokens=None):
+    u8p, f32p = ctypes.POINTER(ctypes.c_uint8), ctypes.POINTER(ctypes.c_float)
+    rawa = np.frombuffer(raw, dtype=np.uint8)
+    xa = np.ascontiguousarray(x, dtype=np.float32)
+    if tokens is None:
+        out = np.empty(rows, np.float32)
+        getattr(lib, f'localai_{name}_matvec')(rawa.ctypes.data_as(u8p), xa.ctypes.data_as(f32p),
+                                               out.ctypes.data_as(f32p), rows, cols, 4)
+    else:
+        out = np.empty((rows, tokens), np.float32)
+        getattr(lib, f'localai_{name}_matmul')(rawa.ctypes.data_as(u8p), xa.ctypes.data_as(f32p),
+                                               out.ctypes.data_as(f32p), rows, cols, tokens, 4)
+    assert lib.localai_hip_last_status() == 0, lib.localai_hip_last_error()
+    return out
+
+
+@pytest.mark.parametrize('name,t', [('q8_0', 8), ('q4_0', 2), ('q4k', 12), ('q5k', 13), ('q6k', 14)])
+def test_legacy_exports(name, t):
+    from localai_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(t)
+    rows, cols = 300, 512
+    raw = random_ggml(rng, t, rows * cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = _legacy(lib, name, raw, x, rows, cols)
+    assert normwise_rel(got, quant.matvec_exact(raw, t, rows, cols, x)) < 1e-5
+    v = rng.standard_normal((5, cols)).astype(np.float32)
+    got = _legacy(lib, name, raw, v, rows, cols, tokens=5)        # [rows, tokens]
+    assert normwise_rel(got.T, quant.matmul_exact(raw, t, rows, cols, v)) < 1e-5
+
+
+def test_legacy_registered_range_uses_cached_copy():
+    from localai_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(21)
+    rows, cols = 256, 1024
+    buf = np.frombuffer(bytearray(random_ggml(rng, 12, rows * cols)), dtype=np.uint8)
+    x = rng.standard_normal(cols).astype(np.float32)
+    assert lib.localai_hip_register_host(ctypes.c_void_p(buf.ctypes.data), buf.size) == 0
+    y1 = _legacy(lib, 'q4k', buf, x, rows, cols)
+    y2 = _legacy(lib, 'q4k', buf, x, rows, cols)
+    np.testing.assert_array_equal(y1, y2)
+    assert normwise_rel(y1, quant.matvec_exact(buf.tobytes(), 12, rows, cols, x)) < 1e-5
+    assert lib.localai_hip_unregister_host(ctypes.c_void_p(buf.ctypes.data)) == 0
+    assert lib.localai_hip_unregister_host(ctypes.c_void_p(buf.ctypes.data)) == 1
+    assert lib.localai_hip_cache_clear() == 0
+
+
+@pytest.mark.parametrize('t,rows,cols', [(12, 14336, 4096), (14, 4096, 14336), (14, 1024, 4096), (8, 512, 4096)])
+def test_split_k_is_deterministic_and_rearms(t, rows, cols):
+    """Split-K workgroups combine through per-tile counters that the last
+    arrival resets; 30 back-to-back launches must give identical bits."""
+    import torch
+    from localai_amd import device, synth
+    rng = np.random.default_rng(77)
+    raw = synth.quant_tensor(rng, t, rows, cols)
+    x = device.to_device_f32(synth.activations(rng, cols))
+    q = device.QMat.from_ggml(raw, t, rows, cols)
+    outs = [q.matvec(x) for _ in range(30)]
+    torch.cuda.synchronize()
+    first = outs[0].cpu().numpy()
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), first.view(np.uint32))
+    assert normwise_rel(first, quant.matvec_exact(raw, t, rows, cols, x.cpu().numpy())) < 1e-5
+
+
+@pytest.mark.parametrize('t,rows,cols', [(12, 5 * 64, 16384), (14, 7 * 64 - 3, 14336), (12, 9 * 64, 8192),
+                                         (8, 13 * 64 + 1, 8192), (14, 3 * 64, 4096), (12, 17 * 64, 4096)])
+def test_split_k_across_xcds(t, rows, cols):
+    """Tile counts that are not multiples of the 8 XCDs, so the split-K
+    workgroups of one tile are dispatched to different XCDs (separate L2s):
+    the partials must still combine exactly, launch after launch."""
+    import torch
+    from localai_amd import device, synth
+    rng = np.random.default_rng(rows + cols)
+    raw = synth.quant_tensor(rng, t, rows, cols)
+    xh = synth.activations(rng, cols)
+    x = device.to_device_f32(xh)
+    q = device.QMat.from_ggml(raw, t, rows, cols)
+    outs = [q.matvec(x) for _ in range(40)]
+    torch.cuda.synchronize()
+    first = outs[0].cpu().numpy()
+    assert normwise_rel(first, quant.matvec_exact(raw, t, rows, cols, xh)) < 1e-5
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), first.view(np.uint32))

@@ -1,0 +1,219 @@
+"""Pins the CPU oracle (oracle/quant.py) before it is trusted as the checker.
+
+1. Known-answer bytes of the reference test suite (tests/test_dequant.py:36-95).
+2. Golden vectors written by the reference's own compiled kernels
+   (tests/golden/make_golden.py): exact decodes and matvec/matmul outputs.
+3. The live reference library (oracle/_ref), when built, on fresh random inputs.
+4. Identities the formats fix: cross-format reductions, linearity in the
+   scale, exactness of every product.
+"""
+import numpy as np
+import pytest
+
+from oracle import quant
+from oracle import ref as reflib
+
+# ---------------------------------------------------------------- 1. KATs
+
+
+def test_layouts_and_unsupported():
+    expect = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24),
+              8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+    for t, lay in expect.items():
+        assert quant.block_layout(t) == lay
+    with pytest.raises(NotImplementedError):
+        quant.block_layout(99)
+
+
+def test_q8_0_kat():
+    raw = np.float16(0.5).tobytes() + np.arange(-16, 16, dtype=np.int8).tobytes()
+    np.testing.assert_array_equal(quant.dequantize(raw, 8, (32,)), np.arange(-16, 16, dtype=np.float32) * 0.5)
+
+
+def test_q5_0_high_bits_and_signed_range():
+    raw = np.float16(1).tobytes() + bytes(4) + bytes([0x98]) * 16
+    out = quant.dequantize(raw, 6, (32,))
+    np.testing.assert_array_equal(out[:16], -8)
+    np.testing.assert_array_equal(out[16:], -7)
+
+
+def test_q5_1_affine():
+    raw = np.float16(.5).tobytes() + np.float16(1).tobytes() + bytes(4) + bytes([0x21]) * 16
+    out = quant.dequantize(raw, 7, (32,))
+    np.testing.assert_array_equal(out[:16], 1.5)
+    np.testing.assert_array_equal(out[16:], 2.0)
+
+
+def test_float_tensors():
+    v = np.array([1.25, -2.5, 0.0], dtype=np.float32)
+    np.testing.assert_array_equal(quant.dequantize(v.tobytes(), 0, (3,)), v)
+    np.testing.assert_array_equal(quant.dequantize(v.astype(np.float16).tobytes(), 1, (3,)), v)
+
+
+def test_q4_0_nibble_order():
+    out = quant.dequantize(np.float16(1).tobytes() + bytes([0x98]) * 16, 2, (32,))
+    np.testing.assert_array_equal(out[:16], 0)
+    np.testing.assert_array_equal(out[16:], 1)
+
+
+def test_q4_1_affine():
+    raw = np.float16(.5).tobytes() + np.float16(1).tobytes() + bytes([0x21]) * 16
+    out = quant.dequantize(raw, 3, (32,))
+    np.testing.assert_array_equal(out[:16], 1.5)
+    np.testing.assert_array_equal(out[16:], 2.0)
+
+
+def test_q4_k_interleaves_low_high_chunks():
+    scales = bytes([1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1])
+    qs = bytes([0x10] * 32 + [0x20] * 32 + [0x30] * 32 + [0x40] * 32)
+    raw = np.float16(1).tobytes() + np.float16(0).tobytes() + scales + qs
+    out = quant.dequantize(raw, 12, (256,))
+    for g, e in enumerate((0, 1, 0, 2, 0, 3, 0, 4)):
+        np.testing.assert_array_equal(out[g * 32:(g + 1) * 32], e)
+
+
+def test_q4_k_zero_block():
+    raw = np.float16(1).tobytes() + np.float16(0).tobytes() + bytes(12 + 128)
+    np.testing.assert_array_equal(quant.dequantize(raw, 12, (256,)), 0)
+
+
+def test_q5_k_high_bit_planes():
+    scales = bytes([1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1])
+    qs = bytes([0x10] * 32 + [0x20] * 32 + [0x30] * 32 + [0x40] * 32)
+    raw = np.float16(1).tobytes() + np.float16(0).tobytes() + scales + bytes([0xFF]) * 32 + qs
+    out = quant.dequantize(raw, 13, (256,))
+    for g, e in enumerate((16, 17, 16, 18, 16, 19, 16, 20)):
+        np.testing.assert_array_equal(out[g * 32:(g + 1) * 32], e)
+
+
+def test_q4_k_nibble_order_and_scale():
+    scales = bytes([1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1])
+    raw = np.float16(1).tobytes() + np.float16(0).tobytes() + scales + bytes([0x21]) * 128
+    out = quant.dequantize(raw, 12, (256,))
+    for g in range(8):
+        np.testing.assert_array_equal(out[g * 32:(g + 1) * 32], 1 if g % 2 == 0 else 2)
+
+
+def test_q6_k_zero_block():
+    raw = bytes(128 + 64 + 16) + np.float16(1).tobytes()
+    np.testing.assert_array_equal(quant.dequantize(raw, 14, (256,)), 0)
+
+
+def test_q6_k_packed_quads():
+    raw = bytes([0x98]) * 128 + bytes(64) + np.ones(16, dtype=np.int8).tobytes() + np.float16(1).tobytes()
+    out = quant.dequantize(raw, 14, (256,))
+    np.testing.assert_array_equal(out[:64], -24)
+    np.testing.assert_array_equal(out[64:128], -23)
+    np.testing.assert_array_equal(out[128:192], -24)
+    np.testing.assert_array_equal(out[192:], -23)
+
+
+# --------------------------------------------------------- 2. golden vectors
+
+TYPES = (8, 2, 13, 12, 14)
+
+
+@pytest.mark.parametrize('t', TYPES)
+def test_oracle_decode_matches_reference_golden(golden, t):
+    raw = golden[f'raw_{t}'].tobytes()
+    block, bpb = quant.block_layout(t)
+    rows = golden[f'decode_{t}'].shape[0]
+    got = quant.dequantize(raw[:rows * (512 // block) * bpb], t, (rows, 512))
+    np.testing.assert_array_equal(got, golden[f'decode_{t}'])
+
+
+@pytest.mark.parametrize('t', TYPES)
+def test_oracle_matvec_matches_reference_golden(golden, t):
+    raw, x = golden[f'raw_{t}'].tobytes(), golden[f'x_{t}']
+    ref_out = golden[f'matvec_{t}']
+    if t in (12, 13):   # int8-activation AVX2 path, modelled as in tests/test_dequant.py:5-33
+        model = quant.q8_activation_matvec(raw, t, 300, 512, x)
+        np.testing.assert_allclose(ref_out, model, rtol=2e-4, atol=2e-3)
+        # and the exact product differs from it by the activation rounding only
+        exact = quant.matvec_exact(raw, t, 300, 512, x)
+        assert np.max(np.abs(ref_out - exact)) < 0.05 * np.max(np.abs(exact))
+    else:               # tolerances of tests/test_dequant.py:131, :144, :230
+        rtol, atol = (2e-5, 2e-4) if t == 8 else (2e-4, 2e-3)
+        np.testing.assert_allclose(ref_out, quant.matvec_exact(raw, t, 300, 512, x), rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize('t', TYPES)
+def test_oracle_matmul_matches_reference_golden(golden, t):
+    raw, v = golden[f'raw_mm_{t}'].tobytes(), golden['vectors']
+    np.testing.assert_allclose(golden[f'matmul_{t}'], quant.matmul_exact(raw, t, 64, 512, v),
+                               rtol=3e-4, atol=3e-3)   # tests/test_dequant.py:176
+
+
+# ------------------------------------------------------ 3. live reference lib
+
+needs_ref = pytest.mark.skipif(not reflib.available(), reason='oracle/_ref not built')
+
+
+@needs_ref
+@pytest.mark.parametrize('t', TYPES)
+def test_oracle_decode_equals_reference_library(t):
+    from localai_amd import synth
+    rng = np.random.default_rng(1000 + t)
+    raw = synth.quant_tensor(rng, t, 40, 1024)
+    np.testing.assert_array_equal(quant.dequantize(raw, t, (40, 1024)), reflib.decode_rows(raw, t, 40, 1024))
+
+
+# ------------------------------------------------------------ 4. identities
+
+
+def test_q5_0_with_all_high_bits_is_q4_0_plus_8d():
+    rng = np.random.default_rng(3)
+    qs = rng.integers(0, 256, size=16, dtype=np.uint8).tobytes()
+    d = np.float16(0.37).tobytes()
+    q40 = quant.dequantize(d + qs, 2, (32,))
+    q50 = quant.dequantize(d + b'\xff' * 4 + qs, 6, (32,))
+    np.testing.assert_array_equal(q50, q40 + 8 * np.float32(np.float16(0.37)))
+    q50z = quant.dequantize(d + b'\x00' * 4 + qs, 6, (32,))
+    np.testing.assert_array_equal(q50z, q40 - 8 * np.float32(np.float16(0.37)))
+
+
+def test_q5_k_with_zero_high_bits_is_q4_k():
+    rng = np.random.default_rng(4)
+    hdr = rng.integers(0, 256, size=16, dtype=np.uint8).tobytes()
+    qs = rng.integers(0, 256, size=128, dtype=np.uint8).tobytes()
+    np.testing.assert_array_equal(quant.dequantize(hdr + bytes(32) + qs, 13, (256,)),
+                                  quant.dequantize(hdr + qs, 12, (256,)))
+
+
+def test_q4_k_scale_table_bijection():
+    # the 12 scale bytes carry 16 six-bit fields: every byte pattern decodes
+    # to a distinct (sc, mn) table and every table is reachable
+    rng = np.random.default_rng(5)
+    tables = rng.integers(0, 256, size=(2000, 12), dtype=np.uint8)
+    sc, mn = quant.kquant_scale_min(tables)
+    packed = np.concatenate([sc, mn], axis=1).astype(np.int64)
+    assert packed.max() <= 63
+    key = (packed * (64 ** np.arange(16))).sum(axis=1)
+    raw_key = [bytes(r) for r in tables]
+    assert len(set(key.tolist())) == len(set(raw_key))
+
+
+@pytest.mark.parametrize('t', (2, 8, 12, 14))
+def test_decode_is_linear_in_the_block_scale(t):
+    from localai_amd import synth
+    rng = np.random.default_rng(6)
+    raw = bytearray(synth.quant_tensor(rng, t, 4, 512))
+    block, bpb = quant.block_layout(t)
+    base = quant.dequantize(bytes(raw), t, (4, 512))
+    off = 208 if t == 14 else 0
+    for b in range(len(raw) // bpb):   # double every d (and dmin): exact doubling
+        o = b * bpb + off
+        raw[o:o + 2] = (np.frombuffer(raw[o:o + 2], np.float16) * 2).astype(np.float16).tobytes()
+        if t == 12:
+            raw[b * bpb + 2:b * bpb + 4] = (np.frombuffer(raw[b * bpb + 2:b * bpb + 4], np.float16) * 2).astype(np.float16).tobytes()
+    np.testing.assert_array_equal(quant.dequantize(bytes(raw), t, (4, 512)), 2 * base)
+
+
+def test_matvec_exact_matches_bruteforce_scalar():
+    from localai_amd import synth
+    rng = np.random.default_rng(7)
+    raw = synth.quant_tensor(rng, 14, 2, 256)
+    x = rng.standard_normal(256).astype(np.float32)
+    w = quant.dequantize(raw, 14, (2, 256))
+    brute = [sum(float(w[r, c]) * float(x[c]) for c in range(256)) for r in range(2)]
+    np.testing.assert_allclose(quant.matvec_exact(raw, 14, 2, 256, x), brute, rtol=1e-12)
