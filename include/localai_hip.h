@@ -91,6 +91,32 @@ int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out_d
 int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x_dev,
                        float *y_dev, int ntok, void *stream);
 
+/* ---- MoE expert layer ---------------------------------------------------- */
+
+/* Bytes of device workspace localai_hip_moe_forward needs for these sizes. */
+int64_t localai_hip_moe_workspace_size(int64_t tokens, int64_t experts, int top_k,
+                                       int64_t hidden, int64_t inter);
+
+/* Top-k MoE FFN layer; composition of engine/zaya.py:274-307 (router, softmax,
+ * expert selection with ties to the lower index, SiLU*up, weighted combine)
+ * and engine/zaya.py:139-175 (expert = byte slice of a 3-D tensor):
+ *   h_dev         [tokens, hidden] fp32
+ *   router_w_dev  [experts, hidden] fp32;  router_b_dev [experts] fp32 or NULL
+ *   gate_up       handle of [experts, 2*inter, hidden] (rows < inter = gate)
+ *   down          handle of [experts, hidden, inter]
+ *   out_dev       [tokens, hidden] fp32 = sum_s gate[t,s] * expert_s(h[t])
+ *   topk_idx_dev  [tokens, top_k] int32, experts by (logit desc, index asc)
+ *   topk_w_dev    [tokens, top_k] fp32, softmax over the selected logits
+ * Router logits: exact fp64 products summed in a fixed order, rounded to fp32
+ * once, so the selected experts are bit-reproducible.
+ * Limits: experts <= 1024, 1 <= top_k <= min(16, experts), inter % 64 == 0. */
+int localai_hip_moe_forward(const float *h_dev, int64_t tokens, int64_t hidden,
+                            const float *router_w_dev, const float *router_b_dev,
+                            int64_t experts, int top_k, const localai_qmat *gate_up,
+                            const localai_qmat *down, float *out_dev, int32_t *topk_idx_dev,
+                            float *topk_w_dev, void *workspace_dev, int64_t workspace_bytes,
+                            void *stream);
+
 /* ---- host weight registration for the legacy exports -------------------- */
 
 /* Declare [host, host+nbytes) immutable (e.g. a GGUF mmap). Legacy calls whose

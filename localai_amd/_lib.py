@@ -32,6 +32,9 @@ SIGNATURES = {
     'localai_hip_qmat_unpack': (_c_int, [_vp, _vp, _vp]),
     'localai_hip_qmat_dequant': (_c_int, [_vp, _c_i64, _vp, _vp]),
     'localai_hip_matvec': (_c_int, [_vp, _c_i64, _vp, _vp, _c_int, _vp]),
+    'localai_hip_moe_workspace_size': (_c_i64, [_c_i64, _c_i64, _c_int, _c_i64, _c_i64]),
+    'localai_hip_moe_forward': (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp, _vp,
+                                         _vp, _vp, _c_i64, _vp]),
     'localai_hip_register_host': (_c_int, [_vp, ctypes.c_size_t]),
     'localai_hip_unregister_host': (_c_int, [_vp]),
     'localai_hip_cache_clear': (_c_int, []),

@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -45,6 +46,20 @@ int ensure_device() {
     LQ_HIP(hipGetDevice(&cur));
     if (cur != dev) LQ_HIP(hipSetDevice(dev));
     return LOCALAI_OK;
+}
+
+size_t max_lds_per_block() {
+    static std::atomic<int64_t> cached{-1};
+    int64_t v = cached.load();
+    if (v < 0) {
+        int dev = 0, bytes = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            bytes = 64 * 1024;
+        v = bytes;
+        cached.store(v);
+    }
+    return (size_t)v;
 }
 
 }  // namespace lq
@@ -107,23 +122,10 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
     localai_qmat *m = new localai_qmat;
     m->g = g;
     m->data = nullptr;
-    m->partial = nullptr;
-    m->counter = nullptr;
     hipGetDevice(&m->device);
     size_t nbytes = (size_t)(g.matrix_bytes * batch);
     hipError_t e = hipMalloc(&m->data, nbytes);
     if (e != hipSuccess) { delete m; return hip_fail(e, "hipMalloc(qmat)"); }
-    const GemvPlan plan = gemv_plan(g);
-    if (plan.ksplit > 1) {
-        e = hipMalloc(&m->partial, (size_t)plan.ksplit * 8 * g.tiles * 64 * sizeof(float));
-        if (e == hipSuccess) e = hipMalloc(&m->counter, (size_t)g.tiles * sizeof(uint32_t));
-        if (e == hipSuccess) e = hipMemset(m->counter, 0, (size_t)g.tiles * sizeof(uint32_t));
-        if (e != hipSuccess) {
-            hipFree(m->partial); hipFree(m->counter); hipFree(m->data);
-            delete m;
-            return hip_fail(e, "hipMalloc(qmat split-K scratch)");
-        }
-    }
     const uint8_t *dsrc = (const uint8_t *)src;
     void *staging = nullptr;
     size_t gbytes = (size_t)(g.ggml_matrix_bytes * batch);
@@ -132,7 +134,7 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
         if (e == hipSuccess) e = hipMemcpyAsync(staging, src, gbytes, hipMemcpyHostToDevice, s);
         if (e != hipSuccess) {
             if (staging) hipFree(staging);
-            hipFree(m->data); hipFree(m->partial); hipFree(m->counter);
+            hipFree(m->data);
             delete m;
             return hip_fail(e, "qmat upload");
         }
@@ -145,7 +147,7 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
         if (st == LOCALAI_OK && e2 != hipSuccess) st = hip_fail(e2, "qmat repack");
     }
     if (st != LOCALAI_OK) {
-        hipFree(m->data); hipFree(m->partial); hipFree(m->counter);
+        hipFree(m->data);
         delete m;
         return st;
     }
@@ -157,8 +159,6 @@ int localai_hip_qmat_destroy(localai_qmat *m) {
     clear_error();
     if (!m) return LOCALAI_OK;
     hipFree(m->data);
-    hipFree(m->partial);
-    hipFree(m->counter);
     delete m;
     return LOCALAI_OK;
 }
@@ -202,7 +202,31 @@ int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x, fl
     lq_geom one = m->g;
     one.batch = 1;
     return launch_matvec(one, m->data + expert * m->g.matrix_bytes, x, m->g.cols, y, m->g.rows, ntok,
-                         m->partial, m->counter, (hipStream_t)stream);
+                         (hipStream_t)stream);
+}
+
+int64_t localai_hip_moe_workspace_size(int64_t T, int64_t E, int k, int64_t H, int64_t I) {
+    if (T < 1 || E < 1 || k < 1 || H < 1 || I < 1) return -1;
+    return (int64_t)moe_workspace_bytes(T, E, k, H, I);
+}
+
+int localai_hip_moe_forward(const float *h, int64_t T, int64_t H, const float *rw, const float *rb,
+                            int64_t E, int k, const localai_qmat *gu, const localai_qmat *dn, float *out,
+                            int32_t *topk_idx, float *topk_w, void *ws, int64_t ws_bytes, void *stream) {
+    clear_error();
+    if (!h || !rw || !gu || !dn || !out || !topk_idx || !topk_w || !ws) return fail(LOCALAI_EARG, "moe: null pointer");
+    if (T < 1 || H < 1) return fail(LOCALAI_EARG, "moe: tokens and hidden must be >= 1");
+    if (E < 1 || E > 1024) return fail(LOCALAI_EARG, "moe: experts must be in 1..1024");
+    if (k < 1 || k > 16 || k > E) return fail(LOCALAI_EARG, "moe: top_k must be in 1..min(16, experts)");
+    const int64_t I = gu->g.rows / 2;
+    if (gu->g.batch != E || dn->g.batch != E) return fail(LOCALAI_EARG, "moe: expert tensors must hold `experts` matrices");
+    if (gu->g.cols != H || gu->g.rows % 2 || I % 64) return fail(LOCALAI_EARG, "moe: gate_up must be [E, 2*inter, hidden] with inter % 64 == 0");
+    if (dn->g.rows != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe: down must be [E, hidden, inter]");
+    if (ws_bytes < (int64_t)moe_workspace_bytes(T, E, k, H, I)) return fail(LOCALAI_EARG, "moe: workspace too small");
+    if ((reinterpret_cast<uintptr_t>(h) & 15) || (reinterpret_cast<uintptr_t>(ws) & 255))
+        return fail(LOCALAI_EARG, "moe: h must be 16-byte and workspace 256-byte aligned");
+    if (int st = ensure_device()) return st;
+    return launch_moe(h, T, H, rw, rb, E, k, gu, dn, out, topk_idx, topk_w, ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

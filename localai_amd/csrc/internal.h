@@ -9,9 +9,7 @@
 
 struct localai_qmat {
     lq_geom g;
-    uint8_t *data;      // device, g.matrix_bytes * g.batch
-    float *partial;     // split-K partial sums of the matvec, [ksplit][8][tiles][64]
-    uint32_t *counter;  // one arrival counter per row-tile, zero between launches
+    uint8_t *data;      // device, g.matrix_bytes * g.batch (row planes, qformat.h)
     int device;
 };
 
@@ -30,20 +28,26 @@ void set_legacy_status(int status);
     } while (0)
 
 int ensure_device();   // make the library's device current for this thread
+size_t max_lds_per_block();   // LDS bytes a workgroup may use on the current device
 
 // launchers (return LOCALAI_* status)
 int launch_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *packed, int direction,
                   hipStream_t s);
 int launch_dequant_ggml(int t, const void *raw, int64_t n, float *out, hipStream_t s);
-int launch_dequant_packed(const lq_geom &g, const uint8_t *packed, float *out, hipStream_t s);
 struct GemvPlan {
-    int waves;    // waves per workgroup
-    int bpw;      // blocks per wave
-    int ksplit;   // workgroups sharing one row-tile (K split)
+    int waves;        // waves per workgroup (split the K units)
+    int slots;        // 64-value units per lane per wave
+    int rows;         // rows per workgroup
+    int lpr;          // lanes per row (64, or 32 / 16 for short rows)
+    size_t lds_bytes; // dynamic LDS (x staging) per workgroup
 };
-GemvPlan gemv_plan(const lq_geom &g);
+GemvPlan gemv_plan(const lq_geom &g, int nt);
 int launch_matvec(const lq_geom &g, const uint8_t *packed, const float *x, int64_t x_stride,
-                  float *y, int64_t y_stride, int ntok, float *partial, uint32_t *counter,
-                  hipStream_t s);
+                  float *y, int64_t y_stride, int ntok, hipStream_t s);
+
+size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I);
+int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const float *rb, int64_t E, int k,
+               const localai_qmat *gu, const localai_qmat *dn, float *out, int32_t *topk_idx, float *topk_w,
+               void *ws, hipStream_t s);
 
 }  // namespace lq

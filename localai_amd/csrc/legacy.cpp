@@ -98,7 +98,7 @@ int run(int t, const uint8_t *raw, const float *x, float *out, int rows, int col
         hipError_t e = hipMemcpy(g_x, x, (size_t)tokens * cols * 4, hipMemcpyHostToDevice);
         if (e != hipSuccess) st = hip_fail(e, "upload x");
     }
-    if (!st) st = launch_matvec(m->g, m->data, g_x, cols, g_y, rows, tokens, m->partial, m->counter, nullptr);
+    if (!st) st = launch_matvec(m->g, m->data, g_x, cols, g_y, rows, tokens, nullptr);
     if (!st) {
         if (!transpose_out) {
             hipError_t e = hipMemcpy(out, g_y, (size_t)tokens * rows * 4, hipMemcpyDeviceToHost);

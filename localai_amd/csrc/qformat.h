@@ -1,4 +1,4 @@
-// GGML block formats and the device-resident ("lane-interleaved") layout.
+// GGML block formats and the device-resident "row planes" layout.
 // Shared by host and device code.
 //
 // GGML formats (bytes per block / values per block), engine/dequant.py:8-11:
@@ -6,25 +6,34 @@
 //   Q5_1(7) 24/32  Q8_0(8) 34/32  Q4_K(12) 144/256  Q5_K(13) 176/256
 //   Q6_K(14) 210/256
 //
-// Lane-interleaved layout used by the matvec/GEMM kernels. A [rows, cols]
-// matrix is cut into row-tiles of 64 rows (rows padded with zero bytes). Each
-// GGML block is split into 16-byte "chunks" of bulk data plus an optional
-// 2-byte scalar field (the fp16 scale d of Q8_0/Q4_0/Q6_K). Inside a row-tile:
+// Row-planes layout (what a weight handle holds). A row of K values is cut
+// into U = ceil(K / 64) units of 64 values:
+//   Q4_K/Q5_K  u = 4*sb + p       group pair p (groups 2p, 2p+1) of super-block sb
+//   Q6_K       u = 4*sb + 2*h + m values 128h + 32c + 16m + (0..15), c = 0..3,
+//                                 of super-block sb (one 16-byte piece of ql,
+//                                 of ql+32 and of qh per unit)
+//   Q8_0/Q4_0  u                  blocks 2u and 2u+1 (the second is zero
+//                                 padding when the row has an odd block count)
+// Each GGML field goes to its own plane, rows one after another. Per-unit
+// 16-byte pieces are lane-interleaved: units are taken in chunks of 64 (the
+// last chunk holds C = U mod 64 units when that is not zero), and piece j of
+// the i-th unit of a chunk sits at 16 * (chunk_start * P + j * C + i) inside
+// the row (P pieces per unit), so 64 lanes that each fetch piece j of their
+// own unit read 1 KiB contiguous with one load instruction.
 //
-//   bulk : [block b][chunk c][row-in-tile 0..63][16 B]        nb * nchunk * 1 KiB
-//   d16  : [block/8][row-in-tile 0..63][8 x fp16]             ceil(nb/8) * 1 KiB
+//   Q4_K : P0 qs, 2 pieces/unit (GGML byte 16+32p+16j)   P1 d,dmin,scales (byte 0, 16 B per sb)
+//   Q5_K : P0 qs, 2 pieces/unit (byte 48+32p+16j)        P1 qh, 2 pieces per sb (byte 16+16j),
+//          interleaved per chunk of 16 super-blocks      P2 d,dmin,scales (byte 0, 16 B per sb)
+//   Q6_K : P0 ql, 2 pieces/unit (byte 64h+16m+32j)       P1 qh, 1 piece/unit (byte 128+32h+16m)
+//          P2 scales, 4 B/unit: bytes 192+8h+m+2c, c = 0..3 (the unit's four 16-value scales)
+//          P3 d (byte 208, 2 B per sb)
+//   Q8_0 : P0 qs, 4 pieces/unit (block 2u+(j>>1), byte 2+16(j&1))
+//          P1 d of blocks 2u, 2u+1 (4 B/unit)
+//   Q4_0 : P0 qs, 2 pieces/unit (block 2u+j, byte 2)     P1 d of blocks 2u, 2u+1 (4 B/unit)
 //
-// so one wave (64 lanes, lane = row) fetches chunk c of block b for 64 rows
-// with a single fully coalesced 16 B/lane load, and one more 16 B/lane load
-// brings the scales of 8 consecutive blocks. The repack is a byte permutation
-// (plus zero padding), lossless and reversible; GGML bytes stay the ABI.
-//
-// Chunk contents per type (byte ranges refer to the GGML block):
-//   Q4_K : c0 = [0,16) d,dmin,scales[12];  c1..c8 = qs [16,144)
-//   Q5_K : c0 = [0,16) d,dmin,scales;  c1..c2 = qh [16,48);  c3..c10 = qs [48,176)
-//   Q6_K : c0..c7 = ql [0,128);  c8..c11 = qh [128,192);  c12 = scales [192,208);  d16 = [208,210)
-//   Q8_0 : c0..c1 = qs [2,34);  d16 = [0,2)
-//   Q4_0 : c0 = qs [2,18);  d16 = [0,2)
+// Every piece is 16-byte aligned (GGML's 210- and 34-byte blocks are only
+// 2-byte aligned). The repack is lossless and reversible; GGML bytes remain
+// the ABI.
 #pragma once
 #include <stdint.h>
 
@@ -39,7 +48,7 @@
 #define LQ_Q5_K 13
 #define LQ_Q6_K 14
 
-#define LQ_TILE_ROWS 64
+#define LQ_MAX_PLANES 4
 
 #ifdef __HIPCC__
 #define LQ_HD __host__ __device__
@@ -68,55 +77,65 @@ LQ_HD static inline int lq_block_bytes(int t) {
     }
 }
 
-// Types that have a lane-interleaved (repacked) form and matvec/GEMM kernels.
+// Types that have a row-planes form and matvec / GEMM kernels.
 LQ_HD static inline bool lq_repackable(int t) {
     return t == LQ_Q4_0 || t == LQ_Q8_0 || t == LQ_Q4_K || t == LQ_Q5_K || t == LQ_Q6_K;
 }
 
-LQ_HD static inline int lq_nchunk(int t) {
+LQ_HD static inline int lq_nplanes(int t) {
     switch (t) {
-        case LQ_Q4_K: return 9; case LQ_Q5_K: return 11; case LQ_Q6_K: return 13;
-        case LQ_Q8_0: return 2; case LQ_Q4_0: return 1; default: return 0;
+        case LQ_Q4_K: return 2; case LQ_Q5_K: return 3; case LQ_Q6_K: return 4;
+        case LQ_Q8_0: return 2; case LQ_Q4_0: return 2; default: return 0;
     }
 }
 
-LQ_HD static inline bool lq_has_d16(int t) {
-    return t == LQ_Q6_K || t == LQ_Q8_0 || t == LQ_Q4_0;
+// Byte offset, inside a row of a lane-interleaved plane, of 16-byte piece j
+// of item i: n items per row, P pieces per item, chunks of CH items.
+LQ_HD static inline int64_t lq_ilv(int64_t i, int64_t n, int P, int j, int CH) {
+    const int64_t c0 = i - i % CH;
+    const int64_t C = n - c0 < CH ? n - c0 : CH;
+    return 16 * (c0 * P + j * C + (i - c0));
 }
-
-// GGML byte offset of chunk c inside a block
-LQ_HD static inline int lq_chunk_src(int t, int c) {
-    switch (t) {
-        case LQ_Q6_K: return 16 * c;          // ql, qh, scales are contiguous from 0
-        case LQ_Q8_0: return 2 + 16 * c;
-        case LQ_Q4_0: return 2;
-        default: return 16 * c;               // Q4_K / Q5_K: whole block is chunked
-    }
-}
-
-LQ_HD static inline int lq_d16_src(int t) { return t == LQ_Q6_K ? 208 : 0; }
 
 struct lq_geom {
     int type;
+    int nplanes;
     int64_t rows, cols, batch;   // batch = experts for a 3-D [E, rows, cols] tensor
     int64_t nb;                  // blocks per row
-    int64_t tiles;               // row-tiles per matrix
-    int64_t bulk_bytes;          // per tile
-    int64_t tile_bytes;          // per tile (bulk + d16)
-    int64_t matrix_bytes;        // per expert matrix (tiles * tile_bytes)
+    int64_t nu;                  // 64-value units per row
+    int64_t pitch[LQ_MAX_PLANES];   // bytes per row in each plane
+    int64_t plane[LQ_MAX_PLANES];   // byte offset of each plane inside one matrix
+    int64_t matrix_bytes;        // per expert matrix (256-byte aligned)
     int64_t ggml_row_bytes;      // GGML bytes per row
     int64_t ggml_matrix_bytes;   // GGML bytes per expert matrix
 };
+
+LQ_HD static inline int64_t lq_align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
 LQ_HD static inline lq_geom lq_make_geom(int t, int64_t rows, int64_t cols, int64_t batch) {
     lq_geom g;
     g.type = t; g.rows = rows; g.cols = cols; g.batch = batch;
     int bv = lq_block_values(t);
     g.nb = bv ? cols / bv : 0;
-    g.tiles = (rows + LQ_TILE_ROWS - 1) / LQ_TILE_ROWS;
-    g.bulk_bytes = g.nb * lq_nchunk(t) * 1024;
-    g.tile_bytes = g.bulk_bytes + (lq_has_d16(t) ? ((g.nb + 7) / 8) * 1024 : 0);
-    g.matrix_bytes = g.tiles * g.tile_bytes;
+    g.nu = (cols + 63) / 64;
+    g.nplanes = lq_nplanes(t);
+    const int64_t U = g.nu, nb = g.nb;
+    int64_t pitch[LQ_MAX_PLANES] = {0, 0, 0, 0};
+    switch (t) {
+        case LQ_Q4_K: pitch[0] = 32 * U; pitch[1] = 16 * nb; break;
+        case LQ_Q5_K: pitch[0] = 32 * U; pitch[1] = 32 * nb; pitch[2] = 16 * nb; break;
+        case LQ_Q6_K: pitch[0] = 32 * U; pitch[1] = 16 * U; pitch[2] = 4 * U; pitch[3] = 2 * nb; break;
+        case LQ_Q8_0: pitch[0] = 64 * U; pitch[1] = 4 * U; break;
+        case LQ_Q4_0: pitch[0] = 32 * U; pitch[1] = 4 * U; break;
+        default: break;
+    }
+    int64_t off = 0;
+    for (int p = 0; p < LQ_MAX_PLANES; ++p) {
+        g.pitch[p] = pitch[p];
+        g.plane[p] = off;
+        if (p < g.nplanes) off = lq_align256(off + rows * pitch[p]);
+    }
+    g.matrix_bytes = off;
     g.ggml_row_bytes = g.nb * lq_block_bytes(t);
     g.ggml_matrix_bytes = g.ggml_row_bytes * rows;
     return g;

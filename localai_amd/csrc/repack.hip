@@ -1,91 +1,92 @@
-// GGML <-> lane-interleaved repack (a lossless byte permutation, see qformat.h).
+// GGML <-> row-planes repack (a lossless byte permutation plus zero padding,
+// layout in qformat.h).
 #include "dev_common.h"
 #include "internal.h"
 
 namespace lq {
 
-// direction 0: ggml -> packed (padding rows written as zero); 1: packed -> ggml.
-// One thread moves one 16-byte bulk chunk or one 8-block group of fp16 scales.
+// Calls f(plane, offset inside the plane row, GGML offset inside the row or
+// -1 for zero padding, length) for every field piece owned by unit u.
+// Shared per-super-block fields are owned by the super-block's first unit.
+template <class F>
+__device__ __forceinline__ void unit_moves(const lq_geom &g, int64_t u, F f) {
+    const int64_t U = g.nu, nb = g.nb;
+    switch (g.type) {
+        case LQ_Q4_K: {
+            const int64_t sb = u >> 2, p = u & 3, base = sb * 144;
+            for (int j = 0; j < 2; ++j) f(0, lq_ilv(u, U, 2, j, 64), base + 16 + 32 * p + 16 * j, 16);
+            if (p == 0) f(1, 16 * sb, base, 16);
+            break;
+        }
+        case LQ_Q5_K: {
+            const int64_t sb = u >> 2, p = u & 3, base = sb * 176;
+            for (int j = 0; j < 2; ++j) f(0, lq_ilv(u, U, 2, j, 64), base + 48 + 32 * p + 16 * j, 16);
+            if (p == 0) {
+                for (int j = 0; j < 2; ++j) f(1, lq_ilv(sb, nb, 2, j, 16), base + 16 + 16 * j, 16);
+                f(2, 16 * sb, base, 16);
+            }
+            break;
+        }
+        case LQ_Q6_K: {
+            const int64_t sb = u >> 2, h = (u >> 1) & 1, m = u & 1, base = sb * 210;
+            for (int j = 0; j < 2; ++j) f(0, lq_ilv(u, U, 2, j, 64), base + 64 * h + 16 * m + 32 * j, 16);
+            f(1, 16 * u, base + 128 + 32 * h + 16 * m, 16);
+            for (int c = 0; c < 4; ++c) f(2, 4 * u + c, base + 192 + 8 * h + m + 2 * c, 1);
+            if ((u & 3) == 0) f(3, 2 * sb, base + 208, 2);
+            break;
+        }
+        case LQ_Q8_0: {
+            for (int j = 0; j < 4; ++j) {
+                const int64_t b = 2 * u + (j >> 1);
+                f(0, lq_ilv(u, U, 4, j, 64), b < nb ? b * 34 + 2 + 16 * (j & 1) : -1, 16);
+            }
+            for (int i = 0; i < 2; ++i) {
+                const int64_t b = 2 * u + i;
+                f(1, 4 * u + 2 * i, b < nb ? b * 34 : -1, 2);
+            }
+            break;
+        }
+        case LQ_Q4_0: {
+            for (int j = 0; j < 2; ++j) {
+                const int64_t b = 2 * u + j;
+                f(0, lq_ilv(u, U, 2, j, 64), b < nb ? b * 18 + 2 : -1, 16);
+            }
+            for (int i = 0; i < 2; ++i) {
+                const int64_t b = 2 * u + i;
+                f(1, 4 * u + 2 * i, b < nb ? b * 18 : -1, 2);
+            }
+            break;
+        }
+        default: break;
+    }
+}
+
+// direction 0: ggml -> planes (padding written as zeros); 1: planes -> ggml.
+// One thread per (matrix, row, unit); byte copies, since GGML blocks are only
+// 2-byte aligned and the repack runs once per weight upload.
 __global__ void repack_kernel(lq_geom g, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
                               int direction) {
-    const int t = g.type;
-    const int nchunk = lq_nchunk(t);
-    const int bpb = lq_block_bytes(t);
-    const int64_t ngroup = lq_has_d16(t) ? (g.nb + 7) / 8 : 0;
-    const int64_t bulk_items = g.nb * nchunk * 64;
-    const int64_t items_per_tile = bulk_items + ngroup * 64;
-    const int64_t total = g.batch * g.tiles * items_per_tile;
+    const int64_t total = g.batch * g.rows * g.nu;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
-        int64_t e = i / (g.tiles * items_per_tile);
-        int64_t rem = i - e * g.tiles * items_per_tile;
-        int64_t tile = rem / items_per_tile;
-        int64_t it = rem - tile * items_per_tile;
-        int r = (int)(it & 63);
-        int64_t row = tile * 64 + r;
-        bool live = row < g.rows;
-        uint8_t *packed_base = (direction == 0 ? dst : const_cast<uint8_t *>(src)) +
-                               e * g.matrix_bytes + tile * g.tile_bytes;
-        const uint8_t *ggml_row = (direction == 0 ? src : dst) + e * g.ggml_matrix_bytes +
-                                  row * g.ggml_row_bytes;
-        if (it < bulk_items) {
-            int64_t bc = it >> 6;                 // b * nchunk + c
-            int64_t b = bc / nchunk;
-            int c = (int)(bc - b * nchunk);
-            uint8_t *p = packed_base + it * 16;
-            int64_t goff = b * bpb + lq_chunk_src(t, c);
+        const int64_t e = i / (g.rows * g.nu);
+        const int64_t rem = i - e * g.rows * g.nu;
+        const int64_t row = rem / g.nu;
+        const int64_t u = rem - row * g.nu;
+        const int64_t grow = e * g.ggml_matrix_bytes + row * g.ggml_row_bytes;
+        unit_moves(g, u, [&](int p, int64_t pofs, int64_t gofs, int len) {
+            const int64_t prow = e * g.matrix_bytes + g.plane[p] + row * g.pitch[p] + pofs;
             if (direction == 0) {
-                uint8_t tmp[16];
-#pragma unroll
-                for (int k = 0; k < 16; ++k) tmp[k] = live ? ggml_row[goff + k] : 0;
-                uint4 v;
-                __builtin_memcpy(&v, tmp, 16);
-                *reinterpret_cast<uint4 *>(p) = v;
-            } else if (live) {
-                uint4 v = *reinterpret_cast<const uint4 *>(p);
-                uint8_t tmp[16];
-                __builtin_memcpy(tmp, &v, 16);
-                uint8_t *q = const_cast<uint8_t *>(ggml_row) + goff;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) q[k] = tmp[k];
+                for (int k = 0; k < len; ++k) dst[prow + k] = gofs >= 0 ? src[grow + gofs + k] : 0;
+            } else if (gofs >= 0) {
+                for (int k = 0; k < len; ++k) dst[grow + gofs + k] = src[prow + k];
             }
-        } else {
-            int64_t gi = (it - bulk_items) >> 6;   // group of 8 blocks
-            uint8_t *p = packed_base + g.bulk_bytes + (gi * 64 + r) * 16;
-            int dsrc = lq_d16_src(t);
-            if (direction == 0) {
-                uint8_t tmp[16];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    int64_t b = gi * 8 + k;
-                    bool ok = live && b < g.nb;
-                    tmp[2 * k] = ok ? ggml_row[b * bpb + dsrc] : 0;
-                    tmp[2 * k + 1] = ok ? ggml_row[b * bpb + dsrc + 1] : 0;
-                }
-                uint4 v;
-                __builtin_memcpy(&v, tmp, 16);
-                *reinterpret_cast<uint4 *>(p) = v;
-            } else if (live) {
-                uint4 v = *reinterpret_cast<const uint4 *>(p);
-                uint8_t tmp[16];
-                __builtin_memcpy(tmp, &v, 16);
-                uint8_t *q = const_cast<uint8_t *>(ggml_row);
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    int64_t b = gi * 8 + k;
-                    if (b < g.nb) {
-                        q[b * bpb + dsrc] = tmp[2 * k];
-                        q[b * bpb + dsrc + 1] = tmp[2 * k + 1];
-                    }
-                }
-            }
-        }
+        });
     }
 }
 
 int launch_repack(const lq_geom &g, const uint8_t *src, uint8_t *dst, int direction, hipStream_t s) {
-    const int64_t ngroup = lq_has_d16(g.type) ? (g.nb + 7) / 8 : 0;
-    const int64_t total = g.batch * g.tiles * (g.nb * lq_nchunk(g.type) + ngroup) * 64;
+    const int64_t total = g.batch * g.rows * g.nu;
     if (total <= 0) return LOCALAI_OK;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;

@@ -1,0 +1,130 @@
+"""Top-k MoE expert layer on the GPU, and the ZAYA expert-matvec drop-in.
+
+MoELayer        device-resident router + quantized expert tensors; forward()
+                runs route -> permute -> grouped gate_up (+SiLU*up) -> grouped
+                down -> weighted combine (liblocalai_hip.so, one stream).
+expert_matvec   W[e] @ x for expert e of a [E, rows, cols] GGML tensor; the
+                semantics of ZayaModel._expert_matvec (engine/zaya.py:139-175):
+                expert e is the byte slice [e*B, (e+1)*B) of the tensor.
+ZayaExpertsMixin
+                provides `_expert_matvec(self, name, expert, x)` with the
+                reference signature for a model holding `self.gguf` (a GGUFFile
+                with `.tensors[name]` -> (shape, ggml_type, offset) and `._map`).
+
+Selection semantics (generalising engine/zaya.py:290-306 to top-k): router
+logits are ranked (value desc, index asc: the np.argmax tie rule of
+engine/zaya.py:296); gates are the softmax over the k selected logits; expert
+output = W_down[e] @ (silu(g) * u) with [g; u] = W_gate_up[e] @ h (first half
+gate, engine/zaya.py:303-305).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib, device
+from .dequant import block_layout
+
+
+class MoELayer:
+    def __init__(self, router_w, gate_up_raw, down_raw, ggml_type, n_experts, hidden, inter, top_k,
+                 router_b=None, down_type=None):
+        t = device.torch()
+        self.E, self.H, self.I, self.k = int(n_experts), int(hidden), int(inter), int(top_k)
+        dev = device.device()
+        rw = np.ascontiguousarray(router_w, dtype=np.float32)
+        if rw.shape != (self.E, self.H):
+            raise ValueError(f'router weight must be [{self.E}, {self.H}], got {rw.shape}')
+        self.router_w = t.from_numpy(rw.copy()).to(dev)
+        self.router_b = None
+        if router_b is not None:
+            self.router_b = t.from_numpy(np.ascontiguousarray(router_b, dtype=np.float32).copy()).to(dev)
+        self.gate_up = device.QMat.from_ggml(gate_up_raw, ggml_type, 2 * self.I, self.H, self.E)
+        self.down = device.QMat.from_ggml(down_raw, down_type or ggml_type, self.H, self.I, self.E)
+        self._ws = {}
+
+    def workspace(self, tokens):
+        ws = self._ws.get(tokens)
+        if ws is None:
+            n = int(_lib.load().localai_hip_moe_workspace_size(tokens, self.E, self.k, self.H, self.I))
+            if n < 0:
+                raise ValueError('invalid MoE sizes')
+            ws = device.torch().empty(n, dtype=device.torch().uint8, device=device.device())
+            self._ws[tokens] = ws
+        return ws
+
+    def forward_device(self, h, out=None, idx=None, gates=None, stream=None):
+        """h: [T, H] fp32 device tensor -> (out [T, H], topk_idx [T, k] int32, gates [T, k])."""
+        t = device.torch()
+        if h.dim() == 1:
+            h = h.reshape(1, -1)
+        if h.dtype != t.float32 or not h.is_contiguous() or h.data_ptr() % 16:
+            h = h.to(t.float32).contiguous().clone()
+        T = h.shape[0]
+        if h.shape[1] != self.H:
+            raise ValueError(f'h has {h.shape[1]} features, layer expects {self.H}')
+        dev = h.device
+        out = out if out is not None else t.empty((T, self.H), dtype=t.float32, device=dev)
+        idx = idx if idx is not None else t.empty((T, self.k), dtype=t.int32, device=dev)
+        gates = gates if gates is not None else t.empty((T, self.k), dtype=t.float32, device=dev)
+        ws = self.workspace(T)
+        rb = device.ptr(self.router_b) if self.router_b is not None else None
+        _lib.check(_lib.load().localai_hip_moe_forward(
+            device.ptr(h), T, self.H, device.ptr(self.router_w), rb, self.E, self.k,
+            self.gate_up.handle, self.down.handle, device.ptr(out), device.ptr(idx), device.ptr(gates),
+            device.ptr(ws), ws.numel(), ctypes.c_void_p(device.stream_ptr(stream))))
+        return out, idx, gates
+
+    def forward(self, h):
+        """numpy [T, H] -> numpy (out [T, H], topk_idx [T, k], gates [T, k])."""
+        o, i, g = self.forward_device(device.to_device_f32(np.atleast_2d(h)))
+        return o.cpu().numpy(), i.cpu().numpy(), g.cpu().numpy()
+
+
+_expert_cache: dict = {}
+
+
+def expert_matvec(tensor_raw, shape, ggml_type, expert, x):
+    """W[expert] @ x for a [E, rows, cols] GGML tensor given as host bytes.
+
+    The whole 3-D tensor is uploaded once (cached while `tensor_raw` is
+    alive and immutable) and expert `expert` is addressed inside it, like the
+    byte slicing of engine/zaya.py:144-150.
+    """
+    from . import native_quant
+    E, rows, cols = (int(s) for s in shape)
+    block, bpb = block_layout(ggml_type)
+    if cols % block:
+        raise ValueError('expert dimensions do not align to quant blocks')
+    x = np.asarray(x, dtype=np.float32).reshape(-1)
+    if x.size != cols:
+        raise ValueError(f'expert input has {x.size} values, expected {cols}')
+    if not 0 <= int(expert) < E:
+        raise IndexError(f'expert {expert} outside [0, {E})')
+    addr, nbytes = device.host_address(tensor_raw)
+    if nbytes != E * rows * (cols // block) * bpb:
+        raise ValueError('tensor bytes do not match [E, rows, cols]')
+    key = (addr, nbytes, int(ggml_type), E, rows, cols)
+    hit = _expert_cache.get(key)
+    if hit is None:
+        q = device.QMat.from_ggml(tensor_raw, ggml_type, rows, cols, E)
+        if native_quant._immutable(tensor_raw):
+            _expert_cache[key] = (q, tensor_raw)
+    else:
+        q = hit[0]
+    return q.matvec(device.to_device_f32(x), expert=int(expert)).cpu().numpy()
+
+
+class ZayaExpertsMixin:
+    """`_expert_matvec(name, expert, x)` with the signature of engine/zaya.py:139."""
+
+    def _expert_matvec(self, name, expert, x):
+        info = self.gguf.tensors[name]
+        if len(info.shape) != 3 or info.shape[0] != self.n_experts:
+            raise ValueError(f'{name}: expected [experts,out,in], got {info.shape}')
+        block, bpb = block_layout(info.ggml_type)
+        E, rows, cols = info.shape
+        nbytes = E * rows * (cols // block) * bpb
+        raw = memoryview(self.gguf._map)[info.offset:info.offset + nbytes]
+        return expert_matvec(raw, info.shape, info.ggml_type, expert, x)

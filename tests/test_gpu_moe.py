@@ -1,0 +1,115 @@
+"""GPU MoE layer parity against the composition oracle (oracle/moe.py).
+
+Routing indices must be identical (ties to the lower expert index); gates and
+outputs within max-rel 1e-3 (normwise) -- the fp32 pipeline lands near 1e-6."""
+import numpy as np
+import pytest
+
+from oracle import moe as omoe
+from tests.conftest import normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def make_layer(rng, E, H, I, t, scale=0.02, bias=None):
+    from localai_amd import synth
+    rw = (rng.standard_normal((E, H)) * scale).astype(np.float32)
+    gu = synth.quant_tensor(rng, t, 2 * I, H, batch=E)
+    dn = synth.quant_tensor(rng, t, H, I, batch=E)
+    return rw, gu, dn
+
+
+def run_both(rw, gu, dn, t, E, H, I, k, h, bias=None):
+    from localai_amd.moe import MoELayer
+    layer = MoELayer(rw, gu, dn, t, E, H, I, k, router_b=bias)
+    out, idx, g = layer.forward(h)
+    ref_out, ref_idx, ref_g, _ = omoe.moe_forward(h, rw, gu, dn, t, E, k, I, router_bias=bias)
+    return (out, idx, g), (ref_out, ref_idx, ref_g)
+
+
+@pytest.mark.parametrize('T', (1, 8))
+def test_zaya_shaped_decode(T):
+    """hidden 2048, 16 experts, top-2, SwiGLU intermediate 4096, Q6_K experts."""
+    from localai_amd import synth
+    rng = np.random.default_rng(40 + T)
+    E, H, I, k = 16, 2048, 4096, 2
+    rw, gu, dn = make_layer(rng, E, H, I, 14)
+    h = synth.activations(rng, T, H)
+    (out, idx, g), (rout, ridx, rg) = run_both(rw, gu, dn, 14, E, H, I, k, h)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
+    assert normwise_rel(out, rout) < 1e-3
+    assert normwise_rel(out, rout) < 1e-5
+
+
+def test_qwen3_moe_style_small_prefill():
+    """128 experts, top-8, intermediate 768, Q4_K experts, Zipf-skewed router bias."""
+    from localai_amd import synth
+    rng = np.random.default_rng(7)
+    E, H, I, k, T = 128, 2048, 768, 8, 48
+    rw, gu, dn = make_layer(rng, E, H, I, 12)
+    bias = synth.zipf_bias(E)
+    h = synth.activations(rng, T, H)
+    (out, idx, g), (rout, ridx, rg) = run_both(rw, gu, dn, 12, E, H, I, k, h, bias=bias)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
+    assert normwise_rel(out, rout) < 1e-5
+
+
+def test_forced_router_ties_pick_lower_index():
+    from localai_amd import synth
+    rng = np.random.default_rng(8)
+    E, H, I, k, T = 8, 256, 256, 3, 5
+    rw, gu, dn = make_layer(rng, E, H, I, 14)
+    rw[5] = rw[2]          # experts 2 and 5 always tie
+    rw[6] = rw[2]          # and 6
+    rw[2] *= 1.0
+    h = synth.activations(rng, T, H)
+    h[:, :] = np.abs(h) * np.sign(rw[2])[None, :]   # make expert 2's logit the largest
+    (out, idx, g), (rout, ridx, rg) = run_both(rw, gu, dn, 14, E, H, I, k, h)
+    np.testing.assert_array_equal(idx, ridx)
+    assert np.all(idx[:, 0] == 2) and np.all(idx[:, 1] == 5) and np.all(idx[:, 2] == 6)
+    np.testing.assert_allclose(g, 1.0 / 3, rtol=1e-6)
+    assert normwise_rel(out, rout) < 1e-5
+
+
+def test_routing_tables_and_gates_at_full_prefill_size():
+    """512 tokens, 128 experts, top-8 (Qwen3-MoE-style shape): routing indices
+    equal the oracle's, every token's gates sum to one, output finite."""
+    from localai_amd import synth
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(9)
+    E, H, I, k, T = 128, 2048, 768, 8, 512
+    rw, gu, dn = make_layer(rng, E, H, I, 12)
+    bias = synth.zipf_bias(E)
+    h = synth.activations(rng, T, H)
+    layer = MoELayer(rw, gu, dn, 12, E, H, I, k, router_b=bias)
+    out, idx, g = layer.forward(h)
+    logits = omoe.router_logits(h, rw) + bias[None, :]
+    ridx, _ = omoe.topk(logits.astype(np.float32), k)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(g.sum(axis=1), 1.0, rtol=1e-5)
+    assert np.isfinite(out).all()
+    counts = np.bincount(idx.reshape(-1), minlength=E)
+    assert counts.sum() == T * k and counts.max() > 4 * counts.mean()   # Zipf skew present
+
+
+def test_zaya_expert_matvec_mixin():
+    from types import SimpleNamespace
+    from localai_amd import synth
+    from localai_amd.moe import ZayaExpertsMixin
+    from oracle import quant
+    rng = np.random.default_rng(10)
+    E, rows, cols = 4, 128, 512
+    raw = synth.quant_tensor(rng, 14, rows, cols, batch=E)
+    blob = b'\x00' * 64 + raw
+    gguf = SimpleNamespace(tensors={'blk.1.ffn_down_exps.weight': SimpleNamespace(
+        shape=(E, rows, cols), ggml_type=14, offset=64)}, _map=blob)
+    model = type('M', (ZayaExpertsMixin,), {})()
+    model.gguf, model.n_experts = gguf, E
+    x = rng.standard_normal(cols).astype(np.float32)
+    per = len(raw) // E
+    for e in range(E):
+        got = model._expert_matvec('blk.1.ffn_down_exps.weight', e, x)
+        want = quant.matvec_exact(raw[e * per:(e + 1) * per], 14, rows, cols, x)
+        assert normwise_rel(got, want) < 1e-5
