@@ -1,20 +1,25 @@
 #!/usr/bin/env python3
-"""Benchmark of the quantized decode path on one MI355X.
+"""Benchmark of the quantized-matmul / MoE path on one MI355X.
 
-Default workload (one "step"): the seven decode matvecs of one Llama-3-8B
-layer at batch 1 with the Q4_K_M mix -- q/k/o/gate/up in Q4_K, v/down in
-Q6_K -- on seeded synthetic weights (localai_amd/synth.py), weights already
-resident in HBM. Several weight copies (> 2 x 256 MB Infinity Cache) are
-rotated so every step streams from HBM. Each step is replayed from a HIP
-graph captured on the launch stream (launch overhead of 7 small kernels
-would otherwise dominate the ~20 us of GPU work).
+Workloads (one "step" = one pass of the path over one batch of synthetic
+input, weights already resident in HBM, seeded data from localai_amd/synth.py):
 
-Printed: one JSON line. `value` = algorithmic bytes of the layer (weights +
-fp32 in/out vectors, 139,231,232 B) / measured time per layer, in GB/s.
-`roofline` = the dominant kernel (Q4_K matvec, ffn_gate shape 14336x4096)
-timed alone with HIP events on its stream. `cpu_baseline` = the reference's
-own engine/native_quant.cpp kernels (built from source into oracle/_ref) on
-the host cores, with the reference's thread policy.
+  llama3_8b_decode_layer (default)  the seven decode matvecs of one
+      Llama-3-8B layer at batch 1, Q4_K_M mix (q/k/o/gate/up Q4_K, v/down
+      Q6_K). value = algorithmic bytes / time (GB/s).
+  q4k_matvec        one Q4_K matvec at the ffn_gate shape 14336x4096.
+  q8_0_prefill      Q8_0 GEMM 14336x4096 weights x 512 tokens (TFLOP/s).
+  zaya_moe_decode   ZAYA-shaped MoE FFN: hidden 2048, 16 experts, top-2,
+      intermediate 4096, Q6_K experts, T = 1 (T = 8 reported alongside).
+  qwen3_moe_prefill Qwen3-MoE-style prefill: hidden 2048, 128 experts, top-8,
+      intermediate 768, Q4_K experts, 512 tokens, Zipf(1.1) logit bias.
+
+Weight copies beyond 2 x the 256 MB Infinity Cache are rotated so every step
+streams its weights from HBM; steps are replayed from HIP graphs captured on
+the launch stream and timed with HIP events on that stream. `roofline` is the
+dominant kernel of the workload timed alone the same way; `cpu_baseline` is
+the reference's own engine/native_quant.cpp kernels (built from source into
+oracle/_ref) on a bounded sample, on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--cpu-baseline auto|off]
 """
@@ -23,7 +28,6 @@ from __future__ import annotations
 import argparse
 import json
 import os
-import subprocess
 import sys
 import time
 
@@ -33,7 +37,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFS = 2500.0      # dense f16/bf16 MFMA
 MALL_BYTES = 256 << 20
+METRIC = 'µs/layer + achieved HBM GB/s (% of peak) for Q4_K/Q6_K matvec & MoE layer'
+WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill']
 
 
 def log(msg):
@@ -45,35 +52,18 @@ def parse():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=200)
     ap.add_argument('--warmup', type=int, default=20)
-    ap.add_argument('--workload', default='llama3_8b_decode_layer',
-                    choices=['llama3_8b_decode_layer'])
+    ap.add_argument('--workload', default='llama3_8b_decode_layer', choices=WORKLOADS)
     ap.add_argument('--cpu-baseline', default='auto', choices=['auto', 'off'])
     ap.add_argument('--seed', type=int, default=0)
     return ap.parse_args()
 
 
-# ------------------------------------------------------------------ GPU side
-
-def build_layer(torch, device, synth, copies, seed):
-    """copies x 7 weight handles + the three input vectors + outputs."""
-    rng = np.random.default_rng(seed)
-    host = {name: synth.quant_tensor(rng, t, rows, cols) for name, t, rows, cols, _ in synth.LLAMA3_8B_LAYER}
-    vecs = {'h': synth.activations(rng, 4096), 'attn': synth.activations(rng, 4096),
-            'h2': synth.activations(rng, 4096), 'act': synth.activations(rng, 14336)}
-    xs = {k: device.to_device_f32(v) for k, v in vecs.items()}
-    mats = []
-    for _ in range(copies):
-        mats.append({name: device.QMat.from_ggml(host[name], t, rows, cols)
-                     for name, t, rows, cols, _ in synth.LLAMA3_8B_LAYER})
-    outs = {name: torch.empty(rows, dtype=torch.float32, device=device.device())
-            for name, _, rows, _, _ in synth.LLAMA3_8B_LAYER}
-    return host, vecs, xs, mats, outs
+def rotations(bytes_per_step):
+    """Copies needed so consecutive steps touch more than 2 x MALL."""
+    return max(2, -(-2 * MALL_BYTES // max(1, bytes_per_step)) + 1)
 
 
-def run_layer(mats, xs, outs, synth, stream):
-    for name, _, _, _, src in synth.LLAMA3_8B_LAYER:
-        mats[name].matvec(xs[src], out=outs[name], stream=stream)
-
+# ------------------------------------------------------------------ GPU timing
 
 def capture(torch, fn, stream):
     g = torch.cuda.CUDAGraph()
@@ -136,36 +126,303 @@ def reference_threads(rows, t):
     return min(req, os.cpu_count() or 1)
 
 
-def cpu_baseline(host, vecs, synth, layer_bytes):
-    """Time the reference's AVX2 kernels (oracle/_ref) on one layer."""
+def ref_ok():
     from oracle import ref
-    if not (ref.available() and cpu_has_avx2()):
-        return None
-    threads = []
-    calls = []
-    for name, t, rows, cols, src in synth.LLAMA3_8B_LAYER:
-        th = reference_threads(rows, t)
-        threads.append(th)
-        calls.append((host[name], vecs[src], rows, cols, t, th))
-    for _ in range(3):
-        for c in calls:
-            ref.matvec(*c[:5], threads=c[5])
+    return ref.available() and cpu_has_avx2()
+
+
+def time_cpu(fn, min_samples=5, budget_s=10.0, warm=2):
+    for _ in range(warm):
+        fn()
     samples = []
-    t_end = time.perf_counter() + 10.0
-    while len(samples) < 20 or (time.perf_counter() < t_end and len(samples) < 200):
+    t_end = time.perf_counter() + budget_s
+    while len(samples) < min_samples or (time.perf_counter() < t_end and len(samples) < 200):
         t0 = time.perf_counter_ns()
-        for c in calls:
-            ref.matvec(*c[:5], threads=c[5])
+        fn()
         samples.append((time.perf_counter_ns() - t0) / 1e3)
-        if len(samples) >= 20 and time.perf_counter() > t_end:
+        if len(samples) >= min_samples and time.perf_counter() > t_end:
             break
-    us = float(np.median(samples))
-    return {'value': round(layer_bytes / (us * 1e-6) / 1e9, 3), 'unit': 'GB/s',
-            'us_per_layer': round(us, 1), 'cores': max(threads), 'kind': 'reference',
-            'sample': f'{len(samples)} full layers (7 matvecs), median; engine/native_quant.cpp '
-                      f'built with g++ -O2 -mavx2 -mfma, reference thread policy '
-                      f'{dict(zip([n for n, *_ in synth.LLAMA3_8B_LAYER], threads))}; '
-                      f'host {cpu_model()}, {os.cpu_count()} logical CPUs visible'}
+    return float(np.median(samples)), len(samples)
+
+
+def host_note():
+    return f'host {cpu_model()}, {os.cpu_count()} logical CPUs visible'
+
+
+# ---------------------------------------------------------------- workloads
+
+def wl_layer(args, torch, device, synth):
+    layer = synth.LLAMA3_8B_LAYER
+    layer_bytes = synth.layer_algorithmic_bytes()
+    weight_bytes = synth.layer_weight_bytes()
+    copies = rotations(weight_bytes)
+    rng = np.random.default_rng(args.seed)
+    host = {name: synth.quant_tensor(rng, t, rows, cols) for name, t, rows, cols, _ in layer}
+    vecs = {'h': synth.activations(rng, 4096), 'attn': synth.activations(rng, 4096),
+            'h2': synth.activations(rng, 4096), 'act': synth.activations(rng, 14336)}
+    xs = {k: device.to_device_f32(v) for k, v in vecs.items()}
+    log(f'building {copies} weight copies ({copies * weight_bytes / 1e6:.0f} MB)')
+    mats = [{name: device.QMat.from_ggml(host[name], t, rows, cols) for name, t, rows, cols, _ in layer}
+            for _ in range(copies)]
+    outs = {name: torch.empty(rows, dtype=torch.float32, device=device.device()) for name, _, rows, _, _ in layer}
+    stream = torch.cuda.Stream()
+
+    def run(m):
+        for name, _, _, _, src in layer:
+            m[name].matvec(xs[src], out=outs[name], stream=stream)
+
+    graphs = [capture(torch, lambda m=m: run(m), stream) for m in mats]
+    log('timing layer')
+    ms = time_graphs(torch, graphs, stream, args.steps, args.warmup)
+    for name, o in outs.items():
+        if not torch.isfinite(o).all():
+            raise SystemExit(f'non-finite output in {name}')
+    roof = gate_roofline(args, torch, device, host['ffn_gate'], xs['h2'], stream)
+    cpu = None
+    if args.cpu_baseline != 'off' and ref_ok():
+        log('timing CPU baseline (reference AVX2 kernels)')
+        from oracle import ref
+        calls = [(host[name], vecs[src], rows, cols, t, reference_threads(rows, t))
+                 for name, t, rows, cols, src in layer]
+        us, n = time_cpu(lambda: [ref.matvec(*c[:5], threads=c[5]) for c in calls], min_samples=20)
+        cpu = {'value': round(layer_bytes / (us * 1e-6) / 1e9, 3), 'unit': 'GB/s', 'us_per_layer': round(us, 1),
+               'cores': max(c[5] for c in calls), 'kind': 'reference',
+               'sample': f'{n} full layers (7 matvecs), median; engine/native_quant.cpp built with g++ -O2 '
+                         f'-mavx2 -mfma, reference thread policy '
+                         f'{dict((nm, c[5]) for (nm, *_), c in zip(layer, calls))}; {host_note()}'}
+    gbs = layer_bytes / (ms * 1e-3) / 1e9
+    return {
+        'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+        'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
+        'data': 'synthetic (seeded GGML Q4_K/Q6_K bytes, fp32 N(0,1) activations)',
+        'config': {'workload': 'llama3_8b_decode_layer_q4_k_m', 'matvecs': 7, 'batch': 1,
+                   'shapes': [[n, {12: 'Q4_K', 14: 'Q6_K'}[t], r, c] for n, t, r, c, _ in layer],
+                   'algorithmic_bytes_per_layer': layer_bytes, 'weight_copies_rotated': copies,
+                   'launch': 'hip graph per layer'},
+        'roofline': roof, 'cpu_baseline': cpu}
+
+
+def gate_roofline(args, torch, device, gate_host, x, stream):
+    """Q4_K matvec at the ffn_gate shape, rotated over > 2x MALL, timed alone."""
+    gate_bytes = 14336 * 16 * 144 + 4 * 4096 + 4 * 14336
+    nrot = rotations(14336 * 16 * 144)
+    gmats = [device.QMat.from_ggml(gate_host, 12, 14336, 4096) for _ in range(nrot)]
+    gout = torch.empty(14336, dtype=torch.float32, device=device.device())
+    ggraph = capture(torch, lambda: [m.matvec(x, out=gout, stream=stream) for m in gmats], stream)
+    log('timing dominant kernel')
+    kms = time_graphs(torch, [ggraph], stream, max(20, args.steps // 4), 5) / nrot
+    achieved = gate_bytes / (kms * 1e-3) / 1e9
+    for m in gmats:
+        m.close()
+    return {'bound': 'hbm', 'kernel': 'gemv_kernel<Q4_K> 14336x4096', 'achieved': round(achieved, 1),
+            'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None,
+            'us_per_launch': round(kms * 1e3, 3), 'bytes_per_launch': gate_bytes}
+
+
+def wl_q4k(args, torch, device, synth):
+    rng = np.random.default_rng(args.seed)
+    raw = synth.quant_tensor(rng, 12, 14336, 4096)
+    xv = synth.activations(rng, 4096)
+    x = device.to_device_f32(xv)
+    stream = torch.cuda.Stream()
+    roof = gate_roofline(args, torch, device, raw, x, stream)
+    nbytes = roof['bytes_per_launch']
+    ms = roof['us_per_launch'] / 1e3
+    cpu = None
+    if args.cpu_baseline != 'off' and ref_ok():
+        from oracle import ref
+        th = reference_threads(14336, 12)
+        us, n = time_cpu(lambda: ref.matvec(raw, xv, 14336, 4096, 12, threads=th), min_samples=20)
+        cpu = {'value': round(nbytes / (us * 1e-6) / 1e9, 3), 'unit': 'GB/s', 'us_per_layer': round(us, 1),
+               'cores': th, 'kind': 'reference',
+               'sample': f'{n} calls of localai_q4k_matvec 14336x4096, median; {host_note()}'}
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+            'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
+            'data': 'synthetic (seeded GGML Q4_K bytes, fp32 N(0,1) x)',
+            'config': {'workload': 'q4k_matvec_14336x4096', 'batch': 1, 'algorithmic_bytes': nbytes},
+            'roofline': roof, 'cpu_baseline': cpu}
+
+
+def wl_q8_prefill(args, torch, device, synth):
+    rows, cols, tokens = 14336, 4096, 512
+    flops = 2 * rows * cols * tokens
+    rng = np.random.default_rng(args.seed)
+    raw = synth.quant_tensor(rng, 8, rows, cols)
+    xh = synth.activations(rng, tokens, cols)
+    x = device.to_device_f32(xh)
+    wbytes = rows * (cols // 32) * 34
+    copies = rotations(wbytes)
+    log(f'building {copies} Q8_0 weight copies')
+    mats = [device.QMat.from_ggml(raw, 8, rows, cols) for _ in range(copies)]
+    out = torch.empty((tokens, rows), dtype=torch.float32, device=device.device())
+    stream = torch.cuda.Stream()
+    graphs = [capture(torch, lambda m=m: m.matmul(x, out=out, stream=stream), stream) for m in mats]
+    log('timing prefill GEMM')
+    ms = time_graphs(torch, graphs, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
+    if not torch.isfinite(out).all():
+        raise SystemExit('non-finite GEMM output')
+    tfs = flops / (ms * 1e-3) / 1e12
+    cpu = None
+    if args.cpu_baseline != 'off' and ref_ok():
+        from oracle import ref
+        srows = 224                      # 1/64 of the rows, all 512 tokens
+        sub = raw[:srows * (cols // 32) * 34]
+        th = reference_threads(rows, 8)
+        us, n = time_cpu(lambda: ref.matmul(sub, xh, srows, cols, 8, threads=th), min_samples=3, budget_s=15)
+        sflops = 2 * srows * cols * tokens
+        cpu = {'value': round(sflops / (us * 1e-6) / 1e12, 5), 'unit': 'TFLOP/s', 'cores': th, 'kind': 'reference',
+               'us_per_layer': round(us * rows / srows, 1),
+               'sample': f'{n} calls of localai_q8_0_matmul on {srows} of {rows} rows x {tokens} tokens '
+                         f'(median; us_per_layer scaled to all rows); {host_note()}'}
+    return {'value': round(tfs, 2), 'unit': 'TFLOP/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+            'mfma_frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'dtype': 'f16 MFMA, fp32 accumulate',
+            'data': 'synthetic (seeded GGML Q8_0 bytes, fp32 N(0,1) activations)',
+            'config': {'workload': 'q8_0_prefill_gemm_14336x4096x512', 'tokens': tokens, 'flops': flops,
+                       'weight_copies_rotated': copies},
+            'roofline': {'bound': 'mfma', 'kernel': 'x_to_f16 + gemm_kernel<Q8_0> (whole call)',
+                         'achieved': round(tfs, 1), 'peak': MFMA_F16_PEAK_TFS, 'unit': 'TFLOP/s',
+                         'frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'traffic': None,
+                         'us_per_launch': round(ms * 1e3, 3), 'flops_per_launch': flops},
+            'cpu_baseline': cpu}
+
+
+def _moe_setup(args, synth, E, H, I, k, t, T, bias):
+    rng = np.random.default_rng(args.seed)
+    gu = synth.quant_tensor(rng, t, 2 * I, H, batch=E)
+    dn = synth.quant_tensor(rng, t, H, I, batch=E)
+    rw = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    h = synth.activations(rng, T, H)
+    return gu, dn, rw, h
+
+
+def _moe_gpu(args, torch, device, synth, E, H, I, k, t, T, bias, per_expert_bytes, label):
+    from localai_amd.moe import MoELayer
+    gu, dn, rw, h = _moe_setup(args, synth, E, H, I, k, t, T, bias)
+    hd = device.to_device_f32(h)
+    probe = MoELayer(rw, gu, dn, t, E, H, I, k, router_b=bias)
+    _, idx, _ = probe.forward_device(hd)
+    distinct = int(np.unique(idx.cpu().numpy()).size)
+    touched = distinct * per_expert_bytes
+    nbytes = touched + E * H * 4 + 2 * T * H * 4 + (E * 4 if bias is not None else 0)
+    copies = rotations(touched)
+    log(f'{label}: T={T}, {distinct} distinct experts, {copies} layer copies')
+    layers = [probe] + [MoELayer(rw, gu, dn, t, E, H, I, k, router_b=bias) for _ in range(copies - 1)]
+    stream = torch.cuda.Stream()
+    out = torch.empty((T, H), dtype=torch.float32, device=device.device())
+    oi = torch.empty((T, k), dtype=torch.int32, device=device.device())
+    og = torch.empty((T, k), dtype=torch.float32, device=device.device())
+    for L in layers:
+        L.workspace(T)
+    graphs = [capture(torch, lambda L=L: L.forward_device(hd, out=out, idx=oi, gates=og, stream=stream), stream)
+              for L in layers]
+    ms = time_graphs(torch, graphs, stream, args.steps, args.warmup)
+    if not torch.isfinite(out).all():
+        raise SystemExit('non-finite MoE output')
+    return ms, nbytes, distinct, copies, (gu, dn, rw, h, idx.cpu().numpy())
+
+
+def _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, T, bias, threads):
+    """numpy router + the reference kernels per selected expert (engine/zaya.py:303-306)."""
+    from oracle import ref
+    from oracle.quant import block_layout
+    block, bpb = block_layout(t)
+    gub = 2 * I * (H // block) * bpb
+    dnb = H * (I // block) * bpb
+    gbuf, dbuf = np.frombuffer(gu, np.uint8), np.frombuffer(dn, np.uint8)
+
+    def layer():
+        logits = h @ rw.T + (bias if bias is not None else 0.0)
+        sel = np.argsort(-logits, axis=1, kind='stable')[:, :k]
+        out = np.zeros((T, H), np.float32)
+        for e in np.unique(sel):
+            toks = np.nonzero((sel == e).any(axis=1))[0]
+            g_raw = gbuf[e * gub:(e + 1) * gub].tobytes()
+            d_raw = dbuf[e * dnb:(e + 1) * dnb].tobytes()
+            if len(toks) == 1:
+                gu_o = ref.matvec(g_raw, h[toks[0]], 2 * I, H, t, threads=threads)[None]
+            else:
+                gu_o = ref.matmul(g_raw, h[toks], 2 * I, H, t, threads=threads)
+            a = gu_o[:, :I] / (1.0 + np.exp(-np.clip(gu_o[:, :I], -80, 80))) * gu_o[:, I:]
+            if len(toks) == 1:
+                y = ref.matvec(d_raw, a[0].astype(np.float32), H, I, t, threads=threads)[None]
+            else:
+                y = ref.matmul(d_raw, a.astype(np.float32), H, I, t, threads=threads)
+            sl = logits[toks][:, :]
+            for j, tk in enumerate(toks):
+                s = sel[tk]
+                z = np.exp(logits[tk, s] - logits[tk, s].max())
+                out[tk] += (z / z.sum())[list(s).index(e)] * y[j]
+        return out
+    return layer
+
+
+def wl_zaya(args, torch, device, synth):
+    E, H, I, k, t = 16, 2048, 4096, 2, 14
+    per_expert = 2 * I * (H // 256) * 210 + H * (I // 256) * 210
+    res = {}
+    for T in (1, 8):
+        ms, nbytes, distinct, copies, data = _moe_gpu(args, torch, device, synth, E, H, I, k, t, T, None,
+                                                      per_expert, 'zaya')
+        res[T] = (ms, nbytes, distinct, copies, data)
+    ms, nbytes, distinct, copies, data = res[1]
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    ms8, nb8, d8, _, _ = res[8]
+    cpu = None
+    if args.cpu_baseline != 'off' and ref_ok():
+        gu, dn, rw, h, idx = data
+        fn = _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, 1, None, threads=min(4, os.cpu_count() or 1))
+        us, n = time_cpu(fn, min_samples=5, budget_s=10)
+        cpu = {'value': round(nbytes / (us * 1e-6) / 1e9, 3), 'unit': 'GB/s', 'us_per_layer': round(us, 1),
+               'cores': min(4, os.cpu_count() or 1), 'kind': 'reference',
+               'sample': f'{n} MoE layers at T=1 (numpy router + localai_q6k_matvec per selected expert, '
+                         f'threads=4 as engine/zaya.py), median; {host_note()}'}
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+            'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
+            'data': 'synthetic (seeded Q6_K experts, router N(0,0.02), h N(0,1))',
+            'config': {'workload': 'zaya_moe_decode_h2048_e16_top2_i4096_q6k', 'tokens': 1,
+                       'distinct_experts': distinct, 'algorithmic_bytes': nbytes, 'layer_copies_rotated': copies,
+                       'tokens_8': {'us_per_layer': round(ms8 * 1e3, 3), 'distinct_experts': d8,
+                                    'algorithmic_bytes': nb8,
+                                    'GB/s': round(nb8 / (ms8 * 1e-3) / 1e9, 2)}},
+            'roofline': {'bound': 'hbm', 'kernel': 'whole MoE layer (route, permute, grouped gate_up, '
+                                                    'grouped down, combine)',
+                         'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                         'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None,
+                         'us_per_launch': round(ms * 1e3, 3), 'bytes_per_launch': nbytes},
+            'cpu_baseline': cpu}
+
+
+def wl_qwen3(args, torch, device, synth):
+    E, H, I, k, t, T = 128, 2048, 768, 8, 12, 512
+    per_expert = 2 * I * (H // 256) * 144 + H * (I // 256) * 144
+    bias = synth.zipf_bias(E)
+    ms, nbytes, distinct, copies, data = _moe_gpu(args, torch, device, synth, E, H, I, k, t, T, bias,
+                                                  per_expert, 'qwen3')
+    flops = 2 * T * k * (H * 2 * I + I * H)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    tfs = flops / (ms * 1e-3) / 1e12
+    cpu = None
+    if args.cpu_baseline != 'off' and ref_ok():
+        gu, dn, rw, h, idx = data
+        th = min(6, os.cpu_count() or 1)
+        fn = _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, T, bias, threads=th)
+        us, n = time_cpu(fn, min_samples=2, budget_s=20, warm=1)
+        cpu = {'value': round(flops / (us * 1e-6) / 1e12, 5), 'unit': 'TFLOP/s', 'us_per_layer': round(us, 1),
+               'cores': th, 'kind': 'reference',
+               'sample': f'{n} MoE prefill layers (numpy router + localai_q4k_matmul per expert on its gathered '
+                         f'tokens), median; {host_note()}'}
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+            'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'tflops': round(tfs, 2),
+            'mfma_frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'dtype': 'fp32 / f16 MFMA',
+            'data': 'synthetic (seeded Q4_K experts, router N(0,0.02) + Zipf(1.1) logit bias, h N(0,1))',
+            'config': {'workload': 'qwen3_moe_prefill_h2048_e128_top8_i768_q4k_t512', 'tokens': T,
+                       'distinct_experts': distinct, 'algorithmic_bytes': nbytes, 'flops': flops,
+                       'layer_copies_rotated': copies},
+            'roofline': {'bound': 'hbm', 'kernel': 'whole MoE layer', 'achieved': round(gbs, 1),
+                         'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4),
+                         'traffic': None, 'us_per_launch': round(ms * 1e3, 3), 'bytes_per_launch': nbytes},
+            'cpu_baseline': cpu}
 
 
 def main():
@@ -179,57 +436,14 @@ def main():
 
     if native_quant.get_native() is None:
         raise SystemExit('no HIP device / library: the benchmark needs the GPU path')
-    layer_bytes = synth.layer_algorithmic_bytes()
-    weight_bytes = synth.layer_weight_bytes()
-    copies = max(2, -(-2 * MALL_BYTES // weight_bytes) + 1)
-    log(f'building {copies} weight copies ({copies * weight_bytes / 1e6:.0f} MB)')
-    host, vecs, xs, mats, outs = build_layer(torch, device, synth, copies, args.seed)
-    stream = torch.cuda.Stream()
-    graphs = [capture(torch, lambda m=m: run_layer(m, xs, outs, synth, stream), stream) for m in mats]
-    log('graphs captured; timing layer')
-    ms = time_graphs(torch, graphs, stream, args.steps, args.warmup)
-    gbs = layer_bytes / (ms * 1e-3) / 1e9
-
-    # dominant kernel: Q4_K matvec at the ffn_gate shape, rotated over > 2x MALL
-    gate_bytes = 14336 * 16 * 144 + 4 * 4096 + 4 * 14336
-    nrot = -(-2 * MALL_BYTES // (14336 * 16 * 144)) + 1
-    gate_host = host['ffn_gate']
-    gmats = [device.QMat.from_ggml(gate_host, 12, 14336, 4096) for _ in range(nrot)]
-    gout = torch.empty(14336, dtype=torch.float32, device=device.device())
-    # one graph launching the kernel once on each of the nrot copies (no copy twice in a row)
-    ggraph = capture(torch, lambda: [m.matvec(xs['h2'], out=gout, stream=stream) for m in gmats], stream)
-    log('timing dominant kernel')
-    kms = time_graphs(torch, [ggraph], stream, max(20, args.steps // 4), 5) / nrot
-    achieved = gate_bytes / (kms * 1e-3) / 1e9
-
-    # parity spot check of this run's outputs (GPU vs a fresh GPU run is not a check; the
-    # oracle comparison lives in tests/ -- here only sanity: finite outputs)
-    for name, o in outs.items():
-        if not torch.isfinite(o).all():
-            raise SystemExit(f'non-finite output in {name}')
-
-    cpu = None
-    if args.cpu_baseline != 'off':
-        log('timing CPU baseline (reference AVX2 kernels)')
-        cpu = cpu_baseline(host, vecs, synth, layer_bytes)
-
-    line = {
-        'metric': 'µs/layer + achieved HBM GB/s (% of peak) for Q4_K/Q6_K matvec & MoE layer',
-        'value': round(gbs, 2), 'unit': 'GB/s', 'n_gpus': 1, 'steps': args.steps,
-        'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'us_per_layer': round(ms * 1e3, 3),
-        'hbm_frac': round(gbs / HBM_PEAK_GBS, 4),
-        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'fp32',
-        'data': 'synthetic (seeded GGML Q4_K/Q6_K bytes, fp32 N(0,1) activations)',
-        'config': {'workload': 'llama3_8b_decode_layer_q4_k_m', 'matvecs': 7, 'batch': 1,
-                   'shapes': [[n, {12: 'Q4_K', 14: 'Q6_K'}[t], r, c] for n, t, r, c, _ in synth.LLAMA3_8B_LAYER],
-                   'algorithmic_bytes_per_layer': layer_bytes, 'weight_copies_rotated': copies,
-                   'launch': 'hip graph per layer'},
-        'roofline': {'bound': 'hbm', 'kernel': 'gemv_kernel<Q4_K,1> 14336x4096',
-                     'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None,
-                     'us_per_launch': round(kms * 1e3, 3), 'bytes_per_launch': gate_bytes},
-        'cpu_baseline': cpu,
-    }
+    fn = {'llama3_8b_decode_layer': wl_layer, 'q4k_matvec': wl_q4k, 'q8_0_prefill': wl_q8_prefill,
+          'zaya_moe_decode': wl_zaya, 'qwen3_moe_prefill': wl_qwen3}[args.workload]
+    r = fn(args, torch, device, synth)
+    ms = r.pop('ms_per_step')
+    line = {'metric': METRIC, 'value': r.pop('value'), 'unit': r.pop('unit'), 'n_gpus': 1, 'steps': args.steps,
+            'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True, 'scaling': 'weak',
+            'vs_baseline': None}
+    line.update(r)
     print(json.dumps(line), flush=True)
 
 

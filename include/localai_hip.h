@@ -91,6 +91,23 @@ int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out_d
 int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x_dev,
                        float *y_dev, int ntok, void *stream);
 
+/* ---- prefill matmul (MFMA) ---------------------------------------------- */
+
+/* Bytes of device workspace localai_hip_matmul needs for `tokens` rows of x. */
+int64_t localai_hip_matmul_workspace_size(const localai_qmat *m, int64_t tokens);
+
+/* Many-token product with matrix `expert` of the handle; counterpart of
+ * localai_*_matmul (engine/native_quant.cpp:744-768, decoded_matmul_row
+ * :444-531), whose output is [rows, tokens]:
+ *   x_dev  [tokens, cols] fp32 row-major
+ *   y_dev  y_layout 0: [tokens, rows] (x @ W^T);  1: [rows, tokens]
+ * Weights are decoded exactly in fp32 and rounded once to f16; each token row
+ * of x is scaled by a power of two into f16 range and rounded to f16; MFMA
+ * f16 products with fp32 accumulation (normwise error about 2^-12). */
+int localai_hip_matmul(const localai_qmat *m, int64_t expert, const float *x_dev, int64_t tokens,
+                       float *y_dev, int y_layout, void *workspace_dev, int64_t workspace_bytes,
+                       void *stream);
+
 /* ---- MoE expert layer ---------------------------------------------------- */
 
 /* Bytes of device workspace localai_hip_moe_forward needs for these sizes. */

@@ -205,6 +205,27 @@ int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x, fl
                          (hipStream_t)stream);
 }
 
+int64_t localai_hip_matmul_workspace_size(const localai_qmat *m, int64_t tokens) {
+    if (!m || tokens < 0) return -1;
+    return gemm_workspace_bytes(m->g, tokens);
+}
+
+int localai_hip_matmul(const localai_qmat *m, int64_t expert, const float *x, int64_t tokens, float *y,
+                       int y_layout, void *ws, int64_t ws_bytes, void *stream) {
+    clear_error();
+    if (!m || !x || !y) return fail(LOCALAI_EARG, "null pointer");
+    if (expert < 0 || expert >= m->g.batch) return fail(LOCALAI_EARG, "expert index out of range");
+    if (tokens < 1) return fail(LOCALAI_EARG, "tokens must be >= 1");
+    if (y_layout != 0 && y_layout != 1) return fail(LOCALAI_EARG, "y_layout must be 0 or 1");
+    if (!ws) return fail(LOCALAI_EARG, "null workspace");
+    if (int st = ensure_device()) return st;
+    lq_geom one = m->g;
+    one.batch = 1;
+    const int64_t ts = y_layout == 0 ? m->g.rows : 1, rs = y_layout == 0 ? 1 : tokens;
+    return launch_gemm(one, m->data + expert * m->g.matrix_bytes, x, tokens, y, ts, rs, ws, ws_bytes,
+                       (hipStream_t)stream);
+}
+
 int64_t localai_hip_moe_workspace_size(int64_t T, int64_t E, int k, int64_t H, int64_t I) {
     if (T < 1 || E < 1 || k < 1 || H < 1 || I < 1) return -1;
     return (int64_t)moe_workspace_bytes(T, E, k, H, I);

@@ -60,4 +60,10 @@ __device__ __forceinline__ int wave_id() {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
+// g / (1 + exp(-clip(g, -80, 80))), engine/zaya.py:305
+__device__ __forceinline__ float silu(float g) {
+    const float c = fminf(fmaxf(g, -80.0f), 80.0f);
+    return g / (1.0f + expf(-c));
+}
+
 }  // namespace lq

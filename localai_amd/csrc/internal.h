@@ -45,6 +45,18 @@ GemvPlan gemv_plan(const lq_geom &g, int nt);
 int launch_matvec(const lq_geom &g, const uint8_t *packed, const float *x, int64_t x_stride,
                   float *y, int64_t y_stride, int ntok, hipStream_t s);
 
+int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok);
+int launch_gemm(const lq_geom &g, const uint8_t *packed, const float *x, int64_t ntok, float *y, int64_t y_ts,
+                int64_t y_rs, void *ws, int64_t ws_bytes, hipStream_t s);
+
+int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *rows_map, int k, int64_t ntok,
+                    _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s);
+int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, bool gate_up, const _Float16 *Xh, int64_t ldh,
+                    const float *inv, float *Y, int64_t y_ts, int64_t inter, const int32_t *tile_e,
+                    const int32_t *tile_p0, const int32_t *tile_n, const int32_t *n_tiles, int max_tiles,
+                    hipStream_t s);
+int moe_gemm_tile();   // tokens per expert GEMM tile
+
 size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I);
 int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const float *rb, int64_t E, int k,
                const localai_qmat *gu, const localai_qmat *dn, float *out, int32_t *topk_idx, float *topk_w,

@@ -38,6 +38,17 @@ struct MoeTables {
     int32_t *pos;       // [N] position of assignment a in perm
     float *act;         // [N, I] silu(gate)*up per assignment, perm order
     float *ysl;         // [N, H] expert outputs per assignment, perm order
+    // prefill (expert GEMM) path
+    int32_t *tile_e;    // [max_tiles] expert of each token tile
+    int32_t *tile_p0;   // [max_tiles] first perm position of the tile
+    int32_t *tile_n;    // [max_tiles] tokens in the tile (<= tile width)
+    int32_t *n_tiles;   // [1]
+    _Float16 *xh_gu;    // [N, ldh(H)] f16 token rows of h in perm order
+    float *inv_gu;      // [N]
+    _Float16 *xh_dn;    // [N, ldh(I)] f16 act rows
+    float *inv_dn;      // [N]
+    int max_tiles;
+    int tile_w;         // tokens per tile (0: matvec path, no tile list)
 };
 
 // ------------------------------------------------------------------ route
@@ -46,7 +57,7 @@ __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
     return va > vb || (va == vb && ia < ib);
 }
 
-__global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ h, int H,
+__global__ __launch_bounds__(512) void moe_route_kernel(const float *__restrict__ h, int H,
                                                         const float *__restrict__ rw,
                                                         const float *__restrict__ rb, int E, int k,
                                                         float *__restrict__ logits,
@@ -56,10 +67,24 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
     const int t = blockIdx.x;
     const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
     const float *ht = h + (int64_t)t * H;
+    constexpr int CH = 16;                 // values per lane loaded ahead of the sums
     for (int e = w; e < E; e += nw) {
         const float *we = rw + (int64_t)e * H;
         double s = 0.0;
-        for (int i = lane; i < H; i += 64) s = __builtin_fma((double)ht[i], (double)we[i], s);
+        // lane l sums elements l, l + 64, l + 128, ... in that order (exact
+        // fp64 products); the loads of CH elements are issued before their sums
+        for (int i0 = 0; i0 < H; i0 += 64 * CH) {
+            float hv[CH], wv[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int i = i0 + 64 * j + lane;
+                hv[j] = i < H ? ht[i] : 0.0f;
+                wv[j] = i < H ? we[i] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < CH; ++j)
+                if (i0 + 64 * j + lane < H) s = __builtin_fma((double)hv[j], (double)wv[j], s);
+        }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
         if (lane == 0) {
@@ -130,17 +155,25 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__rest
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        int o = 0, na = 0;
+        int o = 0, na = 0, nt = 0;
         for (int e = 0; e < E; ++e) {
             off[e] = o;
             tb.offsets[e] = o;
             tb.counts[e] = total[e];
             if (total[e] > 0) tb.active[na++] = e;
+            if (tb.tile_w > 0)
+                for (int p = 0; p < total[e]; p += tb.tile_w) {
+                    tb.tile_e[nt] = e;
+                    tb.tile_p0[nt] = o + p;
+                    tb.tile_n[nt] = min(tb.tile_w, total[e] - p);
+                    ++nt;
+                }
             o += total[e];
         }
         off[E] = o;
         tb.offsets[E] = o;
         tb.n_active[0] = na;
+        if (tb.tile_w > 0) tb.n_tiles[0] = nt;
     }
     __syncthreads();
     for (int base = a0; base < a1; base += 64) {
@@ -168,78 +201,69 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__rest
 
 // --------------------------------------------------------- grouped matvec
 
-__device__ __forceinline__ float silu(float g) {
-    const float c = fminf(fmaxf(g, -80.0f), 80.0f);
-    return g / (1.0f + expf(-c));
+// register rows per lane: as the dense matvec (gemv.hip); split evenly
+// between the gate and up halves for gate_up
+template <int T, int NT>
+constexpr int moe_rows() {
+    return NT == 2 ? 4 : (T == LQ_Q6_K || T == LQ_Q5_K) ? 4 : 8;
 }
 
-constexpr int MOE_R = 4;   // rows per lane group per matrix half
-
-// One workgroup: a tile of MOE_R * G rows (G = 64 / LPR lane groups) of one
-// expert for NT of its tokens. gate_up: rows r of the gate half and
-// r + inter of the up half (one x staging, one reduction), written as
-// silu(g) * u; down: rows r of the down matrix. With LPR = 64 the waves
-// split the K units. Not inlined: the NT = 1 and NT = 2 bodies would
-// otherwise share one register budget.
-template <int T, int NT, bool GATE_UP, int LPR>
-__device__ __noinline__ void expert_chunk(const uint8_t *__restrict__ Wexp, const lq_geom &g, int64_t row0,
-                                          const float *const *xrow, float *red, float4 *xlds,
-                                          float *__restrict__ outp, int64_t out_stride) {
-    const int w = wave_id(), nw = blockDim.x >> 6;
-    const int64_t half = GATE_UP ? g.rows / 2 : g.rows;
-    constexpr int SETS = GATE_UP ? 2 : 1;
-    constexpr int RT = MOE_R * SETS;     // register rows per lane
-    constexpr int G = 64 / LPR;
-    int vi;
-    bool writer;
-    const float v = wave_rows<T, NT, 1, RT, LPR, SETS>(Wexp, g, row0, half + row0, GATE_UP ? g.rows : half, w,
-                                                       xrow, xlds + w * NT * 16 * LPR, vi, writer);
-    // red[(w * G + group) * RT * NT + value]; value r * NT + t, set-1 rows
-    // (up half) after the MOE_R * NT set-0 values
-    if (writer) red[(w * G + lane_id() / LPR) * RT * NT + vi] = v;
-    __syncthreads();
-    const int i = threadIdx.x;
-    if (i < G * MOE_R * NT) {
-        const int gi = i / (MOE_R * NT), j = i % (MOE_R * NT);
-        float sa = 0.0f, sb = 0.0f;
-        for (int k = 0; k < nw; ++k) {
-            sa += red[(k * G + gi) * RT * NT + j];
-            if (GATE_UP) sb += red[(k * G + gi) * RT * NT + MOE_R * NT + j];
-        }
-        const int r = j / NT, t = j % NT;
-        const int64_t row = row0 + gi * MOE_R + r;
-        if (row < half) outp[t * out_stride + row] = GATE_UP ? silu(sa) * sb : sa;
-    }
-    __syncthreads();
-}
-
-template <int T, bool GATE_UP, int LPR>
+// One workgroup: a tile of RS * G rows (RS register rows per row set, G =
+// 64 / LPR lane groups) of one active expert, for NT of its tokens
+// (blockIdx.z picks which). gate_up: rows r of the gate half and r + inter
+// of the up half share the x staging and the reduction, and the output is
+// silu(g) * u; down: rows r of the down matrix. With LPR = 64 the waves split
+// the K units. A token pair whose second token does not exist repeats the
+// first and skips its writes.
+template <int T, bool GATE_UP, int LPR, int NT>
 __global__ __launch_bounds__(256) void moe_grouped_kernel(const uint8_t *__restrict__ Wall, lq_geom g,
                                                           MoeTables tb, const float *__restrict__ xsrc,
                                                           int64_t x_stride, int k) {
-    extern __shared__ float4 xlds[];            // 2 * 16 * LPR float4 per wave (NT <= 2)
-    __shared__ float red[4 * 2 * MOE_R * 2];    // [waves x groups][rows of both sets][NT <= 2]
+    constexpr int R = moe_rows<T, NT>();
+    constexpr int SETS = GATE_UP ? 2 : 1;
+    constexpr int RS = R / SETS;
+    constexpr int G = 64 / LPR;
+    extern __shared__ float4 xlds[];             // NT * 16 * LPR float4 per wave
+    __shared__ float red[4 * G * R * NT];        // [waves x groups][register rows][NT]
     const int slot = blockIdx.y;
     if (slot >= tb.n_active[0]) return;
     const int e = tb.active[slot];
     const int n = tb.counts[e], base = tb.offsets[e];
+    const int t0 = blockIdx.z * NT;
+    if (t0 >= n) return;
+    const int nv = n - t0 < NT ? n - t0 : NT;
     const uint8_t *Wexp = Wall + (int64_t)e * g.matrix_bytes;
-    const int64_t row0 = (int64_t)blockIdx.x * MOE_R * (64 / LPR);
+    const int64_t half = GATE_UP ? g.rows / 2 : g.rows;
+    const int64_t row0 = (int64_t)blockIdx.x * RS * G;
     // gate_up: x = token rows of h, out = act rows [p, inter]; down: x = act rows, out = ysl rows [p, H]
+    const float *xrow[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int p = base + t0 + (t < nv ? t : 0);
+        const int64_t src = GATE_UP ? (int64_t)(tb.perm[p] / k) : (int64_t)p;
+        xrow[t] = xsrc + src * x_stride;
+    }
     const int64_t out_stride = GATE_UP ? g.rows / 2 : g.rows;
-    float *outbase = GATE_UP ? tb.act : tb.ysl;
-    for (int t0 = 0; t0 < n;) {
-        const int nt = n - t0 >= 2 ? 2 : 1;
-        const float *xrow[2];
-        for (int t = 0; t < 2; ++t) {
-            const int p = base + t0 + (t < nt ? t : 0);
-            const int64_t src = GATE_UP ? (int64_t)(tb.perm[p] / k) : (int64_t)p;
-            xrow[t] = xsrc + src * x_stride;
+    float *outp = (GATE_UP ? tb.act : tb.ysl) + (int64_t)(base + t0) * out_stride;
+    const int w = wave_id(), nw = blockDim.x >> 6;
+    int vi;
+    bool writer;
+    const float v = wave_rows<T, NT, 1, R, LPR, SETS>(Wexp, g, row0, half + row0, GATE_UP ? g.rows : half, w,
+                                                      xrow, xlds + w * NT * 16 * LPR, vi, writer);
+    // value r * NT + t; the up-half rows (set 1) follow the RS * NT set-0 values
+    if (writer) red[(w * G + lane_id() / LPR) * R * NT + vi] = v;
+    __syncthreads();
+    const int i = threadIdx.x;
+    if (i < G * RS * NT) {
+        const int gi = i / (RS * NT), j = i % (RS * NT);
+        float sa = 0.0f, sb = 0.0f;
+        for (int kk = 0; kk < nw; ++kk) {
+            sa += red[(kk * G + gi) * R * NT + j];
+            if (GATE_UP) sb += red[(kk * G + gi) * R * NT + RS * NT + j];
         }
-        float *outp = outbase + (int64_t)(base + t0) * out_stride;
-        if (nt == 2) expert_chunk<T, 2, GATE_UP, LPR>(Wexp, g, row0, xrow, red, xlds, outp, out_stride);
-        else expert_chunk<T, 1, GATE_UP, LPR>(Wexp, g, row0, xrow, red, xlds, outp, out_stride);
-        t0 += nt;
+        const int r = j / NT, t = j % NT;
+        const int64_t row = row0 + gi * RS + r;
+        if (t < nv && row < half) outp[t * out_stride + row] = GATE_UP ? silu(sa) * sb : sa;
     }
 }
 
@@ -263,6 +287,15 @@ __global__ void moe_combine_kernel(const float *__restrict__ ysl, const int32_t 
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Tokens at or above which the layer runs the expert GEMM path (prefill).
+constexpr int64_t MOE_GEMM_TOKENS = 32;
+
+static int64_t moe_max_tiles(int64_t N, int64_t E, int tile_w) {
+    return N / tile_w + (E < N ? E : N);
+}
+
+static int64_t f16_stride(int64_t cols) { return 128 * (((cols + 63) / 64 + 1) / 2); }
+
 size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
     const int64_t N = T * k;
     size_t s = 0;
@@ -271,13 +304,19 @@ size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I
     s += align256(N * 4) * 2;                                        // perm, pos
     s += align256(N * I * 4);                                        // act
     s += align256(N * H * 4);                                        // ysl
+    if (T >= MOE_GEMM_TOKENS) {
+        const int64_t mt = moe_max_tiles(N, E, moe_gemm_tile());
+        s += align256(mt * 4) * 3 + align256(4);
+        s += align256(N * f16_stride(H) * 2) + align256(N * 4);
+        s += align256(N * f16_stride(I) * 2) + align256(N * 4);
+    }
     return s;
 }
 
 static MoeTables carve(void *ws, int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
     const int64_t N = T * k;
     uint8_t *p = (uint8_t *)ws;
-    MoeTables tb;
+    MoeTables tb{};
     auto take = [&](size_t n) { uint8_t *q = p; p += align256(n); return q; };
     tb.logits = (float *)take(T * E * 4);
     tb.counts = (int32_t *)take(E * 4);
@@ -288,36 +327,61 @@ static MoeTables carve(void *ws, int64_t T, int64_t E, int64_t k, int64_t H, int
     tb.pos = (int32_t *)take(N * 4);
     tb.act = (float *)take(N * I * 4);
     tb.ysl = (float *)take(N * H * 4);
+    tb.tile_w = 0;
+    if (T >= MOE_GEMM_TOKENS) {
+        tb.tile_w = moe_gemm_tile();
+        tb.max_tiles = (int)moe_max_tiles(N, E, tb.tile_w);
+        tb.tile_e = (int32_t *)take(tb.max_tiles * 4);
+        tb.tile_p0 = (int32_t *)take(tb.max_tiles * 4);
+        tb.tile_n = (int32_t *)take(tb.max_tiles * 4);
+        tb.n_tiles = (int32_t *)take(4);
+        tb.xh_gu = (_Float16 *)take(N * f16_stride(H) * 2);
+        tb.inv_gu = (float *)take(N * 4);
+        tb.xh_dn = (_Float16 *)take(N * f16_stride(I) * 2);
+        tb.inv_dn = (float *)take(N * 4);
+    }
     return tb;
 }
 
-template <int T, bool GATE_UP>
+template <int T, bool GATE_UP, int NT>
 static void launch_grouped_t(const localai_qmat *m, int lpr, int waves, const MoeTables &tb, const float *xsrc,
-                             int64_t x_stride, int k, int slots, hipStream_t s) {
+                             int64_t x_stride, int k, int slots, int64_t max_tokens, hipStream_t s) {
     const lq_geom &g = m->g;
     const int64_t half = GATE_UP ? g.rows / 2 : g.rows;
-    const int64_t tile = MOE_R * (64 / lpr);
-    dim3 grid((unsigned)((half + tile - 1) / tile), slots), block(64 * waves);
-    const size_t lds = (size_t)waves * 2 * 16 * lpr * 16;
+    const int64_t tile = (int64_t)(moe_rows<T, NT>() / (GATE_UP ? 2 : 1)) * (64 / lpr);
+    dim3 grid((unsigned)((half + tile - 1) / tile), slots, (unsigned)((max_tokens + NT - 1) / NT)),
+        block(64 * waves);
+    const size_t lds = (size_t)waves * NT * 16 * lpr * 16;
     if (lpr == 16)
-        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 16>), grid, block, lds, s, m->data, g, tb, xsrc, x_stride, k);
+        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 16, NT>), grid, block, lds, s, m->data, g, tb, xsrc,
+                           x_stride, k);
     else if (lpr == 32)
-        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 32>), grid, block, lds, s, m->data, g, tb, xsrc, x_stride, k);
+        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 32, NT>), grid, block, lds, s, m->data, g, tb, xsrc,
+                           x_stride, k);
     else
-        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 64>), grid, block, lds, s, m->data, g, tb, xsrc, x_stride, k);
+        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 64, NT>), grid, block, lds, s, m->data, g, tb, xsrc,
+                           x_stride, k);
 }
 
+// max_tokens: an upper bound on the tokens routed to one expert (the token
+// count); workgroups past an expert's count exit at once.
 template <bool GATE_UP>
 static int launch_grouped(const localai_qmat *m, const MoeTables &tb, const float *xsrc, int64_t x_stride,
-                          int k, int slots, hipStream_t s) {
+                          int k, int slots, int64_t max_tokens, hipStream_t s) {
     const lq_geom &g = m->g;
     const int lpr = lanes_per_row(g.nu);
     const int waves = lpr < 64 ? 1 : (int)((g.nu + 63) / 64);
+    const int nt = max_tokens >= 2 ? 2 : 1;
     if (waves > 4) return fail(LOCALAI_EARG, "moe: expert K too large (more than 16384 values per row)");
-    if ((size_t)waves * 2 * 16 * lpr * 16 > max_lds_per_block())
+    if ((size_t)waves * nt * 16 * lpr * 16 > max_lds_per_block())
         return fail(LOCALAI_EARG, "moe: x windows exceed the LDS per workgroup");
+    if ((max_tokens + nt - 1) / nt > 65535) return fail(LOCALAI_EARG, "moe: too many tokens for the matvec path");
     switch (g.type) {
-#define LQ_G(TT) case TT: launch_grouped_t<TT, GATE_UP>(m, lpr, waves, tb, xsrc, x_stride, k, slots, s); break;
+#define LQ_G(TT)                                                                                      \
+    case TT:                                                                                          \
+        if (nt == 2) launch_grouped_t<TT, GATE_UP, 2>(m, lpr, waves, tb, xsrc, x_stride, k, slots, max_tokens, s); \
+        else launch_grouped_t<TT, GATE_UP, 1>(m, lpr, waves, tb, xsrc, x_stride, k, slots, max_tokens, s);        \
+        break;
         LQ_G(LQ_Q4_K) LQ_G(LQ_Q5_K) LQ_G(LQ_Q6_K) LQ_G(LQ_Q8_0) LQ_G(LQ_Q4_0)
 #undef LQ_G
         default: return fail(LOCALAI_ETYPE, "moe: unsupported expert type");
@@ -332,15 +396,29 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
     const int64_t I = gu->g.rows / 2;
     MoeTables tb = carve(ws, T, E, k, H, I);
     size_t sh = (size_t)E * 4;
-    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)T), dim3(256), sh, s, h, (int)H, rw, rb, (int)E, k,
+    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)T), dim3(512), sh, s, h, (int)H, rw, rb, (int)E, k,
                        tb.logits, topk_idx, topk_w);
     LQ_HIP(hipGetLastError());
     size_t sh2 = (size_t)(34 * E + 1) * 4;
     hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), sh2, s, topk_idx, (int)(T * k), (int)E, tb);
     LQ_HIP(hipGetLastError());
     const int slots = (int)(E < T * k ? E : T * k);
-    if (int st = launch_grouped<true>(gu, tb, h, H, k, slots, s)) return st;
-    if (int st = launch_grouped<false>(dn, tb, tb.act, I, k, slots, s)) return st;
+    if (tb.tile_w > 0) {
+        // prefill: gathered f16 token rows -> expert GEMMs on MFMA
+        const int64_t N = T * k;
+        if (gu->g.cols != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe: expert shapes");
+        if (int st = launch_x_to_f16(h, H, H, tb.perm, k, N, tb.xh_gu, f16_stride(H), tb.inv_gu, s)) return st;
+        if (int st = launch_moe_gemm(gu->g, gu->data, true, tb.xh_gu, f16_stride(H), tb.inv_gu, tb.act, I, I,
+                                     tb.tile_e, tb.tile_p0, tb.tile_n, tb.n_tiles, tb.max_tiles, s))
+            return st;
+        if (int st = launch_x_to_f16(tb.act, I, I, nullptr, 1, N, tb.xh_dn, f16_stride(I), tb.inv_dn, s)) return st;
+        if (int st = launch_moe_gemm(dn->g, dn->data, false, tb.xh_dn, f16_stride(I), tb.inv_dn, tb.ysl, H, I,
+                                     tb.tile_e, tb.tile_p0, tb.tile_n, tb.n_tiles, tb.max_tiles, s))
+            return st;
+    } else {
+        if (int st = launch_grouped<true>(gu, tb, h, H, k, slots, T, s)) return st;
+        if (int st = launch_grouped<false>(dn, tb, tb.act, I, k, slots, T, s)) return st;
+    }
     dim3 grid((unsigned)((H + 255) / 256), (unsigned)T);
     hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, s, tb.ysl, tb.pos, topk_w, k, (int)H, out);
     LQ_HIP(hipGetLastError());

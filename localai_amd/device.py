@@ -126,6 +126,30 @@ class QMat:
                                                   ctypes.c_void_p(stream_ptr(stream))))
         return out.reshape(-1) if squeeze else out
 
+    def matmul(self, x, expert=0, out=None, rows_major=False, stream=None):
+        """Prefill product on MFMA: x [tokens, cols] fp32 device tensor ->
+        [tokens, rows] (or [rows, tokens] with rows_major=True, the layout of
+        the reference's localai_*_matmul)."""
+        t = torch()
+        x2 = x
+        if x2.dtype != t.float32 or not x2.is_contiguous():
+            x2 = x2.to(t.float32).contiguous()
+        if x2.dim() != 2 or x2.shape[1] != self.cols:
+            raise ValueError(f'x must be [tokens, {self.cols}]')
+        ntok = x2.shape[0]
+        lib = _lib.load()
+        ws_bytes = int(lib.localai_hip_matmul_workspace_size(self.handle, int(ntok)))
+        ws = t.empty(max(ws_bytes, 1), dtype=t.uint8, device=x2.device)
+        shape = (self.rows, ntok) if rows_major else (ntok, self.rows)
+        if out is None:
+            out = t.empty(shape, dtype=t.float32, device=x2.device)
+        elif tuple(out.shape) != shape or not out.is_contiguous():
+            raise ValueError(f'out must be a contiguous {shape} tensor')
+        _lib.check(lib.localai_hip_matmul(self.handle, int(expert), ptr(x2), int(ntok), ptr(out),
+                                          1 if rows_major else 0, ptr(ws), ws_bytes,
+                                          ctypes.c_void_p(stream_ptr(stream))))
+        return out
+
     def dequant(self, expert=0, stream=None):
         t = torch()
         out = t.empty((self.rows, self.cols), dtype=t.float32, device=device())
