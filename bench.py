@@ -13,6 +13,8 @@ input, weights already resident in HBM, seeded data from localai_amd/synth.py):
       intermediate 4096, Q6_K experts, T = 1 (T = 8 reported alongside).
   qwen3_moe_prefill Qwen3-MoE-style prefill: hidden 2048, 128 experts, top-8,
       intermediate 768, Q4_K experts, 512 tokens, Zipf(1.1) logit bias.
+  hbm_copy          a plain 256 MiB device-to-device copy: the calibration
+      kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE (known bytes per launch).
 
 Weight copies beyond 2 x the 256 MB Infinity Cache are rotated so every step
 streams its weights from HBM; steps are replayed from HIP graphs captured on
@@ -40,7 +42,8 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFS = 2500.0      # dense f16/bf16 MFMA
 MALL_BYTES = 256 << 20
 METRIC = 'µs/layer + achieved HBM GB/s (% of peak) for Q4_K/Q6_K matvec & MoE layer'
-WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill']
+WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill',
+             'hbm_copy']
 
 
 def log(msg):
@@ -215,8 +218,19 @@ def gate_roofline(args, torch, device, gate_host, x, stream):
     for m in gmats:
         m.close()
     return {'bound': 'hbm', 'kernel': 'gemv_kernel<Q4_K> 14336x4096', 'achieved': round(achieved, 1),
-            'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': None,
+            'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4),
+            'traffic': measured_traffic('gemv_q4k_14336x4096_traffic.json'),
             'us_per_launch': round(kms * 1e3, 3), 'bytes_per_launch': gate_bytes}
+
+
+def measured_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes (profiles/), calibrated on a copy of known size; None if absent."""
+    try:
+        with open(os.path.join(ROOT, 'profiles', name)) as f:
+            return int(json.load(f)['traffic_bytes'])
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def wl_q4k(args, torch, device, synth):
@@ -425,6 +439,22 @@ def wl_qwen3(args, torch, device, synth):
             'cpu_baseline': cpu}
 
 
+def wl_copy(args, torch, device, synth):
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device=device.device()).fill_(1)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.Stream()
+    g = capture(torch, lambda: dst.copy_(src), stream)
+    ms = time_graphs(torch, [g], stream, args.steps, args.warmup)
+    gbs = 2 * n / (ms * 1e-3) / 1e9
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'hbm_frac': round(gbs / HBM_PEAK_GBS, 4),
+            'dtype': 'u8', 'data': 'constant bytes',
+            'config': {'workload': 'hbm_copy_256MiB', 'read_bytes': n, 'write_bytes': n},
+            'roofline': {'bound': 'hbm', 'kernel': 'torch copy', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS,
+                         'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
+            'cpu_baseline': None}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -437,7 +467,7 @@ def main():
     if native_quant.get_native() is None:
         raise SystemExit('no HIP device / library: the benchmark needs the GPU path')
     fn = {'llama3_8b_decode_layer': wl_layer, 'q4k_matvec': wl_q4k, 'q8_0_prefill': wl_q8_prefill,
-          'zaya_moe_decode': wl_zaya, 'qwen3_moe_prefill': wl_qwen3}[args.workload]
+          'zaya_moe_decode': wl_zaya, 'qwen3_moe_prefill': wl_qwen3, 'hbm_copy': wl_copy}[args.workload]
     r = fn(args, torch, device, synth)
     ms = r.pop('ms_per_step')
     line = {'metric': METRIC, 'value': r.pop('value'), 'unit': r.pop('unit'), 'n_gpus': 1, 'steps': args.steps,

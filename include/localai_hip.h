@@ -85,7 +85,7 @@ int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out_d
                              void *stream);
 
 /* y[t, r] = sum_c W_e[r, c] * x[t, c] for t < ntok (small-batch decode matvec;
- * ntok in 1..8 per launch, larger counts are processed in passes).
+ * vectors are processed two per launch while cols <= 8192, one otherwise).
  * x_dev is [ntok, cols] fp32 row-major, y_dev is [ntok, rows] fp32.
  * fp32 products of exactly decoded weights, fp32 accumulation. */
 int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x_dev,
@@ -151,7 +151,9 @@ void localai_q4_0_matvec(const uint8_t *raw, const float *x, float *out, int row
 void localai_q4k_matvec(const uint8_t *raw, const float *x, float *out, int rows, int cols, int threads);
 void localai_q5k_matvec(const uint8_t *raw, const float *x, float *out, int rows, int cols, int threads);
 void localai_q6k_matvec(const uint8_t *raw, const float *x, float *out, int rows, int cols, int threads);
-/* out[rows, tokens] = W @ vectors^T (vectors [tokens, cols]).  engine/native_quant.cpp:744-768 */
+/* out[rows, tokens] = W @ vectors^T (vectors [tokens, cols]).  engine/native_quant.cpp:744-768
+ * Fewer than 32 tokens: the fp32 matvec; 32 tokens or more: the MFMA GEMM
+ * (localai_hip_matmul: f16 operands, fp32 accumulation). */
 void localai_q8_0_matmul(const uint8_t *raw, const float *vectors, float *out, int rows, int cols, int tokens, int threads);
 void localai_q4_0_matmul(const uint8_t *raw, const float *vectors, float *out, int rows, int cols, int tokens, int threads);
 void localai_q4k_matmul(const uint8_t *raw, const float *vectors, float *out, int rows, int cols, int tokens, int threads);

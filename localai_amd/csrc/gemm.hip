@@ -126,6 +126,21 @@ __device__ __forceinline__ int window_pos(int u, int j) {
     else return 64 * (u & 1) + j;
 }
 
+typedef _Float16 lq_h2 __attribute__((ext_vector_type(2)));
+
+// Q8_0 weights straight to f16 pairs: byte q + 128 under the f16 exponent of
+// 1024 reads as 1152 + q (exact), minus 1152 gives q exactly, and one f16
+// multiply by d rounds d * q once (the same value as rounding the exact fp32
+// product). Four int8 quants in `w` -> two f16 pairs.
+__device__ __forceinline__ void q8_pairs(uint32_t w, lq_h2 d2, uint32_t &lo, uint32_t &hi) {
+    const uint32_t b = w ^ 0x80808080u;
+    const uint32_t l = (b & 0xFFu) | ((b & 0xFF00u) << 8) | 0x64006400u;
+    const uint32_t h = ((b >> 16) & 0xFFu) | ((b >> 8) & 0xFF0000u) | 0x64006400u;
+    const lq_h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(lq_h2, l) - off) * d2);
+    hi = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(lq_h2, h) - off) * d2);
+}
+
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     const _Float16 ha = (_Float16)a, hb = (_Float16)b;
     return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
@@ -163,10 +178,22 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     const uint8_t *W = a.W;
     int64_t p0;
     int tn;
+    int64_t rtile;
     if constexpr (MODE == GM_DENSE) {
-        p0 = (int64_t)blockIdx.y * BN;
+        // 1-D grid, padded to a multiple of 8. Workgroups are dispatched to the
+        // 8 XCDs round-robin (id % 8); workgroup id -> logical index
+        // xcd * per + id / 8 walks the row tiles of one token tile per XCD, so
+        // each XCD's L2 holds one activation tile while the weights stream.
+        const int id = blockIdx.x, per = gridDim.x / 8;
+        const int L = (id % 8) * per + id / 8;
+        const int nrt = (int)((g.rows + GM_BM - 1) / GM_BM);
+        const int64_t ntt = (a.ntok + BN - 1) / BN;
+        if (L >= nrt * ntt) return;
+        rtile = L % nrt;
+        p0 = (int64_t)(L / nrt) * BN;
         tn = (int)(a.ntok - p0 < BN ? a.ntok - p0 : BN);
     } else {
+        rtile = blockIdx.x;
         const int tile = blockIdx.y;
         if (tile >= a.n_tiles[0]) return;
         W += (int64_t)a.tile_e[tile] * g.matrix_bytes;
@@ -174,7 +201,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         tn = a.tile_n[tile];
     }
     // weight rows of this tile: q -> matrix row (or -1 when past the end)
-    const int64_t r0 = (int64_t)blockIdx.x * (MODE == GM_MOE_GATE_UP ? GM_BM / 2 : GM_BM);
+    const int64_t r0 = rtile * (MODE == GM_MOE_GATE_UP ? GM_BM / 2 : GM_BM);
     auto row_of = [&](int q) -> int64_t {
         if constexpr (MODE == GM_MOE_GATE_UP) {
             // wave row block rb = q / 64, MFMA tile j = (q % 64) / 16: j < 2 gate, j >= 2 up,
@@ -211,18 +238,34 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     };
     auto store = [&](int step) {
         const int u = 2 * step + lh;
-        float v[64];
-        dequant_unit<T>(wreg, u < U ? u : U - 1, v);
         const bool valid = u < U;
         _Float16 *wd = Ws + lr * GM_LD;
+        if constexpr (T == LQ_Q8_0) {
+            const uint32_t dm = valid ? 0xFFFFFFFFu : 0u;
+            const lq_h2 d0 = __builtin_bit_cast(lq_h2, ((wreg.sc & 0xFFFFu) * 0x10001u) & dm);
+            const lq_h2 d1 = __builtin_bit_cast(lq_h2, ((wreg.sc >> 16) * 0x10001u) & dm);
+            const uint4 qs[4] = {wreg.q0, wreg.q1, wreg.q2, wreg.q3};
 #pragma unroll
-        for (int j = 0; j < 64; j += 8) {
-            uint4 p;
-            p.x = valid ? pack_h2(v[j + 0], v[j + 1]) : 0u;
-            p.y = valid ? pack_h2(v[j + 2], v[j + 3]) : 0u;
-            p.z = valid ? pack_h2(v[j + 4], v[j + 5]) : 0u;
-            p.w = valid ? pack_h2(v[j + 6], v[j + 7]) : 0u;
-            *reinterpret_cast<uint4 *>(wd + window_pos<T>(u, j)) = p;
+            for (int c = 0; c < 8; ++c) {      // 8 values per 16-byte LDS write
+                const uint4 q = qs[c >> 1];
+                const lq_h2 d2 = c < 4 ? d0 : d1;
+                uint4 p;
+                q8_pairs(u4_get(q, 2 * (c & 1)), d2, p.x, p.y);
+                q8_pairs(u4_get(q, 2 * (c & 1) + 1), d2, p.z, p.w);
+                *reinterpret_cast<uint4 *>(wd + 64 * (u & 1) + 8 * c) = p;
+            }
+        } else {
+            float v[64];
+            dequant_unit<T>(wreg, u < U ? u : U - 1, v);
+#pragma unroll
+            for (int j = 0; j < 64; j += 8) {
+                uint4 p;
+                p.x = valid ? pack_h2(v[j + 0], v[j + 1]) : 0u;
+                p.y = valid ? pack_h2(v[j + 2], v[j + 3]) : 0u;
+                p.z = valid ? pack_h2(v[j + 4], v[j + 5]) : 0u;
+                p.w = valid ? pack_h2(v[j + 6], v[j + 7]) : 0u;
+                *reinterpret_cast<uint4 *>(wd + window_pos<T>(u, j)) = p;
+            }
         }
         uint4 *xd = reinterpret_cast<uint4 *>(Xs + xr * GM_LD + XV * xp);
 #pragma unroll
@@ -322,14 +365,15 @@ int launch_gemm(const lq_geom &g, const uint8_t *W, const float *X, int64_t ntok
                 int64_t y_rs, void *ws, int64_t ws_bytes, hipStream_t s) {
     if (ntok <= 0) return LOCALAI_OK;
     if (ws_bytes < gemm_workspace_bytes(g, ntok)) return fail(LOCALAI_EARG, "matmul: workspace too small");
-    if (ntok > 65535 * (int64_t)GM_BN) return fail(LOCALAI_EARG, "matmul: too many tokens");
     const int64_t ldh = gemm_ldh(g);
     _Float16 *Xh = (_Float16 *)ws;
     float *inv = (float *)((uint8_t *)ws + ((ntok * ldh * 2 + 255) & ~(int64_t)255));
     if (int st = launch_x_to_f16(X, g.cols, g.cols, nullptr, 1, ntok, Xh, ldh, inv, s)) return st;
     GemmArgs a{};
     a.g = g; a.W = W; a.Xh = Xh; a.ldh = (int)ldh; a.inv = inv; a.ntok = ntok; a.Y = Y; a.y_ts = y_ts; a.y_rs = y_rs;
-    dim3 grid((unsigned)((g.rows + GM_BM - 1) / GM_BM), (unsigned)((ntok + GM_BN - 1) / GM_BN));
+    const int64_t nwg = ((g.rows + GM_BM - 1) / GM_BM) * ((ntok + GM_BN - 1) / GM_BN);
+    if (nwg > ((int64_t)1 << 30)) return fail(LOCALAI_EARG, "matmul: problem too large");
+    dim3 grid((unsigned)((nwg + 7) / 8 * 8));
     return launch_gemm_t<GM_DENSE, GM_BN>(a, grid, s);
 }
 

@@ -15,11 +15,15 @@
 
 namespace lq {
 
-// register rows per lane: 8 for one vector of 4-bit / 8-bit types, 4 for the
-// wider Q5_K/Q6_K units or two vectors, 2 with two unit slots
+// rows per lane group: 8 for one vector (processed 2 per pipeline step), 4
+// for two vectors, 2 with two unit slots
 template <int T, int NT, int S>
 constexpr int rows_per_lane() {
-    return S == 2 ? 2 : NT == 2 ? 4 : (T == LQ_Q6_K || T == LQ_Q5_K) ? 4 : 8;
+    return S == 2 ? 2 : NT == 2 ? 4 : 8;
+}
+template <int T, int NT, int S>
+constexpr int rows_per_step() {
+    return S == 2 ? 2 : 2;
 }
 
 template <int T, int NT, int S, int LPR>
@@ -37,8 +41,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(lq_geom g, const uint8_t *__r
     for (int t = 0; t < NT; ++t) xrow[t] = X + t * x_stride;
     int vi;
     bool writer;
-    const float part = wave_rows<T, NT, S, R, LPR>(W, g, row0, 0, g.rows, w * S, xrow, xlds + w * S * NT * 16 * LPR,
-                                                   vi, writer);
+    const float part = wave_rows<T, NT, S, R, LPR, 1, rows_per_step<T, NT, S>()>(
+        W, g, row0, 0, g.rows, w * S, xrow, xlds + w * S * NT * 16 * LPR, vi, writer);
     if (nw == 1) {
         const int r = vi / NT, t = vi % NT;
         const int64_t row = row0 + (lane_id() / LPR) * R + r;
@@ -63,8 +67,7 @@ GemvPlan gemv_plan(const lq_geom &g, int nt) {
     p.lpr = lanes_per_row(U);
     p.slots = U > 256 ? 2 : 1;
     p.waves = p.lpr < 64 ? 1 : (int)((U + 64 * p.slots - 1) / (64 * p.slots));
-    const bool wide = g.type == LQ_Q6_K || g.type == LQ_Q5_K;
-    const int r = p.slots == 2 ? 2 : nt == 2 ? 4 : wide ? 4 : 8;
+    const int r = p.slots == 2 ? 2 : nt == 2 ? 4 : 8;
     p.rows = r * (64 / p.lpr);
     p.lds_bytes = (size_t)p.waves * p.slots * nt * 16 * p.lpr * 16;
     return p;

@@ -293,26 +293,30 @@ __device__ __forceinline__ float xreduce(float *v, int &index) {
 // Lanes per row for rows of U units: 64, or 32 / 16 when the row is that short.
 __host__ __device__ __forceinline__ int lanes_per_row(int64_t U) { return U <= 16 ? 16 : U <= 32 ? 32 : 64; }
 
-// Rows in flight: lane group gi = lane / LPR (G = 64 / LPR groups) takes rows
+// Rows: lane group gi = lane / LPR (G = 64 / LPR groups) takes rows
 // set_base + gi * RG + rr, rr < RG = R / SETS, of each of the SETS row sets
 // (set 0 starts at row0, set 1 at rowb); rows >= nrows contribute zero.
 // Units: slot s of the wave covers units 64 * (slot0 + s) + (lane % LPR).
 // lds: this wave's S * NT * 16 * LPR float4 of LDS. xrow[t]: vector t (K floats).
+// The R rows are processed P at a time (R / P steps) with the weight fields
+// of the next two steps in flight: step i + 2 is issued once step i's
+// arithmetic is done, so each wave streams its rows while it computes
+// instead of waiting for all of them and computing at the end.
 // Returns, for writer lanes, the partial sum over this wave's units of value
 // vi = r * NT + t (r = set * RG + rr) of the lane's group.
-template <int T, int NT, int S, int R, int LPR, int SETS = 1>
+template <int T, int NT, int S, int R, int LPR, int SETS = 1, int P = R>
 __device__ __forceinline__ float wave_rows(const uint8_t *__restrict__ W, const lq_geom &g, int64_t row0,
                                            int64_t rowb, int64_t nrows, int slot0,
                                            const float *const *xrow, float4 *lds, int &vi, bool &writer) {
-    static_assert(R % SETS == 0 && R * NT <= LPR, "row map");
+    static_assert(R % SETS == 0 && R * NT <= LPR && R % P == 0, "row map");
+    constexpr int STEPS = R / P;
     const int lane = lane_id();
     const int U = (int)g.nu;
     const int gi = lane / LPR, li = lane % LPR;
     constexpr int RG = R / SETS;
-    // x windows are loaded first, then every row's weight fields, and no
-    // arithmetic is placed in between (scheduler barrier): the wave has one
-    // memory round trip, and as loads complete in issue order, the LDS
-    // transposition of x waits only for the x loads.
+    // x windows are loaded first, then the first two steps' weight fields,
+    // with no arithmetic in between (scheduler barrier); loads complete in
+    // issue order, so the LDS transposition of x waits only for the x loads.
     float4 xs[S][NT][LPR / 4];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -324,24 +328,29 @@ __device__ __forceinline__ float wave_rows(const uint8_t *__restrict__ W, const 
 #pragma unroll
         for (int t = 0; t < NT; ++t) stage_load<LPR>(xrow[t] + vc, (int)nq, xs[s][t]);
     }
-    UnitW wt[R][S];
-    bool live[R][S];
+    UnitW wt[2][P][S];
+    bool live[2][P][S];
+    auto issue = [&](int buf, int step) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int set = r / RG, rr = r % RG;
-        const int64_t want = (set ? rowb : row0) + gi * RG + rr;
-        const bool row_live = want < nrows;
-        const int64_t row = row_live ? want : nrows - 1;
+        for (int p = 0; p < P; ++p) {
+            const int r = step * P + p;
+            const int set = r / RG, rr = r % RG;
+            const int64_t want = (set ? rowb : row0) + gi * RG + rr;
+            const bool row_live = want < nrows;
+            const int64_t row = row_live ? want : nrows - 1;
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const int u = 64 * (slot0 + s) + li;
-            const int uc = u < U ? u : U - 1;
-            const int c0 = uc & ~63;
-            const int C = U - c0 < 64 ? U - c0 : 64;
-            live[r][s] = u < U && row_live;
-            wt[r][s] = load_unit_w<T>(W, g, row, uc, C);
+            for (int s = 0; s < S; ++s) {
+                const int u = 64 * (slot0 + s) + li;
+                const int uc = u < U ? u : U - 1;
+                const int c0 = uc & ~63;
+                const int C = U - c0 < 64 ? U - c0 : 64;
+                live[buf][p][s] = u < U && row_live;
+                wt[buf][p][s] = load_unit_w<T>(W, g, row, uc, C);
+            }
         }
-    }
+    };
+    issue(0, 0);
+    if (STEPS > 1) issue(1, 1);
     __builtin_amdgcn_sched_barrier(0);
     float xr[S][NT][64], q4[S][NT][4];
 #pragma unroll
@@ -358,16 +367,25 @@ __device__ __forceinline__ float wave_rows(const uint8_t *__restrict__ W, const 
 #pragma unroll
     for (int i = 0; i < R * NT; ++i) acc[i] = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+    for (int st = 0; st < STEPS; ++st) {
+        const int buf = st & 1;
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const int u = 64 * (slot0 + s) + li;
-            const int uc = u < U ? u : U - 1;
+        for (int p = 0; p < P; ++p) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const float c = unit_dot<T>(wt[r][s], uc, xr[s][t], q4[s][t]);
-                acc[r * NT + t] += live[r][s] ? c : 0.0f;
+            for (int s = 0; s < S; ++s) {
+                const int u = 64 * (slot0 + s) + li;
+                const int uc = u < U ? u : U - 1;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const float c = unit_dot<T>(wt[buf][p][s], uc, xr[s][t], q4[s][t]);
+                    acc[(st * P + p) * NT + t] += live[buf][p][s] ? c : 0.0f;
+                }
             }
+        }
+        if (st + 2 < STEPS) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(buf, st + 2);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     const float total = xreduce<R * NT, LPR>(acc, vi);

@@ -28,8 +28,11 @@ namespace {
 std::mutex g_mu;
 std::vector<std::pair<uintptr_t, size_t>> g_ranges;
 std::map<std::tuple<uintptr_t, int, int, int>, localai_qmat *> g_cache;
-float *g_x = nullptr, *g_y = nullptr;
-size_t g_x_cap = 0, g_y_cap = 0;
+float *g_x = nullptr, *g_y = nullptr, *g_ws = nullptr;
+size_t g_x_cap = 0, g_y_cap = 0, g_ws_cap = 0;
+// tokens from which the legacy matmul runs the MFMA GEMM (f16 operands, fp32
+// accumulation) instead of the fp32 matvec
+constexpr int kGemmTokens = 32;
 
 bool assume_immutable() {
     const char *e = getenv("LOCALAI_HIP_ASSUME_IMMUTABLE");
@@ -98,19 +101,32 @@ int run(int t, const uint8_t *raw, const float *x, float *out, int rows, int col
         hipError_t e = hipMemcpy(g_x, x, (size_t)tokens * cols * 4, hipMemcpyHostToDevice);
         if (e != hipSuccess) st = hip_fail(e, "upload x");
     }
-    if (!st) st = launch_matvec(m->g, m->data, g_x, cols, g_y, rows, tokens, nullptr);
-    if (!st) {
-        if (!transpose_out) {
+    // many-token calls take the MFMA GEMM and write the reference's [rows, tokens]
+    // layout directly (engine/native_quant.cpp:492); fewer tokens take the fp32 matvec
+    const bool gemm = transpose_out && tokens >= kGemmTokens;
+    if (!st && gemm) {
+        const int64_t wsb = gemm_workspace_bytes(m->g, tokens);
+        st = grow(&g_ws, &g_ws_cap, (size_t)(wsb + 3) / 4);
+        if (!st) st = launch_gemm(m->g, m->data, g_x, tokens, g_y, 1, tokens, g_ws, wsb, nullptr);
+        if (!st) {
             hipError_t e = hipMemcpy(out, g_y, (size_t)tokens * rows * 4, hipMemcpyDeviceToHost);
             if (e != hipSuccess) st = hip_fail(e, "download y");
-        } else {
-            // reference matmul output is [rows, tokens] (engine/native_quant.cpp:492)
-            std::vector<float> tmp((size_t)tokens * rows);
-            hipError_t e = hipMemcpy(tmp.data(), g_y, tmp.size() * 4, hipMemcpyDeviceToHost);
-            if (e != hipSuccess) st = hip_fail(e, "download y");
-            else
-                for (int tk = 0; tk < tokens; ++tk)
-                    for (int r = 0; r < rows; ++r) out[(size_t)r * tokens + tk] = tmp[(size_t)tk * rows + r];
+        }
+    } else {
+        if (!st) st = launch_matvec(m->g, m->data, g_x, cols, g_y, rows, tokens, nullptr);
+        if (!st) {
+            if (!transpose_out) {
+                hipError_t e = hipMemcpy(out, g_y, (size_t)tokens * rows * 4, hipMemcpyDeviceToHost);
+                if (e != hipSuccess) st = hip_fail(e, "download y");
+            } else {
+                // reference matmul output is [rows, tokens] (engine/native_quant.cpp:492)
+                std::vector<float> tmp((size_t)tokens * rows);
+                hipError_t e = hipMemcpy(tmp.data(), g_y, tmp.size() * 4, hipMemcpyDeviceToHost);
+                if (e != hipSuccess) st = hip_fail(e, "download y");
+                else
+                    for (int tk = 0; tk < tokens; ++tk)
+                        for (int r = 0; r < rows; ++r) out[(size_t)r * tokens + tk] = tmp[(size_t)tk * rows + r];
+            }
         }
     }
     if (temp) localai_hip_qmat_destroy(m);

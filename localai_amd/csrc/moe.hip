@@ -78,12 +78,16 @@ __global__ __launch_bounds__(512) void moe_route_kernel(const float *__restrict_
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int i = i0 + 64 * j + lane;
-                hv[j] = i < H ? ht[i] : 0.0f;
-                wv[j] = i < H ? we[i] : 0.0f;
+                const int ic = i < H ? i : H - 1;      // unconditional loads: no wait per load
+                hv[j] = ht[ic];
+                wv[j] = we[ic];
             }
 #pragma unroll
-            for (int j = 0; j < CH; ++j)
-                if (i0 + 64 * j + lane < H) s = __builtin_fma((double)hv[j], (double)wv[j], s);
+            for (int j = 0; j < CH; ++j) {
+                // elements past H add an exact zero product
+                const double hj = i0 + 64 * j + lane < H ? (double)hv[j] : 0.0;
+                s = __builtin_fma(hj, (double)wv[j], s);
+            }
         }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);

@@ -113,6 +113,10 @@ def matvec(raw, x, rows: int, cols: int, ggml_type: int, threads: int = 4):
     return y.cpu().numpy()
 
 
+# Token count from which matmul() runs the MFMA GEMM instead of the fp32 matvec.
+GEMM_TOKENS = 32
+
+
 def matmul(raw, vectors, rows: int, cols: int, ggml_type: int, threads: int = 4):
     """X @ W^T for GGML bytes W [rows, cols]; float32 [tokens, rows], or None."""
     expected = _validate(raw, rows, cols, ggml_type)
@@ -128,5 +132,6 @@ def matmul(raw, vectors, rows: int, cols: int, ggml_type: int, threads: int = 4)
         raise ValueError('native quantized matmul received an invalid tensor size')
     q = weights(raw, rows, cols, ggml_type)
     xd = device.to_device_f32(x)
-    y = q.matvec(xd)
+    # many tokens: MFMA GEMM (f16 operands, fp32 accumulation); few: fp32 matvec
+    y = q.matmul(xd) if x.shape[0] >= GEMM_TOKENS else q.matvec(xd)
     return y.cpu().numpy()

@@ -134,6 +134,11 @@ def test_native_quant_mirror_contract():
     assert normwise_rel(m, quant.matmul_exact(raw, 12, 300, 512, v)) < 1e-5
     with pytest.raises(ValueError):
         nq.matmul(raw, v[:, :256], 300, 512, 12)
+    # from 32 tokens the MFMA GEMM path (f16 operands): the GEMM tolerance
+    v = rng.standard_normal((40, 512)).astype(np.float32)
+    m = nq.matmul(raw, v, 300, 512, 12)
+    assert m.shape == (40, 300)
+    assert normwise_rel(m, quant.matmul_exact(raw, 12, 300, 512, v)) < 1e-3
 
 
 def test_native_quant_cache_reuses_immutable_weights():
@@ -189,6 +194,9 @@ def test_legacy_exports(name, t):
     v = rng.standard_normal((5, cols)).astype(np.float32)
     got = _legacy(lib, name, raw, v, rows, cols, tokens=5)        # [rows, tokens]
     assert normwise_rel(got.T, quant.matmul_exact(raw, t, rows, cols, v)) < 1e-5
+    v = rng.standard_normal((33, cols)).astype(np.float32)       # MFMA GEMM path
+    got = _legacy(lib, name, raw, v, rows, cols, tokens=33)
+    assert normwise_rel(got.T, quant.matmul_exact(raw, t, rows, cols, v)) < 1e-3
 
 
 def test_legacy_registered_range_uses_cached_copy():
