@@ -48,6 +48,14 @@ int ensure_device() {
     return LOCALAI_OK;
 }
 
+// The MFMA matvec (gemv_mfma.hip) keeps a second, tile-form copy of Q4_K
+// weights for single-vector decode; LOCALAI_HIP_MFMA_MATVEC=0 turns it off
+// (the row-plane matvec then serves every call).
+bool mfma_matvec_enabled() {
+    const char *e = getenv("LOCALAI_HIP_MFMA_MATVEC");
+    return !(e && e[0] == '0');
+}
+
 size_t max_lds_per_block() {
     static std::atomic<int64_t> cached{-1};
     int64_t v = cached.load();
@@ -122,6 +130,8 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
     localai_qmat *m = new localai_qmat;
     m->g = g;
     m->data = nullptr;
+    m->tiles = nullptr;
+    m->tile_bytes = 0;
     hipGetDevice(&m->device);
     size_t nbytes = (size_t)(g.matrix_bytes * batch);
     hipError_t e = hipMalloc(&m->data, nbytes);
@@ -141,6 +151,16 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
         dsrc = (const uint8_t *)staging;
     }
     int st = launch_repack(g, dsrc, m->data, 0, s);
+    if (st == LOCALAI_OK && mfma_matvec_enabled() && mt_matrix_bytes(g) > 0) {
+        m->tile_bytes = mt_matrix_bytes(g);
+        e = hipMalloc(&m->tiles, (size_t)(m->tile_bytes * batch));
+        if (e != hipSuccess) {
+            m->tiles = nullptr;
+            st = hip_fail(e, "hipMalloc(qmat tiles)");
+        } else {
+            st = launch_mt_repack(g, dsrc, m->tiles, m->tile_bytes, s);
+        }
+    }
     if (staging) {
         hipError_t e2 = hipStreamSynchronize(s);
         hipFree(staging);
@@ -148,6 +168,7 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
     }
     if (st != LOCALAI_OK) {
         hipFree(m->data);
+        if (m->tiles) hipFree(m->tiles);
         delete m;
         return st;
     }
@@ -159,6 +180,7 @@ int localai_hip_qmat_destroy(localai_qmat *m) {
     clear_error();
     if (!m) return LOCALAI_OK;
     hipFree(m->data);
+    if (m->tiles) hipFree(m->tiles);
     delete m;
     return LOCALAI_OK;
 }
@@ -201,6 +223,8 @@ int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x, fl
     if (int st = ensure_device()) return st;
     lq_geom one = m->g;
     one.batch = 1;
+    if (m->tiles && ntok == 1)
+        return launch_matvec_mfma(one, m->tiles + expert * m->tile_bytes, x, y, (hipStream_t)stream);
     return launch_matvec(one, m->data + expert * m->g.matrix_bytes, x, m->g.cols, y, m->g.rows, ntok,
                          (hipStream_t)stream);
 }

@@ -11,6 +11,8 @@ struct localai_qmat {
     lq_geom g;
     uint8_t *data;      // device, g.matrix_bytes * g.batch (row planes, qformat.h)
     int device;
+    uint8_t *tiles;     // device, MFMA tile form (gemv_mfma.hip) or null
+    int64_t tile_bytes; // per matrix of the tile form
 };
 
 namespace lq {
@@ -44,6 +46,11 @@ struct GemvPlan {
 GemvPlan gemv_plan(const lq_geom &g, int nt);
 int launch_matvec(const lq_geom &g, const uint8_t *packed, const float *x, int64_t x_stride,
                   float *y, int64_t y_stride, int ntok, hipStream_t s);
+
+int64_t mt_matrix_bytes(const lq_geom &g);
+int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_t dst_matrix_bytes, hipStream_t s);
+int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s);
+bool mfma_matvec_enabled();
 
 int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok);
 int launch_gemm(const lq_geom &g, const uint8_t *packed, const float *x, int64_t ntok, float *y, int64_t y_ts,

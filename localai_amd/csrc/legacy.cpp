@@ -113,7 +113,8 @@ int run(int t, const uint8_t *raw, const float *x, float *out, int rows, int col
             if (e != hipSuccess) st = hip_fail(e, "download y");
         }
     } else {
-        if (!st) st = launch_matvec(m->g, m->data, g_x, cols, g_y, rows, tokens, nullptr);
+        if (!st) st = (m->tiles && tokens == 1) ? launch_matvec_mfma(m->g, m->tiles, g_x, g_y, nullptr)
+                                                : launch_matvec(m->g, m->data, g_x, cols, g_y, rows, tokens, nullptr);
         if (!st) {
             if (!transpose_out) {
                 hipError_t e = hipMemcpy(out, g_y, (size_t)tokens * rows * 4, hipMemcpyDeviceToHost);
