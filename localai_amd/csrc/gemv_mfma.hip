@@ -1,53 +1,52 @@
 // Decode matvec on MFMA for Q4_K and Q6_K: y[r] = sum_c W[r, c] * x[c].
 //
 // Weights come from a second device form of the matrix, the "tile form": rows
-// in tiles of 16, and per (tile, super-block) one 2304-byte block
-//   qs piece 0 [64 lanes][16 B]   qs piece 1 [64 lanes][16 B]   headers [16 rows][16 B]
-// where lane L = n + 16c (row n of the tile, 8-value chunk c) holds bytes
-// 32p + 8c .. 32p + 8c + 7 of the row's qs for group pairs p = 0, 1 (piece 0)
-// and p = 2, 3 (piece 1). That is exactly the B operand of
-// v_mfma_f32_16x16x32_f16 (lane l: k = 8 (l / 16) .. + 7, n = l % 16), so
-// every load instruction of a wave reads 1 KiB contiguous.
+// in tiles of 16, and per (tile, super-block) one block whose quant bytes are
+// stored so that each 16-byte lane slice is directly the B operand of
+// v_mfma_i32_16x16x64_i8 (lane l: column n = l % 16, k = 16 (l / 16) .. + 15,
+// bytes in k order). Lane L = n + 16c of a block holds row n's bytes
+// 8c .. 8c + 7 of two 32-byte quant chunks, so every load instruction of a
+// wave reads 1 KiB contiguous.
 //
-// Arithmetic, per (tile, super-block), one MFMA per 32-value group g:
-//   B = the group's 4-bit quants as f16 subnormals (bits = q, value q * 2^-24:
-//       exact; high nibbles are taken in place, value 16 q * 2^-24)
-//   A = x of the group as an exact two-term f16 expansion: x * 2^s = hi + lo
-//       (hi = f16(x 2^s), lo = f16(x 2^s - hi); 22 significant bits), in the
-//       rows m = 2g (hi) and 2g + 1 (lo) of the 16-row A operand, zero
-//       elsewhere (block diagonal)
-//   D[m][n] accumulates, after the 8 groups, sum_k q * x_split for every
-//   (group, split) in its own row m: products are exact in fp32 and the sums
-//   are fp32, so D carries the group dot products at fp32 accuracy.
-// Lane l then holds D rows 4 (l / 16) .. + 3 of row n = l % 16: groups 2q
-// and 2q + 1 (q = l / 16), both splits, and applies the group scales once:
-//   acc += d sc_2q (D0 + D1) + d sc_2q+1 (D2 + D3) / 16   (times 2^24 2^-s)
-//        - dmin (mn_2q X_2q + mn_2q+1 X_2q+1)               (X = group sums of x)
-// -- the factorisation of engine/native_quant.cpp:183-231 without quantising x.
+// Arithmetic, per (tile, super-block):
+//   B = the quants as unsigned bytes (Q4_K: a nibble, 0..15, masked in place;
+//       Q6_K: low nibble | high 2 bits << 4, 0..63), four MFMAs of 64 values
+//   A = x as three int8 pieces per value: with 2^s chosen per scale group so
+//       that max |x| 2^s lies in [32, 64),
+//         x 2^s = p0 + p1 / 128 + p2 / 16384 + e,  |e| <= 2^-15,
+//       each piece rounded with the 1.5 * 2^23 magic-number add (exact steps).
+//       A row m = 4 slot + piece carries one scale group in its k range and
+//       zero elsewhere (block diagonal), so D[4 slot + piece][n] is the exact
+//       integer dot product of that group's quants with one piece.
+//   The lane holding D rows 4q .. 4q + 2 of column n then forms
+//     sum_group q x = 2^-s (D0 + D1 / 128 + D2 / 16384)
+//   and applies the group's scales -- the factorisation of
+//   engine/native_quant.cpp:183-231 (Q4_K) and :298-341 (Q6_K) without
+//   quantising x (relative error of x about 1e-6 of the group maximum).
 //
-// x staging: each wave converts the x values of its super-blocks into the
-// A fragment layout in its own LDS region ([m][c][8 halves] per super-block)
-// plus the eight group sums; lane l reads the fragment of its (m, c) into
-// A register a[m / 2] with an exec mask, so the other seven A registers of
-// the lane stay zero and no VALU work goes into the block-diagonal zeros.
+// x staging: each wave converts the x values of its super-blocks into
+// [group][piece][k / 8][8 bytes] in its own LDS region plus per-group
+// (sum of x, 2^-s); each lane reads the 8 bytes of its (row, k) slice and
+// places them in the low or high half of its A register with an AND mask.
 #include "gemv_core.h"
 #include "internal.h"
 
 namespace lq {
 
-typedef _Float16 mt_h8 __attribute__((ext_vector_type(8)));
-typedef float mt_f4 __attribute__((ext_vector_type(4)));
+typedef int mt_i4 __attribute__((ext_vector_type(4)));
 
 constexpr int MT_ROWS = 16;
 constexpr int MT_Q4K_BLOCK = 2304;
 constexpr int MT_Q6K_BLOCK = 3360;     // ql 2 x 1 KiB, qh 1 KiB, scales 16 x 16 B, d 16 x 2 B
-constexpr int MT_XBYTES = 1024 + 64;   // Q4_K per super-block: A fragments + 8 x (group sum, scale)
-constexpr int MT6_XBYTES = 1024 + 128; // Q6_K per super-block: A fragments + 16 x (sub-block sum, scale)
+constexpr int MT_XBYTES = 1024 + 64;   // Q4_K per super-block: x pieces + 8 x (group sum, 2^-s)
+constexpr int MT6_XBYTES = 1024 + 128; // Q6_K per super-block: x pieces + 16 x (sub-block sum, 2^-s)
 
 __host__ __device__ constexpr int mt_block_bytes(int t) { return t == LQ_Q4_K ? MT_Q4K_BLOCK : MT_Q6K_BLOCK; }
 
+// 0 when the matrix gets no tile form (other types, or K beyond the 72
+// super-blocks the launch plan covers): its matvecs then run on gemv.hip.
 int64_t mt_matrix_bytes(const lq_geom &g) {
-    if (g.type != LQ_Q4_K && g.type != LQ_Q6_K) return 0;
+    if ((g.type != LQ_Q4_K && g.type != LQ_Q6_K) || g.nb > 72) return 0;
     const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
     return lq_align256(tiles * g.nb * mt_block_bytes(g.type));
 }
@@ -120,73 +119,143 @@ int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_
     return LOCALAI_OK;
 }
 
-// f16 pairs (bits = byte value) of bytes 0,1 and 2,3 of a masked dword:
-// v_perm_b32 selector bytes 0..3 pick bytes of the second operand, 0x0C a zero
-__device__ __forceinline__ uint32_t mt_lo_pair(uint32_t m) { return __builtin_amdgcn_perm(0u, m, 0x0C010C00u); }
-__device__ __forceinline__ uint32_t mt_hi_pair(uint32_t m) { return __builtin_amdgcn_perm(0u, m, 0x0C030C02u); }
-// A fragment of a lane in one MFMA: its x values where the lane's row is
-// nonzero, zero elsewhere (mask all ones or all zeros)
-__device__ __forceinline__ mt_h8 mt_masked(uint4 f, uint32_t mask) {
-    return __builtin_bit_cast(mt_h8, make_uint4(f.x & mask, f.y & mask, f.z & mask, f.w & mask));
-}
-
-// B operand of group g (pair g / 2, nibble g % 2) from the lane's two qs pieces
-__device__ __forceinline__ mt_h8 mt_b_q4k(uint4 p0, uint4 p1, int g) {
-    const uint4 pc = (g >> 2) ? p1 : p0;
-    const uint32_t d0 = (g & 2) ? pc.z : pc.x, d1 = (g & 2) ? pc.w : pc.y;
-    const uint32_t mask = (g & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-    const uint32_t m0 = d0 & mask, m1 = d1 & mask;
-    uint4 r;
-    r.x = mt_lo_pair(m0);
-    r.y = mt_hi_pair(m0);
-    r.z = mt_lo_pair(m1);
-    r.w = mt_hi_pair(m1);
-    return __builtin_bit_cast(mt_h8, r);
-}
-
-// Sum / max of a value over each aligned group of 8 lanes, in every lane of
-// the group: DPP quad_perm [1,0,3,2], quad_perm [2,3,0,1], then
-// row_half_mirror (lane i <-> 7 - i inside each 8) -- no LDS round trip.
+// Value of lane l ^ 1 (quad_perm [1,0,3,2], 0xB1), l ^ 2 (quad_perm [2,3,0,1],
+// 0x4E) or 7 - l inside each 8 (row_half_mirror, 0x141): DPP moves used for
+// sums / maxima over aligned groups of 4 or 8 lanes without an LDS round trip.
 template <int CTRL>
 __device__ __forceinline__ float mt_dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float mt_group8_sum(float v) {
-    v += mt_dpp<0xB1>(v);
-    v += mt_dpp<0x4E>(v);
-    return v + mt_dpp<0x141>(v);
-}
-__device__ __forceinline__ float mt_group8_max(float v) {
-    v = fmaxf(v, mt_dpp<0xB1>(v));
-    v = fmaxf(v, mt_dpp<0x4E>(v));
-    return fmaxf(v, mt_dpp<0x141>(v));
+
+constexpr float MT_MAGIC = 12582912.0f;   // 1.5 * 2^23: x + MAGIC holds rint(x) in its low mantissa bits
+
+// Three int8 pieces of a = x 2^s (|a| < 64) as the low bytes of t0, t1, t2:
+// a = p0 + p1 / 128 + p2 / 16384 + e. Every step is exact except the three
+// roundings to integers (fma of exactly representable terms, products by
+// powers of two, differences of nearby numbers).
+__device__ __forceinline__ void mt_split(float x, float S, float S128, uint32_t &b0, uint32_t &b1,
+                                         uint32_t &b2) {
+    const float t0 = __builtin_fmaf(x, S, MT_MAGIC);
+    const float r1 = __builtin_fmaf(x, S128, __builtin_fmaf(-128.0f, t0, 128.0f * MT_MAGIC));
+    const float t1 = r1 + MT_MAGIC;
+    const float r2 = __builtin_fmaf(r1, 128.0f, __builtin_fmaf(-128.0f, t1, 128.0f * MT_MAGIC));
+    const float t2 = r2 + MT_MAGIC;
+    b0 = __builtin_bit_cast(uint32_t, t0);
+    b1 = __builtin_bit_cast(uint32_t, t1);
+    b2 = __builtin_bit_cast(uint32_t, t2);
 }
 
-// SPW super-blocks per wave (the wave's K slice), RT row tiles per workgroup.
-// Per super-block the LDS region holds the A fragments [m = 2j + s][c][8
-// halves] and, per group j, (sum of x, 2^(24 - s_j)) where 2^s_j is the
-// group's power-of-two scale into f16 range.
+// Low bytes of four words packed into one (byte i from word i). v_perm_b32:
+// selector bytes 0..3 pick bytes of the second operand, 4..7 of the first,
+// 0x0C gives zero.
+__device__ __forceinline__ uint32_t mt_pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x0C0C0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(d, c, 0x0C0C0400u);
+    return lo | (hi << 16);
+}
+
+// Scale exponent s for a group maximum m: m 2^s in [32, 64); 0 for zero,
+// infinite or NaN maxima; clamped so 2^s, 2^(s+7) and 2^-s stay normal.
+__device__ __forceinline__ int mt_group_shift(float gmax) {
+    int sh = 0;
+    if (gmax > 0.0f && gmax <= 3.4e38f) {
+        int e;
+        frexpf(gmax, &e);
+        sh = 6 - e;
+        sh = sh > 118 ? 118 : sh < -120 ? -120 : sh;
+    }
+    return sh;
+}
+
+// Convert four x values (natural positions 4 lane .. + 3 of a super-block)
+// into pieces and store them; returns (sum, 2^-s) of the lane's group.
+template <int GL>   // lanes per scale group: 8 (32 values) or 4 (16 values)
+__device__ __forceinline__ float2 mt_stage_x(float4 v, uint8_t *dst, int stride_piece) {
+    float gs = (v.x + v.y) + (v.z + v.w);
+    float gm = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    gs += mt_dpp<0xB1>(gs);
+    gm = fmaxf(gm, mt_dpp<0xB1>(gm));
+    gs += mt_dpp<0x4E>(gs);
+    gm = fmaxf(gm, mt_dpp<0x4E>(gm));
+    if (GL == 8) {
+        gs += mt_dpp<0x141>(gs);
+        gm = fmaxf(gm, mt_dpp<0x141>(gm));
+    }
+    const int sh = mt_group_shift(gm);
+    const float S = ldexpf(1.0f, sh), S128 = ldexpf(1.0f, sh + 7);
+    uint32_t a0, a1, a2, b0, b1, b2, c0, c1, c2, d0, d1, d2;
+    mt_split(v.x, S, S128, a0, a1, a2);
+    mt_split(v.y, S, S128, b0, b1, b2);
+    mt_split(v.z, S, S128, c0, c1, c2);
+    mt_split(v.w, S, S128, d0, d1, d2);
+    *reinterpret_cast<uint32_t *>(dst) = mt_pack4(a0, b0, c0, d0);
+    *reinterpret_cast<uint32_t *>(dst + stride_piece) = mt_pack4(a1, b1, c1, d1);
+    *reinterpret_cast<uint32_t *>(dst + 2 * stride_piece) = mt_pack4(a2, b2, c2, d2);
+    return make_float2(gs, ldexpf(1.0f, -sh));
+}
+
+// A operand: the lane's 8 bytes in the low (mlo) or high (mhi) half, or zero
+__device__ __forceinline__ mt_i4 mt_place(uint2 r, uint32_t mlo, uint32_t mhi) {
+    return mt_i4{(int)(r.x & mlo), (int)(r.y & mlo), (int)(r.x & mhi), (int)(r.y & mhi)};
+}
+
+// sum over the group of q x from D rows (piece 0, 1, 2), before 2^-s
+__device__ __forceinline__ float mt_pieces(mt_i4 D) {
+    return __builtin_fmaf((float)D[2], 0x1p-14f, __builtin_fmaf((float)D[1], 0x1p-7f, (float)D[0]));
+}
+
+__device__ __forceinline__ mt_i4 mt_as_i4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return mt_i4{(int)a, (int)b, (int)c, (int)d};
+}
+
+// Shared loads of both kernels: x of the wave's super-blocks, then the tile
+// blocks. Every load is unconditional (clamped indices) so they all issue
+// before the first use.
+#define MT_PROLOGUE(XBYTES)                                                                   \
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];                            \
+    const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;                          \
+    const int sb0 = w * SPW;                                                                  \
+    int nsb = nb - sb0;                                                                       \
+    nsb = nsb < 0 ? 0 : nsb > SPW ? SPW : nsb;                                                \
+    uint8_t *wl = smem + w * SPW * (XBYTES);                                                  \
+    float *red = reinterpret_cast<float *>(smem + nw * SPW * (XBYTES));                       \
+    const int64_t tile0 = (int64_t)blockIdx.x * RT;                                           \
+    float4 xv[SPW];                                                                           \
+    _Pragma("unroll") for (int k = 0; k < SPW; ++k) {                                         \
+        const int sb = sb0 + k < nb ? sb0 + k : nb - 1;                                       \
+        xv[k] = *reinterpret_cast<const float4 *>(x + 256 * (int64_t)sb + 4 * lane);          \
+    }
+
+// Cross-wave and cross-lane-group sum of acc[RT] into y
+#define MT_EPILOGUE                                                                           \
+    _Pragma("unroll") for (int t = 0; t < RT; ++t) red[(w * RT + t) * 64 + lane] = acc[t];   \
+    __syncthreads();                                                                          \
+    const int i = threadIdx.x;                                                                \
+    if (i < RT * 16) {                                                                        \
+        const int t = i >> 4, n = i & 15;                                                     \
+        float s = 0.0f;                                                                       \
+        for (int k = 0; k < nw; ++k) {                                                        \
+            const float *r = red + (k * RT + t) * 64 + n;                                     \
+            s += (r[0] + r[16]) + (r[32] + r[48]);                                            \
+        }                                                                                     \
+        const int64_t row = (tile0 + t) * MT_ROWS + n;                                        \
+        if (tile0 + t < tiles && row < rows) y[row] = s;                                      \
+    }
+
+// ------------------------------------------------------------------- Q4_K
+// MFMA t of a super-block takes qs piece t / 2, nibble t % 2: bytes 0..7 of
+// lane group q are values 8q .. 8q + 7 of group gA(t), bytes 8..15 those of
+// group gB(t) = gA(t) + 2, with gA = 0, 1, 4, 5. MFMAs 0, 1 accumulate into D0
+// and 2, 3 into D1; MFMA t uses A slots 2 (t % 2) (group gA) and
+// 2 (t % 2) + 1 (group gB), so D lane group q ends with group
+// (q / 2) + 2 (q % 2) (+ 4 for D1).
+// LDS per super-block: pieces [group 8][piece 4][k / 8: 4][8 B] (1 KiB), then
+// (sum, 2^-s) per group.
 template <int SPW, int RT, int MAXT>
 __global__ __launch_bounds__(MAXT) void gemv_mfma_q4k(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
-                                                     int64_t tiles, const float *__restrict__ x,
-                                                     float *__restrict__ y) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
-    const int sb0 = w * SPW;
-    int nsb = nb - sb0;
-    nsb = nsb < 0 ? 0 : nsb > SPW ? SPW : nsb;
-    uint8_t *wl = smem + w * SPW * MT_XBYTES;
-    float *red = reinterpret_cast<float *>(smem + nw * SPW * MT_XBYTES);   // [nw][RT][64]
-    const int64_t tile0 = (int64_t)blockIdx.x * RT;
-
-    // ---- loads: x first (it is needed first), then every weight block ----
-    float4 xv[SPW];
-#pragma unroll
-    for (int k = 0; k < SPW; ++k) {
-        const int sb = sb0 + k < nb ? sb0 + k : nb - 1;
-        const float4 v = *reinterpret_cast<const float4 *>(x + 256 * (int64_t)sb + 4 * lane);
-        xv[k] = v;   // unconditional: fragments of k >= nsb are written but never read
-    }
+                                                      int64_t tiles, const float *__restrict__ x,
+                                                      float *__restrict__ y) {
+    MT_PROLOGUE(MT_XBYTES)
     uint4 q0[RT][SPW], q1[RT][SPW], hd[RT][SPW];
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
@@ -203,42 +272,24 @@ __global__ __launch_bounds__(MAXT) void gemv_mfma_q4k(const uint8_t *__restrict_
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- x -> A fragments (hi/lo f16 of x * 2^s_j per group) + group data ----
-    {
-        const int j = lane >> 3, c = (lane & 7) >> 1;
-        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    {   // lane l: values 4l .. 4l + 3 = group l / 8, k / 8 = (l % 8) / 2, byte 4 (l % 2)
+        const int g = lane >> 3;
 #pragma unroll
         for (int k = 0; k < SPW; ++k) {
-            const float4 v = xv[k];
-            const float gs = mt_group8_sum((v.x + v.y) + (v.z + v.w));
-            const float gmax = mt_group8_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-            int sh = 0;
-            if (gmax > 0.0f && gmax <= 3.4e38f) {
-                int e;
-                frexpf(gmax, &e);
-                sh = 15 - e;                  // group max * 2^sh in [2^14, 2^15)
-                sh = sh > 100 ? 100 : sh < -100 ? -100 : sh;
-            }
-            const float up = ldexpf(1.0f, sh);
             uint8_t *frag = wl + k * MT_XBYTES;
-            if ((lane & 7) == 7)
-                reinterpret_cast<float2 *>(frag + 1024)[j] = make_float2(gs, ldexpf(1.0f, 24 - sh));
-            const float a0 = v.x * up, a1 = v.y * up, a2 = v.z * up, a3 = v.w * up;
-            const _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1, h2 = (_Float16)a2, h3 = (_Float16)a3;
-            const _Float16 l0 = (_Float16)(a0 - (float)h0), l1 = (_Float16)(a1 - (float)h1);
-            const _Float16 l2 = (_Float16)(a2 - (float)h2), l3 = (_Float16)(a3 - (float)h3);
-            *reinterpret_cast<h4 *>(frag + ((2 * j) * 4 + c) * 16 + (lane & 1) * 8) = h4{h0, h1, h2, h3};
-            *reinterpret_cast<h4 *>(frag + ((2 * j + 1) * 4 + c) * 16 + (lane & 1) * 8) = h4{l0, l1, l2, l3};
+            const float2 gd = mt_stage_x<8>(xv[k], frag + g * 128 + ((lane & 7) >> 1) * 8 + 4 * (lane & 1), 32);
+            if ((lane & 7) == 0) reinterpret_cast<float2 *>(frag + 1024)[g] = gd;
         }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-    // ---- MFMA over (tile, super-block) ----
-    mt_h8 a[8];
-    const int m = lane & 15, q = lane >> 4, ga = m >> 1;
-    uint32_t amask[8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) amask[g] = ga == g ? ~0u : 0u;
+    const int m = lane & 15, q = lane >> 4, slot = m >> 2, pc = m & 3;
+    const int ga = (slot >> 1) + 2 * (slot & 1);   // A: group of this lane's row in MFMAs t = slot / 2, + 2
+    const int gd = (q >> 1) + 2 * (q & 1);         // D: group of this lane's rows in D0 (D1: + 4)
+    const uint32_t on = pc < 3 ? ~0u : 0u;
+    const uint32_t mlo = (slot & 1) ? 0u : on, mhi = (slot & 1) ? on : 0u;
+    const uint32_t ev = (slot >> 1) ? 0u : ~0u, od = ~ev;
+    const int aoff = ga * 128 + pc * 32 + q * 8;
     float acc[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) acc[t] = 0.0f;
@@ -246,97 +297,54 @@ __global__ __launch_bounds__(MAXT) void gemv_mfma_q4k(const uint8_t *__restrict_
     for (int k = 0; k < SPW; ++k) {
         if (k >= nsb) break;
         const uint8_t *frag = wl + k * MT_XBYTES;
-        const uint4 f = *reinterpret_cast<const uint4 *>(frag + (m * 4 + q) * 16);
-        // lane's A fragment lives in a[m / 2] only; the other registers are zero
-#pragma unroll
-        for (int g = 0; g < 8; ++g) a[g] = mt_masked(f, amask[g]);
-        // (sum, 2^(24 - s)) of groups 2q and 2q + 1
-        const float4 gx = *reinterpret_cast<const float4 *>(frag + 1024 + 16 * q);
+        const uint2 r0 = *reinterpret_cast<const uint2 *>(frag + aoff);
+        const uint2 r1 = *reinterpret_cast<const uint2 *>(frag + aoff + 512);
+        const mt_i4 A0 = mt_place(r0, mlo & ev, mhi & ev), A1 = mt_place(r0, mlo & od, mhi & od);
+        const mt_i4 A2 = mt_place(r1, mlo & ev, mhi & ev), A3 = mt_place(r1, mlo & od, mhi & od);
+        const float2 x0 = reinterpret_cast<const float2 *>(frag + 1024)[gd];
+        const float2 x1 = reinterpret_cast<const float2 *>(frag + 1024)[gd + 4];
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            mt_f4 dacc = mt_f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int g = 0; g < 8; ++g)
-                dacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[g], mt_b_q4k(q0[t][k], q1[t][k], g), dacc, 0, 0, 0);
-            uint32_t sc0, sc1, mn0, mn1;
-            kq_pair(hd[t][k], q, sc0, sc1, mn0, mn1);
-            const float d = f16_to_f32(hd[t][k].x), dmin = f16_to_f32(hd[t][k].x >> 16);
-            const float s = __builtin_fmaf((float)sc1 * 0.0625f * gx.w, dacc[2] + dacc[3],
-                                           (float)sc0 * gx.y * (dacc[0] + dacc[1]));
-            acc[t] = __builtin_fmaf(d, s, acc[t]);
-            acc[t] = __builtin_fmaf(-dmin, __builtin_fmaf((float)mn0, gx.x, (float)mn1 * gx.z), acc[t]);
+            const uint4 a = q0[t][k], b = q1[t][k];
+            const uint32_t M = 0x0F0F0F0Fu;
+            mt_i4 D0 = mt_i4{0, 0, 0, 0}, D1 = mt_i4{0, 0, 0, 0};
+            D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, mt_as_i4(a.x & M, a.y & M, a.z & M, a.w & M), D0, 0, 0, 0);
+            D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                A1, mt_as_i4((a.x >> 4) & M, (a.y >> 4) & M, (a.z >> 4) & M, (a.w >> 4) & M), D0, 0, 0, 0);
+            D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, mt_as_i4(b.x & M, b.y & M, b.z & M, b.w & M), D1, 0, 0, 0);
+            D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                A3, mt_as_i4((b.x >> 4) & M, (b.y >> 4) & M, (b.z >> 4) & M, (b.w >> 4) & M), D1, 0, 0, 0);
+            // 6-bit scale / min of groups gd (< 4) and gd + 4 (engine/dequant.py:107-113)
+            const uint4 h = hd[t][k];
+            const uint32_t s0 = __builtin_amdgcn_ubfe(h.y, 8 * gd, 8);
+            const uint32_t s4 = __builtin_amdgcn_ubfe(h.z, 8 * gd, 8);
+            const uint32_t s8 = __builtin_amdgcn_ubfe(h.w, 8 * gd, 8);
+            const float sc0 = (float)(s0 & 63u), mn0 = (float)(s4 & 63u);
+            const float sc1 = (float)((s8 & 15u) | ((s0 >> 6) << 4)), mn1 = (float)((s8 >> 4) | ((s4 >> 6) << 4));
+            const float d = f16_to_f32(h.x), dmin = f16_to_f32(h.x >> 16);
+            const float v = __builtin_fmaf(sc1 * x1.y, mt_pieces(D1), sc0 * x0.y * mt_pieces(D0));
+            const float u = __builtin_fmaf(mn1, x1.x, mn0 * x0.x);
+            acc[t] = __builtin_fmaf(-dmin, u, __builtin_fmaf(d, v, acc[t]));
         }
     }
-    // ---- reduce over the four lanes of a row and the waves, through LDS ----
-#pragma unroll
-    for (int t = 0; t < RT; ++t) red[(w * RT + t) * 64 + lane] = acc[t];
-    __syncthreads();
-    const int i = threadIdx.x;
-    if (i < RT * 16) {
-        const int t = i >> 4, n = i & 15;
-        float s = 0.0f;
-        for (int k = 0; k < nw; ++k) {
-            const float *r = red + (k * RT + t) * 64 + n;
-            s += (r[0] + r[16]) + (r[32] + r[48]);
-        }
-        const int64_t row = (tile0 + t) * MT_ROWS + n;
-        if (tile0 + t < tiles && row < rows) y[row] = s;
-    }
+    MT_EPILOGUE
 }
 
 // ------------------------------------------------------------------- Q6_K
-// MFMA t of a super-block covers natural values 32t .. 32t + 31 (half h =
-// t / 4, quad c' = t % 4): q = ((ql >> 4 (c' / 2)) & 15) | ((qh >> 2c') & 3) << 4
-// (engine/dequant.py:146-165), 0..63, as f16 subnormals. The block-diagonal A
-// rows are (sub-block of the half jj = 0..7, split): value 32 (t % 4) + 8c + e
-// of the half lies in sub-block 2 (t % 4) + c / 2, so lane (m, c) is nonzero
-// in MFMA t only when m / 2 = 2 (t % 4) + c / 2, i.e. in A register a[m / 4].
-// t6 is a compile-time constant after unrolling at every call site
-__device__ __forceinline__ mt_h8 mt_b_q6k(int t6, uint4 ql_h, uint4 qh) {
-    const int cq = t6 & 3, h = t6 >> 2;
-    const uint32_t d0 = (cq & 1) ? ql_h.z : ql_h.x, d1 = (cq & 1) ? ql_h.w : ql_h.y;
-    const uint32_t e0 = h ? qh.z : qh.x, e1 = h ? qh.w : qh.y;
-    const uint32_t m0 = ((d0 >> (4 * (cq >> 1))) & 0x0F0F0F0Fu) | (((e0 >> (2 * cq)) & 0x03030303u) << 4);
-    const uint32_t m1 = ((d1 >> (4 * (cq >> 1))) & 0x0F0F0F0Fu) | (((e1 >> (2 * cq)) & 0x03030303u) << 4);
-    uint4 r;
-    r.x = mt_lo_pair(m0);
-    r.y = mt_hi_pair(m0);
-    r.z = mt_lo_pair(m1);
-    r.w = mt_hi_pair(m1);
-    return __builtin_bit_cast(mt_h8, r);
-}
-
-__device__ __forceinline__ float mt_quad_sum(float v) {
-    v += mt_dpp<0xB1>(v);
-    return v + mt_dpp<0x4E>(v);
-}
-__device__ __forceinline__ float mt_quad_max(float v) {
-    v = fmaxf(v, mt_dpp<0xB1>(v));
-    return fmaxf(v, mt_dpp<0x4E>(v));
-}
-
-// Per super-block LDS: A fragments [half][jj][split][c & 1][8 halves] (1 KiB)
-// and per sub-block (sum of x, 2^(24 - s)) (128 B).
+// MFMA i of a super-block covers values 64 i .. 64 i + 63 (half i / 2, ql
+// nibble i % 2): bytes 0..7 of lane group q are sub-block 4i + q / 2, values
+// 8 (q % 2) + 0..7, and bytes 8..15 sub-block 4i + 2 + q / 2. Quants are
+// q = (ql >> 4 (i % 2)) & 15 | ((qh >> 2 j) & 3) << 4 (engine/dequant.py:146-165),
+// unsigned; the -32 offset goes through the sub-block sums of x. Each MFMA
+// has its own D; A slot = sub-block 4i + slot, so D lane group q holds
+// sub-block 4i + q.
+// LDS per super-block: pieces [sub-block 16][piece 4][k / 8: 2][8 B] (1 KiB),
+// then (sum, 2^-s) per sub-block.
 template <int SPW, int RT, int MAXT>
 __global__ __launch_bounds__(MAXT) void gemv_mfma_q6k(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
                                                       int64_t tiles, const float *__restrict__ x,
                                                       float *__restrict__ y) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
-    const int sb0 = w * SPW;
-    int nsb = nb - sb0;
-    nsb = nsb < 0 ? 0 : nsb > SPW ? SPW : nsb;
-    uint8_t *wl = smem + w * SPW * MT6_XBYTES;
-    float *red = reinterpret_cast<float *>(smem + nw * SPW * MT6_XBYTES);   // [nw][RT][64]
-    const int64_t tile0 = (int64_t)blockIdx.x * RT;
-
-    float4 xv[SPW];
-#pragma unroll
-    for (int k = 0; k < SPW; ++k) {
-        const int sb = sb0 + k < nb ? sb0 + k : nb - 1;
-        const float4 v = *reinterpret_cast<const float4 *>(x + 256 * (int64_t)sb + 4 * lane);
-        xv[k] = v;   // unconditional: fragments of k >= nsb are written but never read
-    }
+    MT_PROLOGUE(MT6_XBYTES)
     uint4 ql0[RT][SPW], ql1[RT][SPW], qh[RT][SPW], sc[RT][SPW];
     uint32_t dd[RT][SPW];
 #pragma unroll
@@ -356,43 +364,21 @@ __global__ __launch_bounds__(MAXT) void gemv_mfma_q6k(const uint8_t *__restrict_
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- x -> A fragments and sub-block data ----
-    {
-        const int h = lane >> 5, jj = (lane & 31) >> 2, cb = (lane & 3) >> 1;
-        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    {   // lane l: values 4l .. 4l + 3 = sub-block l / 4, k / 8 = (l % 4) / 2, byte 4 (l % 2)
+        const int j = lane >> 2;
 #pragma unroll
         for (int k = 0; k < SPW; ++k) {
-            const float4 v = xv[k];
-            const float gs = mt_quad_sum((v.x + v.y) + (v.z + v.w));
-            const float gmax = mt_quad_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-            int sh = 0;
-            if (gmax > 0.0f && gmax <= 3.4e38f) {
-                int e;
-                frexpf(gmax, &e);
-                sh = 15 - e;
-                sh = sh > 100 ? 100 : sh < -100 ? -100 : sh;
-            }
-            const float up = ldexpf(1.0f, sh);
             uint8_t *frag = wl + k * MT6_XBYTES;
-            if ((lane & 3) == 0)
-                reinterpret_cast<float2 *>(frag + 1024)[8 * h + jj] = make_float2(gs, ldexpf(1.0f, 24 - sh));
-            const float a0 = v.x * up, a1 = v.y * up, a2 = v.z * up, a3 = v.w * up;
-            const _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1, h2 = (_Float16)a2, h3 = (_Float16)a3;
-            const _Float16 l0 = (_Float16)(a0 - (float)h0), l1 = (_Float16)(a1 - (float)h1);
-            const _Float16 l2 = (_Float16)(a2 - (float)h2), l3 = (_Float16)(a3 - (float)h3);
-            const int base = ((h * 8 + jj) * 2) * 2 + cb;     // [h][jj][s][cb], s = 0
-            *reinterpret_cast<h4 *>(frag + base * 16 + (lane & 1) * 8) = h4{h0, h1, h2, h3};
-            *reinterpret_cast<h4 *>(frag + (base + 2) * 16 + (lane & 1) * 8) = h4{l0, l1, l2, l3};
+            const float2 gd = mt_stage_x<4>(xv[k], frag + j * 64 + ((lane & 3) >> 1) * 8 + 4 * (lane & 1), 16);
+            if ((lane & 3) == 0) reinterpret_cast<float2 *>(frag + 1024)[j] = gd;
         }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-    mt_h8 a[4];
-    const int m = lane & 15, q = lane >> 4, jj = m >> 1, sp = m & 1;
-    const bool active = (q >> 1) == (jj & 1);
-    uint32_t amask[4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) amask[g] = (active && (jj >> 1) == g) ? ~0u : 0u;
+    const int m = lane & 15, q = lane >> 4, slot = m >> 2, pc = m & 3;
+    const uint32_t on = (pc < 3 && (slot & 1) == (q >> 1)) ? ~0u : 0u;
+    const uint32_t mlo = (slot >> 1) ? 0u : on, mhi = (slot >> 1) ? on : 0u;
+    const int aoff = slot * 64 + pc * 16 + (q & 1) * 8;
     float acc[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) acc[t] = 0.0f;
@@ -400,71 +386,60 @@ __global__ __launch_bounds__(MAXT) void gemv_mfma_q6k(const uint8_t *__restrict_
     for (int k = 0; k < SPW; ++k) {
         if (k >= nsb) break;
         const uint8_t *frag = wl + k * MT6_XBYTES;
+        mt_i4 A[4];
+        float2 xg[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint4 f = *reinterpret_cast<const uint4 *>(frag + ((((h * 8 + jj) * 2 + sp) * 2) + (q & 1)) * 16);
+        for (int i = 0; i < 4; ++i) {
+            A[i] = mt_place(*reinterpret_cast<const uint2 *>(frag + aoff + 256 * i), mlo, mhi);
+            xg[i] = reinterpret_cast<const float2 *>(frag + 1024)[4 * i + q];
+        }
 #pragma unroll
-            for (int g = 0; g < 4; ++g) a[g] = mt_masked(f, amask[g]);
-            // (sum, scale) of sub-blocks 8h + 2q and 8h + 2q + 1
-            const float4 gx = *reinterpret_cast<const float4 *>(frag + 1024 + 8 * (8 * h + 2 * q));
+        for (int t = 0; t < RT; ++t) {
+            const uint32_t L = 0x0F0F0F0Fu;
+            float s = 0.0f;
 #pragma unroll
-            for (int t = 0; t < RT; ++t) {
-                const uint4 qlh = h ? ql1[t][k] : ql0[t][k];
-                mt_f4 dacc = mt_f4{0.0f, 0.0f, 0.0f, 0.0f};
-                dacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], mt_b_q6k(4 * h + 0, qlh, qh[t][k]), dacc, 0, 0, 0);
-                dacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], mt_b_q6k(4 * h + 1, qlh, qh[t][k]), dacc, 0, 0, 0);
-                dacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2], mt_b_q6k(4 * h + 2, qlh, qh[t][k]), dacc, 0, 0, 0);
-                dacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[3], mt_b_q6k(4 * h + 3, qlh, qh[t][k]), dacc, 0, 0, 0);
-                // int8 scales 8h + 2q, 8h + 2q + 1 of row n
-                const uint32_t sw = (q >> 1) ? (h ? sc[t][k].w : sc[t][k].y) : (h ? sc[t][k].z : sc[t][k].x);
-                const uint32_t s2 = sw >> (16 * (q & 1));
-                const float sa = (float)(int8_t)(s2 & 0xFFu), sb = (float)(int8_t)((s2 >> 8) & 0xFFu);
-                const float va = __builtin_fmaf(gx.y, dacc[0] + dacc[1], -32.0f * gx.x);
-                const float vb = __builtin_fmaf(gx.w, dacc[2] + dacc[3], -32.0f * gx.z);
-                acc[t] = __builtin_fmaf(f16_to_f32(dd[t][k]), __builtin_fmaf(sa, va, sb * vb), acc[t]);
+            for (int i = 0; i < 4; ++i) {
+                const uint4 l = (i >> 1) ? ql1[t][k] : ql0[t][k];
+                const uint32_t e0 = (i >> 1) ? qh[t][k].z : qh[t][k].x;
+                const uint32_t e1 = (i >> 1) ? qh[t][k].w : qh[t][k].y;
+                mt_i4 B;
+                if (i & 1)
+                    B = mt_as_i4(((l.x >> 4) & L) | (e0 & 0x30303030u), ((l.y >> 4) & L) | (e1 & 0x30303030u),
+                                 ((l.z >> 4) & L) | ((e0 >> 2) & 0x30303030u),
+                                 ((l.w >> 4) & L) | ((e1 >> 2) & 0x30303030u));
+                else
+                    B = mt_as_i4((l.x & L) | ((e0 << 4) & 0x30303030u), (l.y & L) | ((e1 << 4) & 0x30303030u),
+                                 (l.z & L) | ((e0 << 2) & 0x30303030u), (l.w & L) | ((e1 << 2) & 0x30303030u));
+                const mt_i4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], B, mt_i4{0, 0, 0, 0}, 0, 0, 0);
+                const uint32_t sw = i == 0 ? sc[t][k].x : i == 1 ? sc[t][k].y : i == 2 ? sc[t][k].z : sc[t][k].w;
+                const float scf = (float)(int)__builtin_amdgcn_sbfe((int)sw, 8 * q, 8);   // the builtin returns unsigned
+                s = __builtin_fmaf(scf, __builtin_fmaf(mt_pieces(D), xg[i].y, -32.0f * xg[i].x), s);
             }
+            acc[t] = __builtin_fmaf(f16_to_f32(dd[t][k]), s, acc[t]);
         }
     }
-#pragma unroll
-    for (int t = 0; t < RT; ++t) red[(w * RT + t) * 64 + lane] = acc[t];
-    __syncthreads();
-    const int i = threadIdx.x;
-    if (i < RT * 16) {
-        const int t = i >> 4, n = i & 15;
-        float s = 0.0f;
-        for (int k = 0; k < nw; ++k) {
-            const float *r = red + (k * RT + t) * 64 + n;
-            s += (r[0] + r[16]) + (r[32] + r[48]);
-        }
-        const int64_t row = (tile0 + t) * MT_ROWS + n;
-        if (tile0 + t < tiles && row < rows) y[row] = s;
-    }
+    MT_EPILOGUE
 }
 
-// Launch plan: the waves of a workgroup split the super-blocks. Rows of at
-// most 32 super-blocks use up to 16 waves with SPW * RT <= 2 (short per-wave
-// work keeps the latency chain of each wave short; 128 VGPRs suffice), longer
-// rows up to 8 waves with SPW = ceil(nb / 8). Two row tiles per workgroup when
-// that still gives about 4096 waves.
+#undef MT_PROLOGUE
+#undef MT_EPILOGUE
+
+// Launch plan: the waves of a workgroup split the super-blocks of one row
+// tile (or RT tiles), SPW super-blocks per wave.
+//   nb <= 32: SPW = 1 or 2, up to 16 waves; two tiles per workgroup when
+//             there are enough tiles to keep every CU busy
+//   nb > 32:  SPW = ceil(nb / 12), up to 12 waves (768 threads, so each wave
+//             may hold all of its SPW blocks in registers)
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s) {
     if (g.type != LQ_Q4_K && g.type != LQ_Q6_K) return fail(LOCALAI_ETYPE, "mfma matvec: Q4_K / Q6_K only");
     if (reinterpret_cast<uintptr_t>(x) & 15) return fail(LOCALAI_EARG, "mfma matvec: x must be 16-byte aligned");
     const int nb = (int)g.nb;
+    if (nb > 72) return fail(LOCALAI_EARG, "mfma matvec: K too large (more than 18432 values)");
     const bool q6 = g.type == LQ_Q6_K;
     const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
-    int spw = (nb + 15) / 16, waves, rt;
-    bool big;
-    if (spw <= 2) {
-        waves = (nb + spw - 1) / spw;
-        rt = (spw == 1 && tiles * waves >= 4096) ? 2 : 1;
-        big = true;
-    } else {
-        spw = (nb + 7) / 8;
-        waves = (nb + spw - 1) / spw;
-        rt = 1;
-        big = false;
-    }
-    if (spw > 8) return fail(LOCALAI_EARG, "mfma matvec: K too large (more than 16384 values)");
+    const int spw = nb <= 32 ? (nb + 15) / 16 : (nb + 11) / 12;
+    const int waves = (nb + spw - 1) / spw;
+    const int rt = (spw == 1 && tiles * waves >= 4096) ? 2 : 1;
     dim3 grid((unsigned)((tiles + rt - 1) / rt)), block(64 * waves);
     const size_t lds = (size_t)waves * spw * (q6 ? MT6_XBYTES : MT_XBYTES) + (size_t)waves * rt * 64 * 4;
 #define MT_L(S, R, M)                                                                                     \
@@ -472,19 +447,13 @@ int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, floa
         if (q6) hipLaunchKernelGGL((gemv_mfma_q6k<S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y); \
         else hipLaunchKernelGGL((gemv_mfma_q4k<S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y);    \
     } while (0)
-    if (big) {
-        if (spw == 1 && rt == 2) MT_L(1, 2, 1024);
-        else if (spw == 1) MT_L(1, 1, 1024);
-        else MT_L(2, 1, 1024);
-    } else {
-        switch (spw) {
-            case 3: MT_L(3, 1, 512); break;
-            case 4: MT_L(4, 1, 512); break;
-            case 5: MT_L(5, 1, 512); break;
-            case 6: MT_L(6, 1, 512); break;
-            case 7: MT_L(7, 1, 512); break;
-            default: MT_L(8, 1, 512); break;
-        }
+    switch (spw) {
+        case 1: if (rt == 2) MT_L(1, 2, 1024); else MT_L(1, 1, 1024); break;
+        case 2: MT_L(2, 1, 1024); break;
+        case 3: MT_L(3, 1, 768); break;
+        case 4: MT_L(4, 1, 768); break;
+        case 5: MT_L(5, 1, 768); break;
+        default: MT_L(6, 1, 768); break;
     }
 #undef MT_L
     LQ_HIP(hipGetLastError());
