@@ -91,6 +91,16 @@ int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out_d
 int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x_dev,
                        float *y_dev, int ntok, void *stream);
 
+/* Several decode matvecs that share one input vector:
+ *   ys_dev[j][r] = sum_c W_j[r, c] * x[c],  W_j = matrix experts[j] of mats[j]
+ * (experts may be NULL: matrix 0 of every handle). Counterpart of consecutive
+ * mat() calls on one vector -- attn_q/k/v (engine/model.py:185-187) and
+ * ffn_gate/up (engine/model.py:232) -- with the Q4_K / Q6_K matrices computed
+ * in one launch (results identical to localai_hip_matvec on each matrix).
+ * 1 <= n <= 8; every matrix must have the same cols. */
+int localai_hip_matvec_many(int n, const localai_qmat *const *mats, const int64_t *experts,
+                            const float *x_dev, float *const *ys_dev, void *stream);
+
 /* ---- prefill matmul (MFMA) ---------------------------------------------- */
 
 /* Bytes of device workspace localai_hip_matmul needs for `tokens` rows of x. */

@@ -32,6 +32,7 @@ SIGNATURES = {
     'localai_hip_qmat_unpack': (_c_int, [_vp, _vp, _vp]),
     'localai_hip_qmat_dequant': (_c_int, [_vp, _c_i64, _vp, _vp]),
     'localai_hip_matvec': (_c_int, [_vp, _c_i64, _vp, _vp, _c_int, _vp]),
+    'localai_hip_matvec_many': (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp]),
     'localai_hip_matmul_workspace_size': (_c_i64, [_vp, _c_i64]),
     'localai_hip_matmul': (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_i64, _vp]),
     'localai_hip_moe_workspace_size': (_c_i64, [_c_i64, _c_i64, _c_int, _c_i64, _c_i64]),

@@ -229,6 +229,43 @@ int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x, fl
                          (hipStream_t)stream);
 }
 
+int localai_hip_matvec_many(int n, const localai_qmat *const *mats, const int64_t *experts, const float *x,
+                            float *const *ys, void *stream) {
+    clear_error();
+    if (n < 1 || n > 8) return fail(LOCALAI_EARG, "n must be 1..8");
+    if (!mats || !x || !ys) return fail(LOCALAI_EARG, "null pointer");
+    for (int j = 0; j < n; ++j) {
+        if (!mats[j] || !ys[j]) return fail(LOCALAI_EARG, "null pointer");
+        const int64_t e = experts ? experts[j] : 0;
+        if (e < 0 || e >= mats[j]->g.batch) return fail(LOCALAI_EARG, "expert index out of range");
+        if (mats[j]->g.cols != mats[0]->g.cols) return fail(LOCALAI_EARG, "all matrices need the same cols");
+    }
+    if (int st = ensure_device()) return st;
+    hipStream_t s = (hipStream_t)stream;
+    // matrices with a tile form share one MFMA launch; the rest run one by one
+    lq_geom geo[8];
+    const lq_geom *gp[8];
+    const uint8_t *wt[8];
+    float *yp[8];
+    int nf = 0;
+    for (int j = 0; j < n; ++j) {
+        const int64_t e = experts ? experts[j] : 0;
+        lq_geom one = mats[j]->g;
+        one.batch = 1;
+        if (mats[j]->tiles) {
+            geo[nf] = one;
+            gp[nf] = &geo[nf];
+            wt[nf] = mats[j]->tiles + e * mats[j]->tile_bytes;
+            yp[nf] = ys[j];
+            ++nf;
+        } else if (int st = launch_matvec(one, mats[j]->data + e * mats[j]->g.matrix_bytes, x, one.cols, ys[j],
+                                          one.rows, 1, s)) {
+            return st;
+        }
+    }
+    return nf ? launch_matvec_mfma_many(nf, gp, wt, x, yp, s) : LOCALAI_OK;
+}
+
 int64_t localai_hip_matmul_workspace_size(const localai_qmat *m, int64_t tokens) {
     if (!m || tokens < 0) return -1;
     return gemm_workspace_bytes(m->g, tokens);

@@ -36,6 +36,7 @@ namespace lq {
 typedef int mt_i4 __attribute__((ext_vector_type(4)));
 
 constexpr int MT_ROWS = 16;
+constexpr int MT_MAX_JOBS = 8;        // matrices per fused launch (localai_hip_matvec_many)
 constexpr int MT_Q4K_BLOCK = 2304;
 constexpr int MT_Q6K_BLOCK = 3360;     // ql 2 x 1 KiB, qh 1 KiB, scales 16 x 16 B, d 16 x 2 B
 constexpr int MT_XBYTES = 1024 + 64;   // Q4_K per super-block: x pieces + 8 x (group sum, 2^-s)
@@ -219,7 +220,7 @@ __device__ __forceinline__ mt_i4 mt_as_i4(uint32_t a, uint32_t b, uint32_t c, ui
     nsb = nsb < 0 ? 0 : nsb > SPW ? SPW : nsb;                                                \
     uint8_t *wl = smem + w * SPW * (XBYTES);                                                  \
     float *red = reinterpret_cast<float *>(smem + nw * SPW * (XBYTES));                       \
-    const int64_t tile0 = (int64_t)blockIdx.x * RT;                                           \
+    const int64_t tile0 = blk * RT;                                                           \
     float4 xv[SPW];                                                                           \
     _Pragma("unroll") for (int k = 0; k < SPW; ++k) {                                         \
         const int sb = sb0 + k < nb ? sb0 + k : nb - 1;                                       \
@@ -251,10 +252,9 @@ __device__ __forceinline__ mt_i4 mt_as_i4(uint32_t a, uint32_t b, uint32_t c, ui
 // (q / 2) + 2 (q % 2) (+ 4 for D1).
 // LDS per super-block: pieces [group 8][piece 4][k / 8: 4][8 B] (1 KiB), then
 // (sum, 2^-s) per group.
-template <int SPW, int RT, int MAXT>
-__global__ __launch_bounds__(MAXT) void gemv_mfma_q4k(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
-                                                      int64_t tiles, const float *__restrict__ x,
-                                                      float *__restrict__ y) {
+template <int SPW, int RT>
+__device__ __forceinline__ void mt_body_q4k(const uint8_t *__restrict__ Wt, int64_t rows, int nb, int64_t tiles,
+                                            const float *__restrict__ x, float *__restrict__ y, int64_t blk) {
     MT_PROLOGUE(MT_XBYTES)
     uint4 q0[RT][SPW], q1[RT][SPW], hd[RT][SPW];
 #pragma unroll
@@ -340,10 +340,9 @@ __global__ __launch_bounds__(MAXT) void gemv_mfma_q4k(const uint8_t *__restrict_
 // sub-block 4i + q.
 // LDS per super-block: pieces [sub-block 16][piece 4][k / 8: 2][8 B] (1 KiB),
 // then (sum, 2^-s) per sub-block.
-template <int SPW, int RT, int MAXT>
-__global__ __launch_bounds__(MAXT) void gemv_mfma_q6k(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
-                                                      int64_t tiles, const float *__restrict__ x,
-                                                      float *__restrict__ y) {
+template <int SPW, int RT>
+__device__ __forceinline__ void mt_body_q6k(const uint8_t *__restrict__ Wt, int64_t rows, int nb, int64_t tiles,
+                                            const float *__restrict__ x, float *__restrict__ y, int64_t blk) {
     MT_PROLOGUE(MT6_XBYTES)
     uint4 ql0[RT][SPW], ql1[RT][SPW], qh[RT][SPW], sc[RT][SPW];
     uint32_t dd[RT][SPW];
@@ -424,12 +423,72 @@ __global__ __launch_bounds__(MAXT) void gemv_mfma_q6k(const uint8_t *__restrict_
 #undef MT_PROLOGUE
 #undef MT_EPILOGUE
 
+// One matrix: workgroup b takes row tiles b RT .. b RT + RT - 1.
+template <int SPW, int RT, int MAXT>
+__global__ __launch_bounds__(MAXT) void gemv_mfma_q4k(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
+                                                      int64_t tiles, const float *__restrict__ x,
+                                                      float *__restrict__ y) {
+    mt_body_q4k<SPW, RT>(Wt, rows, nb, tiles, x, y, blockIdx.x);
+}
+template <int SPW, int RT, int MAXT>
+__global__ __launch_bounds__(MAXT) void gemv_mfma_q6k(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
+                                                      int64_t tiles, const float *__restrict__ x,
+                                                      float *__restrict__ y) {
+    mt_body_q6k<SPW, RT>(Wt, rows, nb, tiles, x, y, blockIdx.x);
+}
+
+// Several matrices with the same K and the same x in one launch: job j owns
+// workgroups blk0[j] .. blk0[j + 1] - 1 (uniform branch per workgroup).
+struct MtJobs {
+    const uint8_t *Wt[MT_MAX_JOBS];
+    float *y[MT_MAX_JOBS];
+    int64_t rows[MT_MAX_JOBS];
+    int64_t blk0[MT_MAX_JOBS + 1];
+    int type[MT_MAX_JOBS];
+    int n;
+};
+template <int SPW, int RT, int MAXT>
+__global__ __launch_bounds__(MAXT) void gemv_mfma_many(MtJobs jobs, int nb, const float *__restrict__ x) {
+    const int64_t b = blockIdx.x;
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < MT_MAX_JOBS; ++i)
+        if (i < jobs.n && b >= jobs.blk0[i]) j = i;
+    const int64_t tiles = (jobs.rows[j] + MT_ROWS - 1) / MT_ROWS;
+    if (jobs.type[j] == LQ_Q6_K) mt_body_q6k<SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
+    else mt_body_q4k<SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
+}
+
 // Launch plan: the waves of a workgroup split the super-blocks of one row
 // tile (or RT tiles), SPW super-blocks per wave.
-//   nb <= 32: SPW = 1 or 2, up to 16 waves; two tiles per workgroup when
-//             there are enough tiles to keep every CU busy
+//   nb <= 32, >= 768 tiles: SPW = ceil(nb / 16), up to 16 waves, two tiles
+//             per workgroup when SPW = 1 (x staged once for both)
+//   nb <= 32, fewer tiles:  SPW = ceil(nb / 8), up to 8 waves, one tile per
+//             workgroup, so that small matrices still spread over the CUs
 //   nb > 32:  SPW = ceil(nb / 12), up to 12 waves (768 threads, so each wave
 //             may hold all of its SPW blocks in registers)
+struct MtPlan {
+    int spw, waves, rt;
+};
+static MtPlan mt_plan(int nb, int64_t tiles) {
+    MtPlan p;
+    const bool big = tiles >= 768;
+    p.spw = nb > 32 ? (nb + 11) / 12 : big ? (nb + 15) / 16 : (nb + 7) / 8;
+    p.waves = (nb + p.spw - 1) / p.spw;
+    p.rt = (big && p.spw == 1) ? 2 : 1;
+    return p;
+}
+
+#define MT_DISPATCH(L)                                         \
+    switch (p.spw) {                                           \
+        case 1: if (p.rt == 2) L(1, 2, 1024); else L(1, 1, 1024); break; \
+        case 2: L(2, 1, 1024); break;                          \
+        case 3: L(3, 1, 768); break;                           \
+        case 4: L(4, 1, 768); break;                           \
+        case 5: L(5, 1, 768); break;                           \
+        default: L(6, 1, 768); break;                          \
+    }
+
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s) {
     if (g.type != LQ_Q4_K && g.type != LQ_Q6_K) return fail(LOCALAI_ETYPE, "mfma matvec: Q4_K / Q6_K only");
     if (reinterpret_cast<uintptr_t>(x) & 15) return fail(LOCALAI_EARG, "mfma matvec: x must be 16-byte aligned");
@@ -437,25 +496,53 @@ int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, floa
     if (nb > 72) return fail(LOCALAI_EARG, "mfma matvec: K too large (more than 18432 values)");
     const bool q6 = g.type == LQ_Q6_K;
     const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
-    const int spw = nb <= 32 ? (nb + 15) / 16 : (nb + 11) / 12;
-    const int waves = (nb + spw - 1) / spw;
-    const int rt = (spw == 1 && tiles * waves >= 4096) ? 2 : 1;
-    dim3 grid((unsigned)((tiles + rt - 1) / rt)), block(64 * waves);
-    const size_t lds = (size_t)waves * spw * (q6 ? MT6_XBYTES : MT_XBYTES) + (size_t)waves * rt * 64 * 4;
+    const MtPlan p = mt_plan(nb, tiles);
+    dim3 grid((unsigned)((tiles + p.rt - 1) / p.rt)), block(64 * p.waves);
+    const size_t lds = (size_t)p.waves * p.spw * (q6 ? MT6_XBYTES : MT_XBYTES) + (size_t)p.waves * p.rt * 64 * 4;
 #define MT_L(S, R, M)                                                                                     \
     do {                                                                                                  \
         if (q6) hipLaunchKernelGGL((gemv_mfma_q6k<S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y); \
         else hipLaunchKernelGGL((gemv_mfma_q4k<S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y);    \
     } while (0)
-    switch (spw) {
-        case 1: if (rt == 2) MT_L(1, 2, 1024); else MT_L(1, 1, 1024); break;
-        case 2: MT_L(2, 1, 1024); break;
-        case 3: MT_L(3, 1, 768); break;
-        case 4: MT_L(4, 1, 768); break;
-        case 5: MT_L(5, 1, 768); break;
-        default: MT_L(6, 1, 768); break;
-    }
+    MT_DISPATCH(MT_L)
 #undef MT_L
+    LQ_HIP(hipGetLastError());
+    return LOCALAI_OK;
+}
+
+int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const *Wt, const float *x,
+                            float *const *y, hipStream_t s) {
+    if (n < 1 || n > MT_MAX_JOBS) return fail(LOCALAI_EARG, "mfma matvec: 1..8 matrices per fused launch");
+    if (reinterpret_cast<uintptr_t>(x) & 15) return fail(LOCALAI_EARG, "mfma matvec: x must be 16-byte aligned");
+    const int nb = (int)g[0]->nb;
+    if (nb > 72) return fail(LOCALAI_EARG, "mfma matvec: K too large (more than 18432 values)");
+    int64_t total_tiles = 0;
+    bool any_q6 = false;
+    for (int j = 0; j < n; ++j) {
+        if (g[j]->type != LQ_Q4_K && g[j]->type != LQ_Q6_K) return fail(LOCALAI_ETYPE, "mfma matvec: Q4_K / Q6_K only");
+        if (g[j]->nb != nb) return fail(LOCALAI_EARG, "mfma matvec: fused matrices need the same cols");
+        total_tiles += (g[j]->rows + MT_ROWS - 1) / MT_ROWS;
+        any_q6 |= g[j]->type == LQ_Q6_K;
+    }
+    const MtPlan p = mt_plan(nb, total_tiles);
+    MtJobs jobs = {};
+    jobs.n = n;
+    int64_t b = 0;
+    for (int j = 0; j < n; ++j) {
+        jobs.Wt[j] = Wt[j];
+        jobs.y[j] = y[j];
+        jobs.rows[j] = g[j]->rows;
+        jobs.type[j] = g[j]->type;
+        jobs.blk0[j] = b;
+        b += ((g[j]->rows + MT_ROWS - 1) / MT_ROWS + p.rt - 1) / p.rt;
+    }
+    for (int j = n; j <= MT_MAX_JOBS; ++j) jobs.blk0[j] = b;
+    dim3 grid((unsigned)b), block(64 * p.waves);
+    const size_t lds = (size_t)p.waves * p.spw * (any_q6 ? MT6_XBYTES : MT_XBYTES) + (size_t)p.waves * p.rt * 64 * 4;
+#define MT_L(S, R, M) hipLaunchKernelGGL((gemv_mfma_many<S, R, M>), grid, block, lds, s, jobs, nb, x)
+    MT_DISPATCH(MT_L)
+#undef MT_L
+#undef MT_DISPATCH
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
 }

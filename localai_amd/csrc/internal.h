@@ -50,6 +50,8 @@ int launch_matvec(const lq_geom &g, const uint8_t *packed, const float *x, int64
 int64_t mt_matrix_bytes(const lq_geom &g);
 int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_t dst_matrix_bytes, hipStream_t s);
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s);
+int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const *Wt, const float *x,
+                            float *const *y, hipStream_t s);
 bool mfma_matvec_enabled();
 
 int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok);

@@ -180,3 +180,27 @@ class QMat:
             self.close()
         except Exception:
             pass
+
+
+def matvec_many(mats, x, outs=None, experts=None, stream=None):
+    """y_j = W_j @ x for several matrices sharing x (same cols), as one launch
+    for the Q4_K / Q6_K matrices: q/k/v or gate/up of a decode step.
+    Returns the list of [rows_j] outputs."""
+    t = torch()
+    if not mats or len(mats) > 8:
+        raise ValueError('matvec_many takes 1..8 matrices')
+    x2 = x.reshape(-1)
+    if x2.dtype != t.float32 or not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.to(t.float32).contiguous().clone()
+    for m in mats:
+        if m.cols != x2.shape[0]:
+            raise ValueError(f'x has {x2.shape[0]} values, matrix has {m.cols} columns')
+    if outs is None:
+        outs = [t.empty(m.rows, dtype=t.float32, device=x2.device) for m in mats]
+    n = len(mats)
+    handles = (ctypes.c_void_p * n)(*[m.handle.value for m in mats])
+    ex = (ctypes.c_int64 * n)(*([0] * n if experts is None else [int(e) for e in experts]))
+    ys = (ctypes.c_void_p * n)(*[ptr(o) for o in outs])
+    _lib.check(_lib.load().localai_hip_matvec_many(n, handles, ex, ptr(x2), ys,
+                                                   ctypes.c_void_p(stream_ptr(stream))))
+    return outs

@@ -253,3 +253,61 @@ def test_split_k_across_xcds(t, rows, cols):
     assert normwise_rel(first, quant.matvec_exact(raw, t, rows, cols, xh)) < 1e-5
     for o in outs[1:]:
         np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), first.view(np.uint32))
+
+
+@pytest.mark.parametrize('shapes', [
+    # attn_q / attn_k / attn_v of a Q4_K_M decode step (v in Q6_K): one mixed launch
+    [(12, 512, 4096), (12, 128, 4096), (14, 128, 4096)],
+    # ffn_gate / ffn_up shape family, ragged rows, long K (768-thread plan)
+    [(12, 100, 14336), (14, 37, 14336)],
+    # a matrix without a tile form (Q8_0) runs beside the fused Q4_K / Q6_K launch
+    [(8, 64, 2048), (14, 200, 2048), (12, 1, 2048), (12, 33, 2048)],
+])
+def test_matvec_many_matches_single(shapes):
+    """localai_hip_matvec_many gives bit-identical results to one matvec per
+    matrix (the same per-tile arithmetic), and both match the oracle."""
+    from localai_amd import device
+    rng = np.random.default_rng(len(shapes) * 1000 + shapes[0][1])
+    cols = shapes[0][2]
+    x = rng.standard_normal(cols).astype(np.float32)
+    raws = [random_ggml(rng, t, rows * cols) for t, rows, _ in shapes]
+    mats = [device.QMat.from_ggml(r, t, rows, cols) for r, (t, rows, _) in zip(raws, shapes)]
+    xd = device.to_device_f32(x)
+    try:
+        fused = [o.cpu().numpy() for o in device.matvec_many(mats, xd)]
+        single = [m.matvec(xd).cpu().numpy() for m in mats]
+    finally:
+        for m in mats:
+            m.close()
+    for (t, rows, _), raw, f, s in zip(shapes, raws, fused, single):
+        np.testing.assert_array_equal(f, s)
+        assert normwise_rel(f, quant.matvec_exact(raw, t, rows, cols, x)) < 1e-5
+
+
+def test_matvec_many_experts_and_errors():
+    """Expert selection per job, and the argument checks of the fused entry."""
+    from localai_amd import _lib, device
+    rng = np.random.default_rng(77)
+    E, rows, cols = 3, 48, 1024
+    raw = random_ggml(rng, 14, E * rows * cols)
+    m = device.QMat.from_ggml(raw, 14, rows, cols, batch=E)
+    other = device.QMat.from_ggml(random_ggml(rng, 12, rows * 512), 12, rows, 512)
+    x = rng.standard_normal(cols).astype(np.float32)
+    xd = device.to_device_f32(x)
+    try:
+        outs = device.matvec_many([m, m], xd, experts=[2, 0])
+        per = rows * cols * 210 // 256
+        for o, e in zip(outs, (2, 0)):
+            ref = quant.matvec_exact(raw[e * per:(e + 1) * per], 14, rows, cols, x)
+            assert normwise_rel(o.cpu().numpy(), ref) < 1e-5
+        with pytest.raises(ValueError):
+            device.matvec_many([m, other], xd)
+        lib = _lib.load()
+        h = (ctypes.c_void_p * 1)(m.handle.value)
+        ex = (ctypes.c_int64 * 1)(E)
+        ys = (ctypes.c_void_p * 1)(device.ptr(outs[0]))
+        assert lib.localai_hip_matvec_many(1, h, ex, device.ptr(xd), ys, None) != 0
+        assert lib.localai_hip_matvec_many(9, h, None, device.ptr(xd), ys, None) != 0
+    finally:
+        m.close()
+        other.close()
