@@ -136,7 +136,8 @@ int64_t localai_hip_moe_workspace_size(int64_t tokens, int64_t experts, int top_
  *   topk_w_dev    [tokens, top_k] fp32, softmax over the selected logits
  * Router logits: exact fp64 products summed in a fixed order, rounded to fp32
  * once, so the selected experts are bit-reproducible.
- * Limits: experts <= 1024, 1 <= top_k <= min(16, experts), inter % 64 == 0. */
+ * Limits: experts <= 1024, 1 <= top_k <= min(16, experts), inter % 64 == 0;
+ * h_dev and router_w_dev 16-byte aligned, workspace 256-byte aligned. */
 int localai_hip_moe_forward(const float *h_dev, int64_t tokens, int64_t hidden,
                             const float *router_w_dev, const float *router_b_dev,
                             int64_t experts, int top_k, const localai_qmat *gate_up,

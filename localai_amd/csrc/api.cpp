@@ -305,8 +305,9 @@ int localai_hip_moe_forward(const float *h, int64_t T, int64_t H, const float *r
     if (gu->g.cols != H || gu->g.rows % 2 || I % 64) return fail(LOCALAI_EARG, "moe: gate_up must be [E, 2*inter, hidden] with inter % 64 == 0");
     if (dn->g.rows != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe: down must be [E, hidden, inter]");
     if (ws_bytes < (int64_t)moe_workspace_bytes(T, E, k, H, I)) return fail(LOCALAI_EARG, "moe: workspace too small");
-    if ((reinterpret_cast<uintptr_t>(h) & 15) || (reinterpret_cast<uintptr_t>(ws) & 255))
-        return fail(LOCALAI_EARG, "moe: h must be 16-byte and workspace 256-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(h) & 15) || (reinterpret_cast<uintptr_t>(rw) & 15) ||
+        (reinterpret_cast<uintptr_t>(ws) & 255))
+        return fail(LOCALAI_EARG, "moe: h and router_w must be 16-byte and workspace 256-byte aligned");
     if (int st = ensure_device()) return st;
     return launch_moe(h, T, H, rw, rb, E, k, gu, dn, out, topk_idx, topk_w, ws, (hipStream_t)stream);
 }

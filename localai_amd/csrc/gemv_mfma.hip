@@ -1,48 +1,14 @@
-// Decode matvec on MFMA for Q4_K and Q6_K: y[r] = sum_c W[r, c] * x[c].
-//
-// Weights come from a second device form of the matrix, the "tile form": rows
-// in tiles of 16, and per (tile, super-block) one block whose quant bytes are
-// stored so that each 16-byte lane slice is directly the B operand of
-// v_mfma_i32_16x16x64_i8 (lane l: column n = l % 16, k = 16 (l / 16) .. + 15,
-// bytes in k order). Lane L = n + 16c of a block holds row n's bytes
-// 8c .. 8c + 7 of two 32-byte quant chunks, so every load instruction of a
-// wave reads 1 KiB contiguous.
-//
-// Arithmetic, per (tile, super-block):
-//   B = the quants as unsigned bytes (Q4_K: a nibble, 0..15, masked in place;
-//       Q6_K: low nibble | high 2 bits << 4, 0..63), four MFMAs of 64 values
-//   A = x as three int8 pieces per value: with 2^s chosen per scale group so
-//       that max |x| 2^s lies in [32, 64),
-//         x 2^s = p0 + p1 / 128 + p2 / 16384 + e,  |e| <= 2^-15,
-//       each piece rounded with the 1.5 * 2^23 magic-number add (exact steps).
-//       A row m = 4 slot + piece carries one scale group in its k range and
-//       zero elsewhere (block diagonal), so D[4 slot + piece][n] is the exact
-//       integer dot product of that group's quants with one piece.
-//   The lane holding D rows 4q .. 4q + 2 of column n then forms
-//     sum_group q x = 2^-s (D0 + D1 / 128 + D2 / 16384)
-//   and applies the group's scales -- the factorisation of
-//   engine/native_quant.cpp:183-231 (Q4_K) and :298-341 (Q6_K) without
-//   quantising x (relative error of x about 1e-6 of the group maximum).
-//
-// x staging: each wave converts the x values of its super-blocks into
-// [group][piece][k / 8][8 bytes] in its own LDS region plus per-group
-// (sum of x, 2^-s); each lane reads the 8 bytes of its (row, k) slice and
-// places them in the low or high half of its A register with an AND mask.
-#include "gemv_core.h"
+// Decode matvec on i8 MFMA over the tile form of Q4_K / Q6_K matrices:
+// y[r] = sum_c W[r, c] * x[c]. The tile form, the arithmetic and the
+// building blocks are described in mfma_core.h; this file holds the repack
+// into the tile form, the matvec kernels (one matrix, or several matrices
+// with one x in a single launch) and their launch plan.
+#include "mfma_core.h"
 #include "internal.h"
 
 namespace lq {
 
-typedef int mt_i4 __attribute__((ext_vector_type(4)));
-
-constexpr int MT_ROWS = 16;
 constexpr int MT_MAX_JOBS = 8;        // matrices per fused launch (localai_hip_matvec_many)
-constexpr int MT_Q4K_BLOCK = 2304;
-constexpr int MT_Q6K_BLOCK = 3360;     // ql 2 x 1 KiB, qh 1 KiB, scales 16 x 16 B, d 16 x 2 B
-constexpr int MT_XBYTES = 1024 + 64;   // Q4_K per super-block: x pieces + 8 x (group sum, 2^-s)
-constexpr int MT6_XBYTES = 1024 + 128; // Q6_K per super-block: x pieces + 16 x (sub-block sum, 2^-s)
-
-__host__ __device__ constexpr int mt_block_bytes(int t) { return t == LQ_Q4_K ? MT_Q4K_BLOCK : MT_Q6K_BLOCK; }
 
 // 0 when the matrix gets no tile form (other types, or K beyond the 72
 // super-blocks the launch plan covers): its matvecs then run on gemv.hip.
@@ -120,321 +86,36 @@ int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_
     return LOCALAI_OK;
 }
 
-// Value of lane l ^ 1 (quad_perm [1,0,3,2], 0xB1), l ^ 2 (quad_perm [2,3,0,1],
-// 0x4E) or 7 - l inside each 8 (row_half_mirror, 0x141): DPP moves used for
-// sums / maxima over aligned groups of 4 or 8 lanes without an LDS round trip.
-template <int CTRL>
-__device__ __forceinline__ float mt_dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-constexpr float MT_MAGIC = 12582912.0f;   // 1.5 * 2^23: x + MAGIC holds rint(x) in its low mantissa bits
-
-// Three int8 pieces of a = x 2^s (|a| < 64) as the low bytes of t0, t1, t2:
-// a = p0 + p1 / 128 + p2 / 16384 + e. Every step is exact except the three
-// roundings to integers (fma of exactly representable terms, products by
-// powers of two, differences of nearby numbers).
-__device__ __forceinline__ void mt_split(float x, float S, float S128, uint32_t &b0, uint32_t &b1,
-                                         uint32_t &b2) {
-    const float t0 = __builtin_fmaf(x, S, MT_MAGIC);
-    const float r1 = __builtin_fmaf(x, S128, __builtin_fmaf(-128.0f, t0, 128.0f * MT_MAGIC));
-    const float t1 = r1 + MT_MAGIC;
-    const float r2 = __builtin_fmaf(r1, 128.0f, __builtin_fmaf(-128.0f, t1, 128.0f * MT_MAGIC));
-    const float t2 = r2 + MT_MAGIC;
-    b0 = __builtin_bit_cast(uint32_t, t0);
-    b1 = __builtin_bit_cast(uint32_t, t1);
-    b2 = __builtin_bit_cast(uint32_t, t2);
-}
-
-// Low bytes of four words packed into one (byte i from word i). v_perm_b32:
-// selector bytes 0..3 pick bytes of the second operand, 4..7 of the first,
-// 0x0C gives zero.
-__device__ __forceinline__ uint32_t mt_pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x0C0C0400u);
-    const uint32_t hi = __builtin_amdgcn_perm(d, c, 0x0C0C0400u);
-    return lo | (hi << 16);
-}
-
-// Scale exponent s for a group maximum m: m 2^s in [32, 64); 0 for zero,
-// infinite or NaN maxima; clamped so 2^s, 2^(s+7) and 2^-s stay normal.
-__device__ __forceinline__ int mt_group_shift(float gmax) {
-    int sh = 0;
-    if (gmax > 0.0f && gmax <= 3.4e38f) {
-        int e;
-        frexpf(gmax, &e);
-        sh = 6 - e;
-        sh = sh > 118 ? 118 : sh < -120 ? -120 : sh;
-    }
-    return sh;
-}
-
-// Convert four x values (natural positions 4 lane .. + 3 of a super-block)
-// into pieces and store them; returns (sum, 2^-s) of the lane's group.
-template <int GL>   // lanes per scale group: 8 (32 values) or 4 (16 values)
-__device__ __forceinline__ float2 mt_stage_x(float4 v, uint8_t *dst, int stride_piece) {
-    float gs = (v.x + v.y) + (v.z + v.w);
-    float gm = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    gs += mt_dpp<0xB1>(gs);
-    gm = fmaxf(gm, mt_dpp<0xB1>(gm));
-    gs += mt_dpp<0x4E>(gs);
-    gm = fmaxf(gm, mt_dpp<0x4E>(gm));
-    if (GL == 8) {
-        gs += mt_dpp<0x141>(gs);
-        gm = fmaxf(gm, mt_dpp<0x141>(gm));
-    }
-    const int sh = mt_group_shift(gm);
-    const float S = ldexpf(1.0f, sh), S128 = ldexpf(1.0f, sh + 7);
-    uint32_t a0, a1, a2, b0, b1, b2, c0, c1, c2, d0, d1, d2;
-    mt_split(v.x, S, S128, a0, a1, a2);
-    mt_split(v.y, S, S128, b0, b1, b2);
-    mt_split(v.z, S, S128, c0, c1, c2);
-    mt_split(v.w, S, S128, d0, d1, d2);
-    *reinterpret_cast<uint32_t *>(dst) = mt_pack4(a0, b0, c0, d0);
-    *reinterpret_cast<uint32_t *>(dst + stride_piece) = mt_pack4(a1, b1, c1, d1);
-    *reinterpret_cast<uint32_t *>(dst + 2 * stride_piece) = mt_pack4(a2, b2, c2, d2);
-    return make_float2(gs, ldexpf(1.0f, -sh));
-}
-
-// A operand: the lane's 8 bytes in the low (mlo) or high (mhi) half, or zero
-__device__ __forceinline__ mt_i4 mt_place(uint2 r, uint32_t mlo, uint32_t mhi) {
-    return mt_i4{(int)(r.x & mlo), (int)(r.y & mlo), (int)(r.x & mhi), (int)(r.y & mhi)};
-}
-
-// sum over the group of q x from D rows (piece 0, 1, 2), before 2^-s
-__device__ __forceinline__ float mt_pieces(mt_i4 D) {
-    return __builtin_fmaf((float)D[2], 0x1p-14f, __builtin_fmaf((float)D[1], 0x1p-7f, (float)D[0]));
-}
-
-__device__ __forceinline__ mt_i4 mt_as_i4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    return mt_i4{(int)a, (int)b, (int)c, (int)d};
-}
-
-// Shared loads of both kernels: x of the wave's super-blocks, then the tile
-// blocks. Every load is unconditional (clamped indices) so they all issue
-// before the first use.
-#define MT_PROLOGUE(XBYTES)                                                                   \
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];                            \
-    const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;                          \
-    const int sb0 = w * SPW;                                                                  \
-    int nsb = nb - sb0;                                                                       \
-    nsb = nsb < 0 ? 0 : nsb > SPW ? SPW : nsb;                                                \
-    uint8_t *wl = smem + w * SPW * (XBYTES);                                                  \
-    float *red = reinterpret_cast<float *>(smem + nw * SPW * (XBYTES));                       \
-    const int64_t tile0 = blk * RT;                                                           \
-    float4 xv[SPW];                                                                           \
-    _Pragma("unroll") for (int k = 0; k < SPW; ++k) {                                         \
-        const int sb = sb0 + k < nb ? sb0 + k : nb - 1;                                       \
-        xv[k] = *reinterpret_cast<const float4 *>(x + 256 * (int64_t)sb + 4 * lane);          \
-    }
-
-// Cross-wave and cross-lane-group sum of acc[RT] into y
-#define MT_EPILOGUE                                                                           \
-    _Pragma("unroll") for (int t = 0; t < RT; ++t) red[(w * RT + t) * 64 + lane] = acc[t];   \
-    __syncthreads();                                                                          \
-    const int i = threadIdx.x;                                                                \
-    if (i < RT * 16) {                                                                        \
-        const int t = i >> 4, n = i & 15;                                                     \
-        float s = 0.0f;                                                                       \
-        for (int k = 0; k < nw; ++k) {                                                        \
-            const float *r = red + (k * RT + t) * 64 + n;                                     \
-            s += (r[0] + r[16]) + (r[32] + r[48]);                                            \
-        }                                                                                     \
-        const int64_t row = (tile0 + t) * MT_ROWS + n;                                        \
-        if (tile0 + t < tiles && row < rows) y[row] = s;                                      \
-    }
-
-// ------------------------------------------------------------------- Q4_K
-// MFMA t of a super-block takes qs piece t / 2, nibble t % 2: bytes 0..7 of
-// lane group q are values 8q .. 8q + 7 of group gA(t), bytes 8..15 those of
-// group gB(t) = gA(t) + 2, with gA = 0, 1, 4, 5. MFMAs 0, 1 accumulate into D0
-// and 2, 3 into D1; MFMA t uses A slots 2 (t % 2) (group gA) and
-// 2 (t % 2) + 1 (group gB), so D lane group q ends with group
-// (q / 2) + 2 (q % 2) (+ 4 for D1).
-// LDS per super-block: pieces [group 8][piece 4][k / 8: 4][8 B] (1 KiB), then
-// (sum, 2^-s) per group.
-template <int SPW, int RT>
-__device__ __forceinline__ void mt_body_q4k(const uint8_t *__restrict__ Wt, int64_t rows, int nb, int64_t tiles,
-                                            const float *__restrict__ x, float *__restrict__ y, int64_t blk) {
-    MT_PROLOGUE(MT_XBYTES)
-    uint4 q0[RT][SPW], q1[RT][SPW], hd[RT][SPW];
+// RT row tiles of one matrix, workgroup index blk within the matrix
+template <int TYPE, int SPW, int RT>
+__device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
+                                                int64_t tiles, const float *__restrict__ x,
+                                                float *__restrict__ y, int64_t blk) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    float4 xv[1][SPW];
+    mt_load_x<SPW>(xv[0], x, nb, sb0, lane);   // x first: it is consumed first
+    MtW<TYPE> w[RT][SPW];
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-        const int64_t tile = tile0 + t < tiles ? tile0 + t : tiles - 1;
-#pragma unroll
-        for (int k = 0; k < SPW; ++k) {
-            const int kk = k < nsb ? k : 0;
-            const int sb = sb0 + kk < nb ? sb0 + kk : nb - 1;
-            const uint8_t *blk = Wt + (tile * nb + sb) * MT_Q4K_BLOCK;
-            q0[t][k] = ld16(blk + 16 * lane);
-            q1[t][k] = ld16(blk + 1024 + 16 * lane);
-            hd[t][k] = ld16(blk + 2048 + 16 * (lane & 15));
-        }
+        const int64_t tile = blk * RT + t < tiles ? blk * RT + t : tiles - 1;
+        mt_load_tile<TYPE, SPW>(w[t], Wt + tile * nb * mt_block_bytes(TYPE), nb, sb0, nsb, lane);
     }
     __builtin_amdgcn_sched_barrier(0);
-
-    {   // lane l: values 4l .. 4l + 3 = group l / 8, k / 8 = (l % 8) / 2, byte 4 (l % 2)
-        const int g = lane >> 3;
-#pragma unroll
-        for (int k = 0; k < SPW; ++k) {
-            uint8_t *frag = wl + k * MT_XBYTES;
-            const float2 gd = mt_stage_x<8>(xv[k], frag + g * 128 + ((lane & 7) >> 1) * 8 + 4 * (lane & 1), 32);
-            if ((lane & 7) == 0) reinterpret_cast<float2 *>(frag + 1024)[g] = gd;
-        }
+    float *fin;
+    mt_pass<TYPE, SPW, RT, 1>(w, xv, nsb, smem, fin);
+    const int i = threadIdx.x;
+    if (i < RT * 16) {
+        const int64_t tile = blk * RT + (i >> 4), row = tile * MT_ROWS + (i & 15);
+        if (tile < tiles && row < rows) y[row] = fin[i];
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-
-    const int m = lane & 15, q = lane >> 4, slot = m >> 2, pc = m & 3;
-    const int ga = (slot >> 1) + 2 * (slot & 1);   // A: group of this lane's row in MFMAs t = slot / 2, + 2
-    const int gd = (q >> 1) + 2 * (q & 1);         // D: group of this lane's rows in D0 (D1: + 4)
-    const uint32_t on = pc < 3 ? ~0u : 0u;
-    const uint32_t mlo = (slot & 1) ? 0u : on, mhi = (slot & 1) ? on : 0u;
-    const uint32_t ev = (slot >> 1) ? 0u : ~0u, od = ~ev;
-    const int aoff = ga * 128 + pc * 32 + q * 8;
-    float acc[RT];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) acc[t] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < SPW; ++k) {
-        if (k >= nsb) break;
-        const uint8_t *frag = wl + k * MT_XBYTES;
-        const uint2 r0 = *reinterpret_cast<const uint2 *>(frag + aoff);
-        const uint2 r1 = *reinterpret_cast<const uint2 *>(frag + aoff + 512);
-        const mt_i4 A0 = mt_place(r0, mlo & ev, mhi & ev), A1 = mt_place(r0, mlo & od, mhi & od);
-        const mt_i4 A2 = mt_place(r1, mlo & ev, mhi & ev), A3 = mt_place(r1, mlo & od, mhi & od);
-        const float2 x0 = reinterpret_cast<const float2 *>(frag + 1024)[gd];
-        const float2 x1 = reinterpret_cast<const float2 *>(frag + 1024)[gd + 4];
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            const uint4 a = q0[t][k], b = q1[t][k];
-            const uint32_t M = 0x0F0F0F0Fu;
-            mt_i4 D0 = mt_i4{0, 0, 0, 0}, D1 = mt_i4{0, 0, 0, 0};
-            D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, mt_as_i4(a.x & M, a.y & M, a.z & M, a.w & M), D0, 0, 0, 0);
-            D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                A1, mt_as_i4((a.x >> 4) & M, (a.y >> 4) & M, (a.z >> 4) & M, (a.w >> 4) & M), D0, 0, 0, 0);
-            D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, mt_as_i4(b.x & M, b.y & M, b.z & M, b.w & M), D1, 0, 0, 0);
-            D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                A3, mt_as_i4((b.x >> 4) & M, (b.y >> 4) & M, (b.z >> 4) & M, (b.w >> 4) & M), D1, 0, 0, 0);
-            // 6-bit scale / min of groups gd (< 4) and gd + 4 (engine/dequant.py:107-113)
-            const uint4 h = hd[t][k];
-            const uint32_t s0 = __builtin_amdgcn_ubfe(h.y, 8 * gd, 8);
-            const uint32_t s4 = __builtin_amdgcn_ubfe(h.z, 8 * gd, 8);
-            const uint32_t s8 = __builtin_amdgcn_ubfe(h.w, 8 * gd, 8);
-            const float sc0 = (float)(s0 & 63u), mn0 = (float)(s4 & 63u);
-            const float sc1 = (float)((s8 & 15u) | ((s0 >> 6) << 4)), mn1 = (float)((s8 >> 4) | ((s4 >> 6) << 4));
-            const float d = f16_to_f32(h.x), dmin = f16_to_f32(h.x >> 16);
-            const float v = __builtin_fmaf(sc1 * x1.y, mt_pieces(D1), sc0 * x0.y * mt_pieces(D0));
-            const float u = __builtin_fmaf(mn1, x1.x, mn0 * x0.x);
-            acc[t] = __builtin_fmaf(-dmin, u, __builtin_fmaf(d, v, acc[t]));
-        }
-    }
-    MT_EPILOGUE
 }
 
-// ------------------------------------------------------------------- Q6_K
-// MFMA i of a super-block covers values 64 i .. 64 i + 63 (half i / 2, ql
-// nibble i % 2): bytes 0..7 of lane group q are sub-block 4i + q / 2, values
-// 8 (q % 2) + 0..7, and bytes 8..15 sub-block 4i + 2 + q / 2. Quants are
-// q = (ql >> 4 (i % 2)) & 15 | ((qh >> 2 j) & 3) << 4 (engine/dequant.py:146-165),
-// unsigned; the -32 offset goes through the sub-block sums of x. Each MFMA
-// has its own D; A slot = sub-block 4i + slot, so D lane group q holds
-// sub-block 4i + q.
-// LDS per super-block: pieces [sub-block 16][piece 4][k / 8: 2][8 B] (1 KiB),
-// then (sum, 2^-s) per sub-block.
-template <int SPW, int RT>
-__device__ __forceinline__ void mt_body_q6k(const uint8_t *__restrict__ Wt, int64_t rows, int nb, int64_t tiles,
-                                            const float *__restrict__ x, float *__restrict__ y, int64_t blk) {
-    MT_PROLOGUE(MT6_XBYTES)
-    uint4 ql0[RT][SPW], ql1[RT][SPW], qh[RT][SPW], sc[RT][SPW];
-    uint32_t dd[RT][SPW];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        const int64_t tile = tile0 + t < tiles ? tile0 + t : tiles - 1;
-#pragma unroll
-        for (int k = 0; k < SPW; ++k) {
-            const int kk = k < nsb ? k : 0;
-            const int sb = sb0 + kk < nb ? sb0 + kk : nb - 1;
-            const uint8_t *blk = Wt + (tile * nb + sb) * MT_Q6K_BLOCK;
-            ql0[t][k] = ld16(blk + 16 * lane);
-            ql1[t][k] = ld16(blk + 1024 + 16 * lane);
-            qh[t][k] = ld16(blk + 2048 + 16 * lane);
-            sc[t][k] = ld16(blk + 3072 + 16 * (lane & 15));
-            dd[t][k] = *reinterpret_cast<const uint16_t *>(blk + 3328 + 2 * (lane & 15));
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    {   // lane l: values 4l .. 4l + 3 = sub-block l / 4, k / 8 = (l % 4) / 2, byte 4 (l % 2)
-        const int j = lane >> 2;
-#pragma unroll
-        for (int k = 0; k < SPW; ++k) {
-            uint8_t *frag = wl + k * MT6_XBYTES;
-            const float2 gd = mt_stage_x<4>(xv[k], frag + j * 64 + ((lane & 3) >> 1) * 8 + 4 * (lane & 1), 16);
-            if ((lane & 3) == 0) reinterpret_cast<float2 *>(frag + 1024)[j] = gd;
-        }
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-
-    const int m = lane & 15, q = lane >> 4, slot = m >> 2, pc = m & 3;
-    const uint32_t on = (pc < 3 && (slot & 1) == (q >> 1)) ? ~0u : 0u;
-    const uint32_t mlo = (slot >> 1) ? 0u : on, mhi = (slot >> 1) ? on : 0u;
-    const int aoff = slot * 64 + pc * 16 + (q & 1) * 8;
-    float acc[RT];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) acc[t] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < SPW; ++k) {
-        if (k >= nsb) break;
-        const uint8_t *frag = wl + k * MT6_XBYTES;
-        mt_i4 A[4];
-        float2 xg[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            A[i] = mt_place(*reinterpret_cast<const uint2 *>(frag + aoff + 256 * i), mlo, mhi);
-            xg[i] = reinterpret_cast<const float2 *>(frag + 1024)[4 * i + q];
-        }
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            const uint32_t L = 0x0F0F0F0Fu;
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint4 l = (i >> 1) ? ql1[t][k] : ql0[t][k];
-                const uint32_t e0 = (i >> 1) ? qh[t][k].z : qh[t][k].x;
-                const uint32_t e1 = (i >> 1) ? qh[t][k].w : qh[t][k].y;
-                mt_i4 B;
-                if (i & 1)
-                    B = mt_as_i4(((l.x >> 4) & L) | (e0 & 0x30303030u), ((l.y >> 4) & L) | (e1 & 0x30303030u),
-                                 ((l.z >> 4) & L) | ((e0 >> 2) & 0x30303030u),
-                                 ((l.w >> 4) & L) | ((e1 >> 2) & 0x30303030u));
-                else
-                    B = mt_as_i4((l.x & L) | ((e0 << 4) & 0x30303030u), (l.y & L) | ((e1 << 4) & 0x30303030u),
-                                 (l.z & L) | ((e0 << 2) & 0x30303030u), (l.w & L) | ((e1 << 2) & 0x30303030u));
-                const mt_i4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], B, mt_i4{0, 0, 0, 0}, 0, 0, 0);
-                const uint32_t sw = i == 0 ? sc[t][k].x : i == 1 ? sc[t][k].y : i == 2 ? sc[t][k].z : sc[t][k].w;
-                const float scf = (float)(int)__builtin_amdgcn_sbfe((int)sw, 8 * q, 8);   // the builtin returns unsigned
-                s = __builtin_fmaf(scf, __builtin_fmaf(mt_pieces(D), xg[i].y, -32.0f * xg[i].x), s);
-            }
-            acc[t] = __builtin_fmaf(f16_to_f32(dd[t][k]), s, acc[t]);
-        }
-    }
-    MT_EPILOGUE
-}
-
-#undef MT_PROLOGUE
-#undef MT_EPILOGUE
-
-// One matrix: workgroup b takes row tiles b RT .. b RT + RT - 1.
-template <int SPW, int RT, int MAXT>
-__global__ __launch_bounds__(MAXT) void gemv_mfma_q4k(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
-                                                      int64_t tiles, const float *__restrict__ x,
-                                                      float *__restrict__ y) {
-    mt_body_q4k<SPW, RT>(Wt, rows, nb, tiles, x, y, blockIdx.x);
-}
-template <int SPW, int RT, int MAXT>
-__global__ __launch_bounds__(MAXT) void gemv_mfma_q6k(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
-                                                      int64_t tiles, const float *__restrict__ x,
-                                                      float *__restrict__ y) {
-    mt_body_q6k<SPW, RT>(Wt, rows, nb, tiles, x, y, blockIdx.x);
+template <int TYPE, int SPW, int RT, int MAXT>
+__global__ __launch_bounds__(MAXT) void gemv_mfma(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
+                                                  int64_t tiles, const float *__restrict__ x,
+                                                  float *__restrict__ y) {
+    mt_matvec_block<TYPE, SPW, RT>(Wt, rows, nb, tiles, x, y, blockIdx.x);
 }
 
 // Several matrices with the same K and the same x in one launch: job j owns
@@ -455,8 +136,10 @@ __global__ __launch_bounds__(MAXT) void gemv_mfma_many(MtJobs jobs, int nb, cons
     for (int i = 1; i < MT_MAX_JOBS; ++i)
         if (i < jobs.n && b >= jobs.blk0[i]) j = i;
     const int64_t tiles = (jobs.rows[j] + MT_ROWS - 1) / MT_ROWS;
-    if (jobs.type[j] == LQ_Q6_K) mt_body_q6k<SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
-    else mt_body_q4k<SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
+    if (jobs.type[j] == LQ_Q6_K)
+        mt_matvec_block<LQ_Q6_K, SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
+    else
+        mt_matvec_block<LQ_Q4_K, SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
 }
 
 // Launch plan: the waves of a workgroup split the super-blocks of one row
@@ -498,11 +181,11 @@ int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, floa
     const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
     const MtPlan p = mt_plan(nb, tiles);
     dim3 grid((unsigned)((tiles + p.rt - 1) / p.rt)), block(64 * p.waves);
-    const size_t lds = (size_t)p.waves * p.spw * (q6 ? MT6_XBYTES : MT_XBYTES) + (size_t)p.waves * p.rt * 64 * 4;
-#define MT_L(S, R, M)                                                                                     \
-    do {                                                                                                  \
-        if (q6) hipLaunchKernelGGL((gemv_mfma_q6k<S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y); \
-        else hipLaunchKernelGGL((gemv_mfma_q4k<S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y);    \
+    const size_t lds = mt_lds_bytes(g.type, p.waves, p.spw, 1, p.rt);
+#define MT_L(S, R, M)                                                                                           \
+    do {                                                                                                        \
+        if (q6) hipLaunchKernelGGL((gemv_mfma<LQ_Q6_K, S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y); \
+        else hipLaunchKernelGGL((gemv_mfma<LQ_Q4_K, S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y);    \
     } while (0)
     MT_DISPATCH(MT_L)
 #undef MT_L
@@ -538,7 +221,7 @@ int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const
     }
     for (int j = n; j <= MT_MAX_JOBS; ++j) jobs.blk0[j] = b;
     dim3 grid((unsigned)b), block(64 * p.waves);
-    const size_t lds = (size_t)p.waves * p.spw * (any_q6 ? MT6_XBYTES : MT_XBYTES) + (size_t)p.waves * p.rt * 64 * 4;
+    const size_t lds = mt_lds_bytes(any_q6 ? LQ_Q6_K : LQ_Q4_K, p.waves, p.spw, 1, p.rt);
 #define MT_L(S, R, M) hipLaunchKernelGGL((gemv_mfma_many<S, R, M>), grid, block, lds, s, jobs, nb, x)
     MT_DISPATCH(MT_L)
 #undef MT_L

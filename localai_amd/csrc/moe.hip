@@ -10,7 +10,8 @@
 //   silu(g)      = g / (1 + exp(-clip(g, -80, 80)))  (engine/zaya.py:305)
 //
 // Kernels (one stream, in order):
-//   route     one workgroup per token: router logits, top-k, gates
+//   route     one workgroup per token: router logits, top-k, gates (for a
+//             single token also the permutation tables below)
 //   permute   one workgroup: expert histogram, exclusive scan, stable
 //             expert-major permutation of the T*k assignments (LDS)
 //   gate_up   grouped matvec over the active experts, one workgroup per
@@ -19,12 +20,13 @@
 //   combine   gate-weighted sum of each token's k expert outputs (fixed order)
 //
 // Router logits are bit-reproducible: each is a sum of exact fp64 products
-// h*w in a fixed order (lane l sums elements l, l+64, ...; then a pairwise
-// tree over the 64 lanes), rounded to fp32 once.
+// h*w in a fixed order (lane l sums elements 256j + 4l + c, j-major; then a
+// pairwise tree over the 64 lanes), rounded to fp32 once.
 #include <math.h>
 
 #include "gemv_core.h"
 #include "internal.h"
+#include "mfma_core.h"
 
 namespace lq {
 
@@ -53,40 +55,80 @@ struct MoeTables {
 
 // ------------------------------------------------------------------ route
 
+// (logit desc, index asc); a NaN logit ranks below every number, NaNs by
+// index -- the order of np.lexsort((index, -logit)) (oracle/moe.py topk)
 __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
+    const bool na = va != va, nb = vb != vb;
+    if (na || nb) return nb && (!na || ia < ib);
     return va > vb || (va == vb && ia < ib);
 }
 
-__global__ __launch_bounds__(512) void moe_route_kernel(const float *__restrict__ h, int H,
-                                                        const float *__restrict__ rw,
-                                                        const float *__restrict__ rb, int E, int k,
-                                                        float *__restrict__ logits,
-                                                        int32_t *__restrict__ topk_idx,
-                                                        float *__restrict__ topk_w) {
-    extern __shared__ float lg[];          // E logits of this token
+// Widest hidden size whose fp64 copy of h is staged in LDS (64 KiB); wider
+// rows convert h in registers in every wave.
+constexpr int ROUTE_LDS_H = 8192;
+
+// One workgroup per token. h is converted to fp64 once (in LDS) and shared by
+// the waves, each of which computes whole expert logits; wave 0 then ranks
+// the experts. With `tables` (a single token) the workgroup also writes the
+// expert-major permutation tables of moe_permute_kernel for its k
+// assignments, so the layer needs no permute launch.
+// LDS: E logits, k selected experts (8-byte aligned), then h as fp64.
+template <bool LDS_H>
+__global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ h, int H,
+                                                         const float *__restrict__ rw,
+                                                         const float *__restrict__ rb, int E, int k,
+                                                         float *__restrict__ logits,
+                                                         int32_t *__restrict__ topk_idx,
+                                                         float *__restrict__ topk_w, MoeTables tb, int tables) {
+    extern __shared__ __attribute__((aligned(16))) float lg[];
+    int *sel = reinterpret_cast<int *>(lg + E);
+    double *h64 = reinterpret_cast<double *>(lg + ((E + k + 3) & ~3));
     const int t = blockIdx.x;
     const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
     const float *ht = h + (int64_t)t * H;
-    constexpr int CH = 16;                 // values per lane loaded ahead of the sums
+    constexpr bool lds_h = LDS_H;   // H <= ROUTE_LDS_H
+    if (lds_h) {
+        for (int i = threadIdx.x * 4; i < H; i += blockDim.x * 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(ht + i);
+            *reinterpret_cast<double2 *>(h64 + i) = make_double2(v.x, v.y);
+            *reinterpret_cast<double2 *>(h64 + i + 2) = make_double2(v.z, v.w);
+        }
+        __syncthreads();
+    }
+    constexpr int CH = 8;                  // 16-byte chunks per lane loaded ahead of the sums
     for (int e = w; e < E; e += nw) {
         const float *we = rw + (int64_t)e * H;
         double s = 0.0;
-        // lane l sums elements l, l + 64, l + 128, ... in that order (exact
-        // fp64 products); the loads of CH elements are issued before their sums
-        for (int i0 = 0; i0 < H; i0 += 64 * CH) {
-            float hv[CH], wv[CH];
+        // lane l sums elements 256j + 4l + c (j = 0, 1, ..., c = 0..3) in that
+        // order (exact fp64 products); H is a multiple of 4, so a chunk is
+        // either wholly inside the row or wholly past its end
+        for (int i0 = 0; i0 < H; i0 += 256 * CH) {
+            float4 hv[CH], wv[CH];
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
-                const int i = i0 + 64 * j + lane;
-                const int ic = i < H ? i : H - 1;      // unconditional loads: no wait per load
-                hv[j] = ht[ic];
-                wv[j] = we[ic];
+                const int i = i0 + 256 * j + 4 * lane;
+                const int ic = i < H ? i : H - 4;      // unconditional loads: no wait per load
+                wv[j] = *reinterpret_cast<const float4 *>(we + ic);
+                if (!lds_h) hv[j] = *reinterpret_cast<const float4 *>(ht + ic);
             }
+            __builtin_amdgcn_sched_barrier(0);   // every load issued before the first sum
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
-                // elements past H add an exact zero product
-                const double hj = i0 + 64 * j + lane < H ? (double)hv[j] : 0.0;
-                s = __builtin_fma(hj, (double)wv[j], s);
+                const int i = i0 + 256 * j + 4 * lane;
+                const bool in = i < H;           // chunks past H add exact zero products
+                double2 a, b;
+                if (lds_h) {
+                    const int ic = in ? i : 0;
+                    a = *reinterpret_cast<const double2 *>(h64 + ic);
+                    b = *reinterpret_cast<const double2 *>(h64 + ic + 2);
+                } else {
+                    a = make_double2(hv[j].x, hv[j].y);
+                    b = make_double2(hv[j].z, hv[j].w);
+                }
+                s = __builtin_fma(in ? a.x : 0.0, (double)wv[j].x, s);
+                s = __builtin_fma(in ? a.y : 0.0, (double)wv[j].y, s);
+                s = __builtin_fma(in ? b.x : 0.0, (double)wv[j].z, s);
+                s = __builtin_fma(in ? b.y : 0.0, (double)wv[j].w, s);
             }
         }
 #pragma unroll
@@ -100,33 +142,72 @@ __global__ __launch_bounds__(512) void moe_route_kernel(const float *__restrict_
     }
     __syncthreads();
     if (w != 0) return;
-    // lane l owns experts l, l+64, ...; bit j of `taken` marks expert l+64j as selected
-    uint32_t taken = 0;
     float myv = -INFINITY;
     int myi = 0;
-    for (int r = 0; r < k; ++r) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int e = lane, j = 0; e < E; e += 64, ++j)
-            if (!((taken >> j) & 1u) && better(lg[e], e, bv, bi)) { bv = lg[e]; bi = e; }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, 64);
-            const int oi = __shfl_xor(bi, off, 64);
-            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    if (E <= 64) {
+        // lane e ranks expert e against all E (values broadcast with
+        // readlane): rank = number of experts that beat it; the rank-r expert
+        // is choice r
+        const float v = lane < E ? lg[lane] : 0.0f;
+        int rank = 0;
+        for (int j = 0; j < E; ++j)
+            rank += better(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j)), j,
+                           v, lane);
+        if (lane < E && rank < k) sel[rank] = lane;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (lane < k) {
+            myi = sel[lane];
+            myv = lg[myi];
         }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == r) { myv = bv; myi = bi; }
-    }
-    const float vmax = __shfl(myv, 0, 64);
-    const float ex = lane < k ? expf(myv - vmax) : 0.0f;
-    float z = ex;
+    } else {
+        // lane l owns experts l, l+64, ...; bit j of `taken` marks expert l+64j as selected
+        uint32_t taken = 0;
+        for (int r = 0; r < k; ++r) {
+            float bv = __builtin_nanf("");   // ranks below every expert
+            int bi = 0x7fffffff;
+            for (int e = lane, j = 0; e < E; e += 64, ++j)
+                if (!((taken >> j) & 1u) && better(lg[e], e, bv, bi)) { bv = lg[e]; bi = e; }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) z += __shfl_xor(z, off, 64);
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, 64);
+                const int oi = __shfl_xor(bi, off, 64);
+                if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+            }
+            if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+            if (lane == r) { myv = bv; myi = bi; }
+        }
+    }
+    // gates: softmax over the k selected logits, normaliser summed in choice order
+    const float vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, myv), 0));
+    const float ex = lane < k ? expf(myv - vmax) : 0.0f;
+    float z = 0.0f;
+    for (int j = 0; j < k; ++j) z += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), j));
     if (lane < k) {
         topk_idx[(int64_t)t * k + lane] = myi;
         topk_w[(int64_t)t * k + lane] = ex / z;
     }
+    if (!tables) return;
+    // one token: assignment a = lane (< k) has the distinct expert myi; its
+    // position in expert-major order is the number of selected experts below it
+    int rank = 0;
+    for (int j = 0; j < k; ++j) rank += lane < k && __builtin_amdgcn_readlane(myi, j) < myi;
+    if (lane < k) {
+        tb.perm[rank] = lane;
+        tb.pos[lane] = rank;
+        tb.active[rank] = myi;
+    }
+    for (int e = lane; e <= E; e += 64) {
+        int below = 0, hit = 0;
+        for (int j = 0; j < k; ++j) {
+            const int ej = __builtin_amdgcn_readlane(myi, j);
+            below += ej < e;
+            hit |= ej == e;
+        }
+        tb.offsets[e] = below;
+        if (e < E) tb.counts[e] = hit;
+    }
+    if (lane == 0) tb.n_active[0] = k;
 }
 
 // ---------------------------------------------------------------- permute
@@ -271,6 +352,155 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(const uint8_t *__restr
     }
 }
 
+// -------------------------------------------- grouped matvec on i8 MFMA
+// Decode path for expert tensors that have the tile form (Q4_K / Q6_K,
+// mfma_core.h). A workgroup loads its weight tiles once and walks the tokens
+// routed to its expert, restaging x per token.
+
+// gate_up: workgroup (i, slot) = gate tile i (rows 16i ..) and up tile
+// inter / 16 + i of the slot's expert; act[p, 16i + n] = silu(g) * u
+// (engine/zaya.py:303-306) for every perm position p of the expert.
+// `single` (one token): slot = assignment a, expert topk_idx[a], act row a --
+// the weights are requested after one dependent load.
+template <int TYPE, int SPW, int MAXT>
+__global__ __launch_bounds__(MAXT) void moe_mfma_gate_up(const uint8_t *__restrict__ Wt, int64_t mat_bytes, int nb,
+                                                         int64_t inter, MoeTables tb, const float *__restrict__ h,
+                                                         int64_t H, int k, const int32_t *__restrict__ topk_idx,
+                                                         int single, float *__restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int slot = blockIdx.y;
+    int e;
+    if (single) {
+        e = topk_idx[slot];
+        if (slot == 0) {   // clear the token's output for moe_mfma_down_single
+            const int64_t per = (H + gridDim.x - 1) / gridDim.x;
+            for (int64_t c = blockIdx.x * per + threadIdx.x; c < (blockIdx.x + 1) * per && c < H; c += blockDim.x)
+                out[c] = 0.0f;
+        }
+    } else {
+        if (slot >= tb.n_active[0]) return;
+        e = tb.active[slot];
+    }
+    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    const int64_t i = blockIdx.x, tile_bytes = (int64_t)nb * mt_block_bytes(TYPE);
+    const uint8_t *We = Wt + (int64_t)e * mat_bytes;
+    MtW<TYPE> w[2][SPW];
+    mt_load_tile<TYPE, SPW>(w[0], We + i * tile_bytes, nb, sb0, nsb, lane);
+    mt_load_tile<TYPE, SPW>(w[1], We + (inter / MT_ROWS + i) * tile_bytes, nb, sb0, nsb, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    // the expert's tokens; each next token's row is requested before the
+    // current token's arithmetic
+    const int n = single ? 1 : tb.counts[e], base = single ? slot : tb.offsets[e];
+    const int tok0 = single ? 0 : tb.perm[base] / k;
+    float4 xv[1][SPW];
+    mt_load_x<SPW>(xv[0], h + (int64_t)tok0 * H, nb, sb0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int j = 0; j < n; ++j) {
+        const int p = base + j;
+        float4 xn[1][SPW];
+        if (j + 1 < n) mt_load_x<SPW>(xn[0], h + (int64_t)(tb.perm[p + 1] / k) * H, nb, sb0, lane);
+        float *fin;
+        mt_pass<TYPE, SPW, 2, 1>(w, xv, nsb, smem, fin);
+        const int r = threadIdx.x;
+        if (r < MT_ROWS) tb.act[(int64_t)p * inter + i * MT_ROWS + r] = silu(fin[r]) * fin[MT_ROWS + r];
+        if (j + 1 < n) {
+#pragma unroll
+            for (int kk = 0; kk < SPW; ++kk) xv[0][kk] = xn[0][kk];
+        }
+    }
+}
+
+// down: workgroup (i, slot) = hidden tile i of the slot's expert;
+// ysl[p, 16i + n] for every perm position p of the expert
+template <int TYPE, int SPW, int MAXT>
+__global__ __launch_bounds__(MAXT) void moe_mfma_down(const uint8_t *__restrict__ Wt, int64_t mat_bytes, int nb,
+                                                      int64_t hidden, MoeTables tb, int64_t inter) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int slot = blockIdx.y;
+    if (slot >= tb.n_active[0]) return;
+    const int e = tb.active[slot];
+    const int n = tb.counts[e], base = tb.offsets[e];
+    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    const int64_t i = blockIdx.x;
+    float4 xv[1][SPW];
+    mt_load_x<SPW>(xv[0], tb.act + (int64_t)base * inter, nb, sb0, lane);
+    MtW<TYPE> w[1][SPW];
+    mt_load_tile<TYPE, SPW>(w[0], Wt + (int64_t)e * mat_bytes + i * nb * mt_block_bytes(TYPE), nb, sb0, nsb, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int j = 0; j < n; ++j) {
+        const int p = base + j;
+        float4 xn[1][SPW];
+        if (j + 1 < n) mt_load_x<SPW>(xn[0], tb.act + (int64_t)(p + 1) * inter, nb, sb0, lane);
+        float *fin;
+        mt_pass<TYPE, SPW, 1, 1>(w, xv, nsb, smem, fin);
+        const int r = threadIdx.x;
+        if (r < MT_ROWS && i * MT_ROWS + r < hidden) tb.ysl[(int64_t)p * hidden + i * MT_ROWS + r] = fin[r];
+        if (j + 1 < n) {
+#pragma unroll
+            for (int kk = 0; kk < SPW; ++kk) xv[0][kk] = xn[0][kk];
+        }
+    }
+}
+
+// One token (decode), k <= 2: workgroup (i, s) = hidden tile i of expert
+// topk_idx[s]; out[16i + n] += topk_w[s] * y (out cleared by gate_up). Two
+// additions onto zero give the same sum in either order, so the result does
+// not depend on which workgroup lands first.
+template <int TYPE, int SPW, int MAXT>
+__global__ __launch_bounds__(MAXT) void moe_mfma_down_single(const uint8_t *__restrict__ Wt, int64_t mat_bytes,
+                                                             int nb, int64_t hidden, MoeTables tb, int64_t inter,
+                                                             const int32_t *__restrict__ topk_idx,
+                                                             const float *__restrict__ topk_w,
+                                                             float *__restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    const int64_t i = blockIdx.x;
+    const int s = blockIdx.y;
+    float4 xv[1][SPW];
+    mt_load_x<SPW>(xv[0], tb.act + (int64_t)s * inter, nb, sb0, lane);
+    MtW<TYPE> w[1][SPW];
+    mt_load_tile<TYPE, SPW>(w[0], Wt + (int64_t)topk_idx[s] * mat_bytes + i * nb * mt_block_bytes(TYPE), nb, sb0,
+                            nsb, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    float *fin;
+    mt_pass<TYPE, SPW, 1, 1>(w, xv, nsb, smem, fin);
+    const int r = threadIdx.x;
+    if (r < MT_ROWS && i * MT_ROWS + r < hidden) atomicAdd(out + i * MT_ROWS + r, topk_w[s] * fin[r]);
+}
+
+// One token (decode): hidden tile i of each of its K experts, with the gate
+// weighted sum of moe_combine_kernel in the epilogue (same order, same fma
+// chain, so the result equals down + combine). act rows are in assignment
+// order (gate_up `single`).
+template <int TYPE, int SPW, int K, int MAXT>
+__global__ __launch_bounds__(MAXT) void moe_mfma_down_combine(const uint8_t *__restrict__ Wt, int64_t mat_bytes,
+                                                              int nb, int64_t hidden, MoeTables tb, int64_t inter,
+                                                              const int32_t *__restrict__ topk_idx,
+                                                              const float *__restrict__ topk_w,
+                                                              float *__restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    const int64_t i = blockIdx.x;
+    float4 xv[K][SPW];
+    MtW<TYPE> w[K][SPW];
+#pragma unroll
+    for (int s = 0; s < K; ++s) mt_load_x<SPW>(xv[s], tb.act + (int64_t)s * inter, nb, sb0, lane);
+#pragma unroll
+    for (int s = 0; s < K; ++s)
+        mt_load_tile<TYPE, SPW>(w[s], Wt + (int64_t)topk_idx[s] * mat_bytes + i * nb * mt_block_bytes(TYPE), nb,
+                                sb0, nsb, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    float *fin;
+    mt_pass<TYPE, SPW, K, K>(w, xv, nsb, smem, fin);
+    const int r = threadIdx.x;
+    if (r < MT_ROWS && i * MT_ROWS + r < hidden) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int s = 0; s < K; ++s) acc = __builtin_fmaf(topk_w[s], fin[s * MT_ROWS + r], acc);
+        out[i * MT_ROWS + r] = acc;
+    }
+}
+
 // ---------------------------------------------------------------- combine
 
 // out[t, :] = sum_j topk_w[t, j] * ysl[pos[t*k + j], :], slots in top-k order
@@ -394,18 +624,74 @@ static int launch_grouped(const localai_qmat *m, const MoeTables &tb, const floa
     return LOCALAI_OK;
 }
 
+// MFMA decode path: both expert tensors in the tile form with K <= 32
+// super-blocks: one super-block per wave (up to 16 waves) for K <= 16
+// super-blocks, else four per wave (up to 8 waves, room for the registers).
+static bool moe_mfma_ok(const localai_qmat *gu, const localai_qmat *dn, const float *h, int64_t H, int64_t I) {
+    return gu->tiles && dn->tiles && gu->g.type == dn->g.type && gu->g.nb <= 32 && dn->g.nb <= 32 &&
+           (reinterpret_cast<uintptr_t>(h) & 15) == 0 && I % MT_ROWS == 0 && gu->g.cols == H && dn->g.cols == I;
+}
+
+template <int TYPE>
+static int launch_moe_mfma_t(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
+                             int64_t T, int64_t H, int64_t I, int k, int slots, const int32_t *topk_idx,
+                             const float *topk_w, float *out, bool fused_combine, hipStream_t s) {
+    {
+        const int nb = (int)gu->g.nb, spw = nb <= 16 ? 1 : 4, waves = (nb + spw - 1) / spw;
+        dim3 grid((unsigned)(I / MT_ROWS), slots), block(64 * waves);
+        const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 2);
+        const int single = fused_combine;   // one token: assignment-ordered act rows
+        if (spw == 1)
+            hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, 1, 1024>), grid, block, lds, s, gu->tiles, gu->tile_bytes, nb,
+                               I, tb, h, H, k, topk_idx, single, out);
+        else
+            hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, 4, 512>), grid, block, lds, s, gu->tiles, gu->tile_bytes, nb,
+                               I, tb, h, H, k, topk_idx, single, out);
+        LQ_HIP(hipGetLastError());
+    }
+    const int nb = (int)dn->g.nb, spw = nb <= 16 ? 1 : 4, waves = (nb + spw - 1) / spw;
+    const unsigned tiles = (unsigned)((H + MT_ROWS - 1) / MT_ROWS);
+    if (fused_combine) {
+        const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 1);
+        if (spw == 1)
+            hipLaunchKernelGGL((moe_mfma_down_single<TYPE, 1, 1024>), dim3(tiles, k), dim3(64 * waves), lds, s,
+                               dn->tiles, dn->tile_bytes, nb, H, tb, I, topk_idx, topk_w, out);
+        else
+            hipLaunchKernelGGL((moe_mfma_down_single<TYPE, 4, 512>), dim3(tiles, k), dim3(64 * waves), lds, s,
+                               dn->tiles, dn->tile_bytes, nb, H, tb, I, topk_idx, topk_w, out);
+    } else {
+        const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 1);
+        if (spw == 1)
+            hipLaunchKernelGGL((moe_mfma_down<TYPE, 1, 1024>), dim3(tiles, slots), dim3(64 * waves), lds, s,
+                               dn->tiles, dn->tile_bytes, nb, H, tb, I);
+        else
+            hipLaunchKernelGGL((moe_mfma_down<TYPE, 4, 512>), dim3(tiles, slots), dim3(64 * waves), lds, s,
+                               dn->tiles, dn->tile_bytes, nb, H, tb, I);
+    }
+    LQ_HIP(hipGetLastError());
+    return LOCALAI_OK;
+}
+
 int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const float *rb, int64_t E, int k,
                const localai_qmat *gu, const localai_qmat *dn, float *out, int32_t *topk_idx, float *topk_w,
                void *ws, hipStream_t s) {
     const int64_t I = gu->g.rows / 2;
     MoeTables tb = carve(ws, T, E, k, H, I);
-    size_t sh = (size_t)E * 4;
-    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)T), dim3(512), sh, s, h, (int)H, rw, rb, (int)E, k,
-                       tb.logits, topk_idx, topk_w);
+    const int64_t hpad = H <= ROUTE_LDS_H ? H : 0;   // fp64 copy of h in LDS
+    size_t sh = (size_t)((E + k + 3) & ~3) * 4 + (size_t)hpad * 8;
+    const int one = T == 1 && tb.tile_w == 0;   // single token: the router writes the tables
+    if (hpad)
+        hipLaunchKernelGGL(moe_route_kernel<true>, dim3((unsigned)T), dim3(1024), sh, s, h, (int)H, rw, rb, (int)E, k,
+                           tb.logits, topk_idx, topk_w, tb, one);
+    else
+        hipLaunchKernelGGL(moe_route_kernel<false>, dim3((unsigned)T), dim3(1024), sh, s, h, (int)H, rw, rb, (int)E,
+                           k, tb.logits, topk_idx, topk_w, tb, one);
     LQ_HIP(hipGetLastError());
-    size_t sh2 = (size_t)(34 * E + 1) * 4;
-    hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), sh2, s, topk_idx, (int)(T * k), (int)E, tb);
-    LQ_HIP(hipGetLastError());
+    if (!one) {
+        size_t sh2 = (size_t)(34 * E + 1) * 4;
+        hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), sh2, s, topk_idx, (int)(T * k), (int)E, tb);
+        LQ_HIP(hipGetLastError());
+    }
     const int slots = (int)(E < T * k ? E : T * k);
     if (tb.tile_w > 0) {
         // prefill: gathered f16 token rows -> expert GEMMs on MFMA
@@ -419,6 +705,13 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
         if (int st = launch_moe_gemm(dn->g, dn->data, false, tb.xh_dn, f16_stride(I), tb.inv_dn, tb.ysl, H, I,
                                      tb.tile_e, tb.tile_p0, tb.tile_n, tb.n_tiles, tb.max_tiles, s))
             return st;
+    } else if (moe_mfma_ok(gu, dn, h, H, I)) {
+        // decode on MFMA; one token with k <= 2 folds the combine into down
+        const bool fused = T == 1 && k <= 2;
+        const int st = gu->g.type == LQ_Q6_K
+                           ? launch_moe_mfma_t<LQ_Q6_K>(gu, dn, tb, h, T, H, I, k, slots, topk_idx, topk_w, out, fused, s)
+                           : launch_moe_mfma_t<LQ_Q4_K>(gu, dn, tb, h, T, H, I, k, slots, topk_idx, topk_w, out, fused, s);
+        if (st || fused) return st;
     } else {
         if (int st = launch_grouped<true>(gu, tb, h, H, k, slots, T, s)) return st;
         if (int st = launch_grouped<false>(dn, tb, tb.act, I, k, slots, T, s)) return st;

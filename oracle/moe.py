@@ -12,8 +12,8 @@ renormalised over the selected experts (softmax over the k selected logits),
 and a gate-weighted sum over the k experts.
 
 Routing is made bit-reproducible by a canonical router: each logit is a sum of
-exact fp64 products h*w in a fixed order (64 strided lane sums, then a pairwise
-tree over the lanes), rounded once to fp32. The ranking key is
+exact fp64 products h*w in a fixed order (64 lane sums over interleaved
+4-element chunks, then a pairwise tree over the lanes), rounded once to fp32. The ranking key is
 (logit descending, expert index ascending).
 
 parity unpinned by the reference (no top-k>1 MoE, no MoE test); the tests pin
@@ -33,25 +33,28 @@ LANES = 64
 def router_logits(h, w):
     """Canonical fp32 router logits [T, E] for h [T, H] and w [E, H] (both fp32).
 
-    Sum order: lane l (0..63) accumulates p[l], p[l+64], p[l+128], ... in fp64;
-    the 64 lane sums are then added pairwise s[l] += s[l + off] for
-    off = 32, 16, 8, 4, 2, 1; the result is rounded to fp32 once.
+    Sum order: lane l (0..63) accumulates, for j = 0, 1, ..., the exact fp64
+    products of elements 256 j + 4 l + c, c = 0, 1, 2, 3, in that order (one
+    16-byte load per lane and step); the 64 lane sums are then added pairwise
+    s[l] += s[l + off] for off = 32, 16, 8, 4, 2, 1; the result is rounded to
+    fp32 once.
     """
     h = np.asarray(h, dtype=np.float32)
     w = np.asarray(w, dtype=np.float32)
     T, H = h.shape
     E = w.shape[0]
-    pad = (-H) % LANES
+    pad = (-H) % (4 * LANES)
     hp = np.pad(h.astype(np.float64), ((0, 0), (0, pad)))
     wp = np.pad(w.astype(np.float64), ((0, 0), (0, pad)))
-    steps = hp.shape[1] // LANES
+    steps = hp.shape[1] // (4 * LANES)
     out = np.empty((T, E), dtype=np.float32)
     for t0 in range(0, T, 16):                                   # bound the fp64 temporaries
         prod = hp[t0:t0 + 16, None, :] * wp[None, :, :]          # exact products
-        prod = prod.reshape(prod.shape[0], E, steps, LANES)
+        prod = prod.reshape(prod.shape[0], E, steps, LANES, 4)
         acc = np.zeros((prod.shape[0], E, LANES), dtype=np.float64)
         for i in range(steps):                                   # sequential per lane
-            acc = acc + prod[:, :, i, :]
+            for c in range(4):
+                acc = acc + prod[:, :, i, :, c]
         off = LANES // 2
         while off:
             acc = acc[:, :, :off] + acc[:, :, off:2 * off]

@@ -2,8 +2,9 @@
 
 Routing indices must be identical (ties to the lower expert index); gates and
 outputs within max-rel 1e-3 (normwise). Below 32 tokens the layer runs the
-fp32 grouped matvec path, which lands near 1e-6; from 32 tokens on it runs
-the expert GEMM path (f16 MFMA operands, fp32 accumulation), near 2e-4."""
+grouped matvec path (i8 MFMA on three-piece x for Q4_K / Q6_K experts, fp32
+VALU otherwise), which lands near 1e-6; from 32 tokens on it runs the expert
+GEMM path (f16 MFMA operands, fp32 accumulation), near 2e-4."""
 import numpy as np
 import pytest
 
@@ -137,3 +138,24 @@ def test_zaya_expert_matvec_mixin():
         got = model._expert_matvec('blk.1.ffn_down_exps.weight', e, x)
         want = quant.matvec_exact(raw[e * per:(e + 1) * per], 14, rows, cols, x)
         assert normwise_rel(got, want) < 1e-5
+
+
+@pytest.mark.parametrize('t,k,H,I', [
+    (12, 1, 1024, 512),     # top-1: down + combine fused for one token
+    (12, 3, 1024, 512),     # top-3: grouped down, then the combine kernel
+    (14, 2, 4608, 256),     # gate_up K = 18 super-blocks: four per wave
+    (12, 2, 512, 4352),     # down K = 17 super-blocks: four per wave
+])
+@pytest.mark.parametrize('T', (1, 3))
+def test_mfma_decode_path_shapes(t, k, H, I, T):
+    """Decode (T < 32) with Q4_K / Q6_K experts runs the i8 MFMA expert
+    kernels; every launch-shape branch against the oracle."""
+    from localai_amd import synth
+    rng = np.random.default_rng(T * 100 + k * 10 + t + H)
+    E = 8
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    h = synth.activations(rng, T, H)
+    (out, idx, g), (rout, ridx, rg) = run_both(rw, gu, dn, t, E, H, I, k, h)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
+    assert normwise_rel(out, rout) < 1e-5
