@@ -20,8 +20,9 @@ input, weights already resident in HBM, seeded data from localai_amd/synth.py):
       kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE (known bytes per launch).
 
 Weight copies beyond 2 x the 256 MB Infinity Cache are rotated so every step
-streams its weights from HBM; steps are replayed from HIP graphs captured on
-the launch stream and timed with HIP events on that stream. `roofline` is the
+streams its weights from HBM; one HIP graph holds a whole rotation of steps
+(as a decode step's graph holds every layer), is replayed on the launch
+stream and timed with HIP events on that stream. `roofline` is the
 dominant kernel of the workload timed alone the same way; `cpu_baseline` is
 the reference's own engine/native_quant.cpp kernels (built from source into
 oracle/_ref) on a bounded sample, on the host cores.
@@ -80,6 +81,31 @@ def capture(torch, fn, stream):
             fn()
     torch.cuda.synchronize()
     return g
+
+
+def time_steps(torch, fns, stream, steps, warmup):
+    """Time exactly `steps` steps of the rotation fns[0], fns[1], ... (one
+    function per weight copy). One HIP graph holds a whole rotation, as a
+    decode step's graph holds every layer, so the host launches once per
+    rotation rather than once per step; a second graph holds the first
+    steps mod n. HIP events on the launch stream; returns ms per step."""
+    n = len(fns)
+    full = capture(torch, lambda: [f() for f in fns], stream)
+    q, r = divmod(steps, n)
+    part = capture(torch, lambda: [f() for f in fns[:r]], stream) if r else None
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, -(-warmup // n))):
+            full.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(q):
+            full.replay()
+        if part is not None:
+            part.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps      # ms per step
 
 
 def time_graphs(torch, graphs, stream, steps, warmup):
@@ -189,11 +215,9 @@ def wl_layer(args, torch, device, synth):
         for name, _, _, _, src in layer:
             m[name].matvec(xs[src], out=outs[name], stream=stream)
 
-    graphs = [capture(torch, lambda m=m: run(m), stream) for m in mats]
     log('timing layer')
-    ms = time_graphs(torch, graphs, stream, args.steps, args.warmup)
-    graphs = [capture(torch, lambda m=m: run_single(m), stream) for m in mats]
-    ms_single = time_graphs(torch, graphs, stream, args.steps, args.warmup)
+    ms = time_steps(torch, [lambda m=m: run(m) for m in mats], stream, args.steps, args.warmup)
+    ms_single = time_steps(torch, [lambda m=m: run_single(m) for m in mats], stream, args.steps, args.warmup)
     for name, o in outs.items():
         if not torch.isfinite(o).all():
             raise SystemExit(f'non-finite output in {name}')
@@ -289,9 +313,8 @@ def wl_q8_prefill(args, torch, device, synth):
     mats = [device.QMat.from_ggml(raw, 8, rows, cols) for _ in range(copies)]
     out = torch.empty((tokens, rows), dtype=torch.float32, device=device.device())
     stream = torch.cuda.Stream()
-    graphs = [capture(torch, lambda m=m: m.matmul(x, out=out, stream=stream), stream) for m in mats]
-    log('timing prefill GEMM')
-    ms = time_graphs(torch, graphs, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
+    ms = time_steps(torch, [lambda m=m: m.matmul(x, out=out, stream=stream) for m in mats], stream,
+                    max(10, args.steps // 4), max(3, args.warmup // 4))
     if not torch.isfinite(out).all():
         raise SystemExit('non-finite GEMM output')
     tfs = flops / (ms * 1e-3) / 1e12
@@ -346,9 +369,8 @@ def _moe_gpu(args, torch, device, synth, E, H, I, k, t, T, bias, per_expert_byte
     og = torch.empty((T, k), dtype=torch.float32, device=device.device())
     for L in layers:
         L.workspace(T)
-    graphs = [capture(torch, lambda L=L: L.forward_device(hd, out=out, idx=oi, gates=og, stream=stream), stream)
-              for L in layers]
-    ms = time_graphs(torch, graphs, stream, args.steps, args.warmup)
+    ms = time_steps(torch, [lambda L=L: L.forward_device(hd, out=out, idx=oi, gates=og, stream=stream)
+                            for L in layers], stream, args.steps, args.warmup)
     if not torch.isfinite(out).all():
         raise SystemExit('non-finite MoE output')
     return ms, nbytes, distinct, copies, (gu, dn, rw, h, idx.cpu().numpy())

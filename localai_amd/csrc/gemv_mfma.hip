@@ -111,8 +111,11 @@ __device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, 
     }
 }
 
+// Q4_K workgroups of 1024 threads are held to 64 VGPRs (8 waves per SIMD) so
+// that two fit on a CU; the Q6_K body needs more registers than that
 template <int TYPE, int SPW, int RT, int MAXT>
-__global__ __launch_bounds__(MAXT) void gemv_mfma(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
+__global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(MAXT == 1024 && TYPE == LQ_Q4_K ? 8 : 1)))
+void gemv_mfma(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
                                                   int64_t tiles, const float *__restrict__ x,
                                                   float *__restrict__ y) {
     mt_matvec_block<TYPE, SPW, RT>(Wt, rows, nb, tiles, x, y, blockIdx.x);
@@ -128,15 +131,17 @@ struct MtJobs {
     int type[MT_MAX_JOBS];
     int n;
 };
-template <int SPW, int RT, int MAXT>
-__global__ __launch_bounds__(MAXT) void gemv_mfma_many(MtJobs jobs, int nb, const float *__restrict__ x) {
+// Q6 = false: Q4_K jobs only (no Q6_K body compiled in, 64 VGPRs at 1024 threads)
+template <int SPW, int RT, int MAXT, bool Q6>
+__global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(MAXT == 1024 && !Q6 ? 8 : 1)))
+void gemv_mfma_many(MtJobs jobs, int nb, const float *__restrict__ x) {
     const int64_t b = blockIdx.x;
     int j = 0;
 #pragma unroll
     for (int i = 1; i < MT_MAX_JOBS; ++i)
         if (i < jobs.n && b >= jobs.blk0[i]) j = i;
     const int64_t tiles = (jobs.rows[j] + MT_ROWS - 1) / MT_ROWS;
-    if (jobs.type[j] == LQ_Q6_K)
+    if (Q6 && jobs.type[j] == LQ_Q6_K)
         mt_matvec_block<LQ_Q6_K, SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
     else
         mt_matvec_block<LQ_Q4_K, SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
@@ -153,12 +158,12 @@ __global__ __launch_bounds__(MAXT) void gemv_mfma_many(MtJobs jobs, int nb, cons
 struct MtPlan {
     int spw, waves, rt;
 };
-static MtPlan mt_plan(int nb, int64_t tiles) {
+static MtPlan mt_plan(int nb, int64_t tiles, bool q6) {
     MtPlan p;
     const bool big = tiles >= 768;
     p.spw = nb > 32 ? (nb + 11) / 12 : big ? (nb + 15) / 16 : (nb + 7) / 8;
     p.waves = (nb + p.spw - 1) / p.spw;
-    p.rt = (big && p.spw == 1) ? 2 : 1;
+    p.rt = (big && p.spw == 1 && !q6) ? 2 : 1;   // two Q6_K tiles need more registers
     return p;
 }
 
@@ -179,7 +184,7 @@ int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, floa
     if (nb > 72) return fail(LOCALAI_EARG, "mfma matvec: K too large (more than 18432 values)");
     const bool q6 = g.type == LQ_Q6_K;
     const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
-    const MtPlan p = mt_plan(nb, tiles);
+    const MtPlan p = mt_plan(nb, tiles, q6);
     dim3 grid((unsigned)((tiles + p.rt - 1) / p.rt)), block(64 * p.waves);
     const size_t lds = mt_lds_bytes(g.type, p.waves, p.spw, 1, p.rt);
 #define MT_L(S, R, M)                                                                                           \
@@ -207,7 +212,7 @@ int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const
         total_tiles += (g[j]->rows + MT_ROWS - 1) / MT_ROWS;
         any_q6 |= g[j]->type == LQ_Q6_K;
     }
-    const MtPlan p = mt_plan(nb, total_tiles);
+    const MtPlan p = mt_plan(nb, total_tiles, any_q6);
     MtJobs jobs = {};
     jobs.n = n;
     int64_t b = 0;
@@ -222,7 +227,11 @@ int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const
     for (int j = n; j <= MT_MAX_JOBS; ++j) jobs.blk0[j] = b;
     dim3 grid((unsigned)b), block(64 * p.waves);
     const size_t lds = mt_lds_bytes(any_q6 ? LQ_Q6_K : LQ_Q4_K, p.waves, p.spw, 1, p.rt);
-#define MT_L(S, R, M) hipLaunchKernelGGL((gemv_mfma_many<S, R, M>), grid, block, lds, s, jobs, nb, x)
+#define MT_L(S, R, M)                                                                           \
+    do {                                                                                        \
+        if (any_q6) hipLaunchKernelGGL((gemv_mfma_many<S, R, M, true>), grid, block, lds, s, jobs, nb, x);  \
+        else hipLaunchKernelGGL((gemv_mfma_many<S, R, M, false>), grid, block, lds, s, jobs, nb, x);        \
+    } while (0)
     MT_DISPATCH(MT_L)
 #undef MT_L
 #undef MT_DISPATCH
