@@ -243,7 +243,7 @@ def wl_layer(args, torch, device, synth):
         'config': {'workload': 'llama3_8b_decode_layer_q4_k_m', 'matvecs': 7, 'batch': 1,
                    'shapes': [[n, {12: 'Q4_K', 14: 'Q6_K'}[t], r, c] for n, t, r, c, _ in layer],
                    'algorithmic_bytes_per_layer': layer_bytes, 'weight_copies_rotated': copies,
-                   'launch': 'hip graph per layer; q/k/v and gate/up each one fused launch (shared input)'},
+                   'launch': 'one hip graph per rotation of layer copies; q/k/v and gate/up each one fused launch (shared input)'},
         'roofline': roof, 'cpu_baseline': cpu}
 
 
