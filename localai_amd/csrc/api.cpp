@@ -223,7 +223,7 @@ int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x, fl
     if (int st = ensure_device()) return st;
     lq_geom one = m->g;
     one.batch = 1;
-    if (m->tiles && ntok == 1)
+    if (m->tiles && ntok == 1 && mt_matvec_ok(one))
         return launch_matvec_mfma(one, m->tiles + expert * m->tile_bytes, x, y, (hipStream_t)stream);
     return launch_matvec(one, m->data + expert * m->g.matrix_bytes, x, m->g.cols, y, m->g.rows, ntok,
                          (hipStream_t)stream);
@@ -252,7 +252,7 @@ int localai_hip_matvec_many(int n, const localai_qmat *const *mats, const int64_
         const int64_t e = experts ? experts[j] : 0;
         lq_geom one = mats[j]->g;
         one.batch = 1;
-        if (mats[j]->tiles) {
+        if (mats[j]->tiles && mt_matvec_ok(one)) {
             geo[nf] = one;
             gp[nf] = &geo[nf];
             wt[nf] = mats[j]->tiles + e * mats[j]->tile_bytes;
@@ -283,7 +283,8 @@ int localai_hip_matmul(const localai_qmat *m, int64_t expert, const float *x, in
     lq_geom one = m->g;
     one.batch = 1;
     const int64_t ts = y_layout == 0 ? m->g.rows : 1, rs = y_layout == 0 ? 1 : tokens;
-    return launch_gemm(one, m->data + expert * m->g.matrix_bytes, x, tokens, y, ts, rs, ws, ws_bytes,
+    return launch_gemm(one, m->data + expert * m->g.matrix_bytes, m->tiles ? m->tiles + expert * m->tile_bytes : nullptr,
+                       x, tokens, y, ts, rs, ws, ws_bytes,
                        (hipStream_t)stream);
 }
 

@@ -13,8 +13,11 @@
 // power of two so that its largest magnitude lies in [2^14, 2^15) (exact),
 // rounded to f16, and the output is scaled back by the inverse power. f16 (11
 // significant bits) rather than bf16 (8) keeps the normwise error near 2^-12.
+#include <type_traits>
+
 #include "gemv_core.h"
 #include "internal.h"
+#include "mfma_core.h"
 
 namespace lq {
 
@@ -165,6 +168,8 @@ struct GemmArgs {
     int64_t y_ts, y_rs;
     const int32_t *tile_e, *tile_p0, *tile_n, *n_tiles;
     int64_t inter;
+    const uint8_t *Wt;         // tile form (mfma_core.h) or null; MoE: expert 0
+    int64_t wt_bytes;          // tile-form bytes per matrix
 };
 
 template <int T, int BN, int MODE>
@@ -331,9 +336,260 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     }
 }
 
+// --------------------------------------------------- GEMM on the tile form
+// Q4_K / Q6_K / Q8_0 handles carry the tile form (mfma_core.h). For a 32-value
+// slice of a 256-value block, the 8 quants that lane l (weight row l % 16,
+// k = 8 (l / 16) .. + 7) holds in its 16-byte slice are exactly that lane's
+// part of the B operand of v_mfma_f32_16x16x32_f16. So a wave decodes its own
+// weight rows straight into B registers -- each weight value once per
+// workgroup, exactly in fp32 (or, for Q8_0, exactly as 1152 + q in f16 times
+// d), rounded once to f16 -- and only the f16 activations (A operands) go
+// through LDS, double-buffered and shared by the 4 waves.
+//
+// Workgroup: 4 waves x 2 row tiles (128 weight rows; for gate_up 64 gate rows
+// and the 64 matching up rows) x BN tokens, 128 K values per step.
+
+constexpr int GT_WROWS = 128;          // weight rows per workgroup (dense, down)
+
+template <int T> struct GtRaw;
+template <> struct GtRaw<LQ_Q4_K> { uint4 qs, hd; };
+template <> struct GtRaw<LQ_Q6_K> { uint4 ql, qh, sc; uint32_t d; };
+template <> struct GtRaw<LQ_Q8_0> { uint4 p0, p1, dd; };
+
+// weights of half `half` (values 128 half .. + 127) of one 256-value block
+template <int T>
+__device__ __forceinline__ GtRaw<T> gt_load(const uint8_t *blk, int half, int lane) {
+    GtRaw<T> r;
+    const int n = lane & 15;
+    if constexpr (T == LQ_Q4_K) {
+        r.qs = ld16(blk + half * 1024 + 16 * lane);
+        r.hd = ld16(blk + 2048 + 16 * n);
+    } else if constexpr (T == LQ_Q6_K) {
+        r.ql = ld16(blk + half * 1024 + 16 * lane);
+        r.qh = ld16(blk + 2048 + 16 * lane);
+        r.sc = ld16(blk + 3072 + 16 * n);
+        r.d = *reinterpret_cast<const uint16_t *>(blk + 3328 + 2 * n);
+    } else {
+        r.p0 = ld16(blk + 2 * half * 1024 + 16 * lane);
+        r.p1 = ld16(blk + (2 * half + 1) * 1024 + 16 * lane);
+        r.dd = ld16(blk + 4096 + 16 * n);
+    }
+    return r;
+}
+
+__device__ __forceinline__ uint32_t gt_pk(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
+}
+
+// B operand (8 f16) of slice kk (0..3) of half HALF of the block, lane group q
+template <int T, int HALF, int KK>
+__device__ __forceinline__ lq_h8 gt_b(const GtRaw<T> &r, int q) {
+    uint4 o;
+    if constexpr (T == LQ_Q4_K) {
+        // group g = 4 HALF + KK: qs chunk g / 2 (bytes 8 ((g / 2) % 2) ..), nibble g % 2
+        constexpr int g = 4 * HALF + KK, hb = (g >> 1) & 1, nib = g & 1;
+        const uint32_t s0 = r.hd.y, s4 = r.hd.z, s8 = r.hd.w;   // scale bytes 0..3, 4..7, 8..11
+        uint32_t sc, mn;
+        if constexpr (g < 4) {
+            sc = (s0 >> (8 * g)) & 63u;
+            mn = (s4 >> (8 * g)) & 63u;
+        } else {
+            constexpr int j = g - 4;
+            sc = ((s8 >> (8 * j)) & 15u) | (((s0 >> (8 * j + 6)) & 3u) << 4);
+            mn = ((s8 >> (8 * j + 4)) & 15u) | (((s4 >> (8 * j + 6)) & 3u) << 4);
+        }
+        const float a = f16_to_f32(r.hd.x) * (float)sc, b = f16_to_f32(r.hd.x >> 16) * (float)mn;
+        const uint32_t w0 = ((hb ? r.qs.z : r.qs.x) >> (4 * nib)) & 0x0F0F0F0Fu;
+        const uint32_t w1 = ((hb ? r.qs.w : r.qs.y) >> (4 * nib)) & 0x0F0F0F0Fu;
+        o.x = gt_pk(__builtin_fmaf(a, (float)(w0 & 255u), -b), __builtin_fmaf(a, (float)((w0 >> 8) & 255u), -b));
+        o.y = gt_pk(__builtin_fmaf(a, (float)((w0 >> 16) & 255u), -b), __builtin_fmaf(a, (float)(w0 >> 24), -b));
+        o.z = gt_pk(__builtin_fmaf(a, (float)(w1 & 255u), -b), __builtin_fmaf(a, (float)((w1 >> 8) & 255u), -b));
+        o.w = gt_pk(__builtin_fmaf(a, (float)((w1 >> 16) & 255u), -b), __builtin_fmaf(a, (float)(w1 >> 24), -b));
+    } else if constexpr (T == LQ_Q6_K) {
+        // slice g = 4 HALF + KK: values 128 HALF + 32 KK + 8q .. ; ql nibble KK / 2 of
+        // bytes 8 (KK % 2) ..; qh bits 2 KK of bytes 8 HALF ..; sub-block 2g + q / 2
+        constexpr int g = 4 * HALF + KK;
+        const uint32_t l0 = ((KK & 1) ? r.ql.z : r.ql.x) >> (4 * (KK >> 1));
+        const uint32_t l1 = ((KK & 1) ? r.ql.w : r.ql.y) >> (4 * (KK >> 1));
+        const uint32_t e0 = (HALF ? r.qh.z : r.qh.x) >> (2 * KK), e1 = (HALF ? r.qh.w : r.qh.y) >> (2 * KK);
+        const uint32_t w0 = (l0 & 0x0F0F0F0Fu) | ((e0 & 0x03030303u) << 4);
+        const uint32_t w1 = (l1 & 0x0F0F0F0Fu) | ((e1 & 0x03030303u) << 4);
+        // sub-blocks 2g and 2g + 1 share scale dword g / 2
+        const uint32_t sw = (g >> 1) == 0 ? r.sc.x : (g >> 1) == 1 ? r.sc.y : (g >> 1) == 2 ? r.sc.z : r.sc.w;
+        const int sbyte = ((2 * g) & 3) + (q >> 1);
+        const float dsc = f16_to_f32(r.d) * (float)(int)__builtin_amdgcn_sbfe((int)sw, 8 * sbyte, 8);
+        const float off = -32.0f * dsc;
+        o.x = gt_pk(__builtin_fmaf(dsc, (float)(w0 & 255u), off), __builtin_fmaf(dsc, (float)((w0 >> 8) & 255u), off));
+        o.y = gt_pk(__builtin_fmaf(dsc, (float)((w0 >> 16) & 255u), off), __builtin_fmaf(dsc, (float)(w0 >> 24), off));
+        o.z = gt_pk(__builtin_fmaf(dsc, (float)(w1 & 255u), off), __builtin_fmaf(dsc, (float)((w1 >> 8) & 255u), off));
+        o.w = gt_pk(__builtin_fmaf(dsc, (float)((w1 >> 16) & 255u), off), __builtin_fmaf(dsc, (float)(w1 >> 24), off));
+    } else {
+        // GGML block 4 HALF + KK: piece KK / 2 of the half, bytes 8 (KK % 2) ..
+        const uint4 pc = (KK >> 1) ? r.p1 : r.p0;
+        const uint32_t w0 = (KK & 1) ? pc.z : pc.x, w1 = (KK & 1) ? pc.w : pc.y;
+        constexpr int g = 4 * HALF + KK;
+        const uint32_t dw = g < 2 ? r.dd.x : g < 4 ? r.dd.y : g < 6 ? r.dd.z : r.dd.w;
+        const uint32_t dh = (dw >> (16 * (g & 1))) & 0xFFFFu;
+        const lq_h2 d2 = __builtin_bit_cast(lq_h2, dh * 0x10001u);
+        q8_pairs(w0, d2, o.x, o.y);
+        q8_pairs(w1, d2, o.z, o.w);
+    }
+    return __builtin_bit_cast(lq_h8, o);
+}
+
+// MFMAs of the four 32-value slices of half HALF of a block: B operands
+// decoded from the wave's two row tiles, A operands from the LDS x tile
+// x tile in LDS: [token][16 chunks of 8 halves], chunk c of token t stored at
+// position c ^ (t % 16), so the 16 tokens of an A read hit 16 bank groups
+template <int T, int HALF, int NI>
+__device__ __forceinline__ void gt_half(const GtRaw<T> &w0, const GtRaw<T> &w1, const _Float16 *xs, int lane,
+                                        lq_f4 (&acc)[NI][2]) {
+    const int fr = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        // all A reads of the slice in flight while the B operands are decoded
+        lq_h8 av[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            av[i] = *reinterpret_cast<const lq_h8 *>(xs + (16 * i + fr) * GM_BK + 8 * ((4 * kk + q) ^ fr));
+        lq_h8 b0, b1;
+        if (kk == 0) { b0 = gt_b<T, HALF, 0>(w0, q); b1 = gt_b<T, HALF, 0>(w1, q); }
+        else if (kk == 1) { b0 = gt_b<T, HALF, 1>(w0, q); b1 = gt_b<T, HALF, 1>(w1, q); }
+        else if (kk == 2) { b0 = gt_b<T, HALF, 2>(w0, q); b1 = gt_b<T, HALF, 2>(w1, q); }
+        else { b0 = gt_b<T, HALF, 3>(w0, q); b1 = gt_b<T, HALF, 3>(w1, q); }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], b0, acc[i][0], 0, 0, 0);
+            acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], b1, acc[i][1], 0, 0, 0);
+        }
+    }
+}
+
+template <int T, int BN, int MODE>
+__global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
+    constexpr int NI = BN / 16;            // 16-token MFMA tiles per wave
+    constexpr int XN = BN * 16 / 256;      // 16-byte x chunks per thread and step
+    constexpr int BB = mt_block_bytes(T);
+    __shared__ __attribute__((aligned(16))) _Float16 Xs[2][BN * GM_BK];
+    const lq_geom &g = a.g;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint8_t *Wt = a.Wt;
+    int64_t p0;
+    int tn;
+    int64_t blk;
+    if constexpr (MODE == GM_DENSE) {
+        // 1-D grid, padded to a multiple of 8; workgroup id -> logical index
+        // xcd * per + id / 8 walks the row blocks of one token tile per XCD
+        const int id = blockIdx.x, per = gridDim.x / 8;
+        const int L = (id % 8) * per + id / 8;
+        const int nrb = (int)((g.rows + GT_WROWS - 1) / GT_WROWS);
+        const int64_t ntt = (a.ntok + BN - 1) / BN;
+        if (L >= nrb * ntt) return;
+        blk = L % nrb;
+        p0 = (int64_t)(L / nrb) * BN;
+        tn = (int)(a.ntok - p0 < BN ? a.ntok - p0 : BN);
+    } else {
+        blk = blockIdx.x;
+        const int tile = blockIdx.y;
+        if (tile >= a.n_tiles[0]) return;
+        Wt += (int64_t)a.tile_e[tile] * a.wt_bytes;
+        p0 = a.tile_p0[tile];
+        tn = a.tile_n[tile];
+    }
+    const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS, nsb = mt_nsb(g);
+    // the wave's two row tiles: dense / down 8 blk + 2 wave + j; gate_up
+    // gate tile 4 blk + wave (j = 0) and its up tile inter / 16 + 4 blk + wave
+    int64_t t0, t1;
+    if constexpr (MODE == GM_MOE_GATE_UP) {
+        t0 = 4 * blk + wave;
+        t1 = a.inter / MT_ROWS + 4 * blk + wave;
+    } else {
+        t0 = 8 * blk + 2 * wave;
+        t1 = t0 + 1;
+    }
+    const uint8_t *w0p = Wt + (t0 < tiles ? t0 : tiles - 1) * nsb * BB;
+    const uint8_t *w1p = Wt + (t1 < tiles ? t1 : tiles - 1) * nsb * BB;
+
+    // x loader: instruction i of wave w fills tile chunks (4i + w) * 64 + lane,
+    // i.e. token row (4i + w) * 4 + lane / 16, position lane % 16, from the
+    // row's chunk (lane % 16) ^ (row % 16); straight from global memory into
+    // LDS (no registers), waited for with vmcnt before the step's barrier
+    const _Float16 *xsrc[XN];
+#pragma unroll
+    for (int i = 0; i < XN; ++i) {
+        const int row = (4 * i + wave) * 4 + (lane >> 4), c = (lane & 15) ^ (row & 15);
+        xsrc[i] = a.Xh + (p0 + (row < tn ? row : 0)) * a.ldh + 8 * c;
+    }
+    auto load_x = [&](int buf, int64_t step) {
+#pragma unroll
+        for (int i = 0; i < XN; ++i)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(xsrc[i] + step * GM_BK),
+                (__attribute__((address_space(3))) void *)&Xs[buf][(4 * i + wave) * 64 * 8], 16, 0, 0);
+    };
+
+    lq_f4 acc[NI][2];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        acc[i][0] = lq_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        acc[i][1] = lq_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    // prologue: half 0 of block 0
+    GtRaw<T> a0 = gt_load<T>(w0p, 0, lane), a1 = gt_load<T>(w1p, 0, lane);
+    load_x(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // step loop over blocks: half 0 from Xs[0] / (a0, a1), half 1 from Xs[1] / (b0, b1);
+    // the next half's weights and x are requested before the current half's MFMAs
+    for (int64_t sb = 0; sb < nsb; ++sb) {
+        const GtRaw<T> b0 = gt_load<T>(w0p + sb * BB, 1, lane), b1 = gt_load<T>(w1p + sb * BB, 1, lane);
+        load_x(1, 2 * sb + 1);
+        // nothing crosses: the loads stay ahead of the MFMAs, and the next
+        // half's decode stays behind them (it would wait on these loads)
+        __builtin_amdgcn_sched_barrier(0);
+        gt_half<T, 0, NI>(a0, a1, Xs[0], lane, acc);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // next block (the last block re-reads itself: Xs[0] is not read again)
+        const int64_t nx = sb + 1 < nsb ? sb + 1 : sb;
+        a0 = gt_load<T>(w0p + nx * BB, 0, lane);
+        a1 = gt_load<T>(w1p + nx * BB, 0, lane);
+        load_x(0, 2 * nx);
+        __builtin_amdgcn_sched_barrier(0);
+        gt_half<T, 1, NI>(b0, b1, Xs[1], lane, acc);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    // D[m][n]: lane holds tokens 4 (lane / 16) + v of token tile i, row lane % 16 of row tile j
+    const int fr = lane & 15;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int lt = 16 * i + 4 * (lane >> 4) + v;
+            if (lt >= tn) continue;
+            const int64_t p = p0 + lt;
+            const float sc = a.inv[p];
+            if constexpr (MODE == GM_MOE_GATE_UP) {
+                const int64_t r = t0 * MT_ROWS + fr;
+                if (r < a.inter) a.Y[p * a.y_ts + r] = silu(acc[i][0][v] * sc) * (acc[i][1][v] * sc);
+            } else {
+                const int64_t r0 = t0 * MT_ROWS + fr, r1 = t1 * MT_ROWS + fr;
+                if (t0 < tiles && r0 < g.rows) a.Y[p * a.y_ts + r0 * a.y_rs] = acc[i][0][v] * sc;
+                if (t1 < tiles && r1 < g.rows) a.Y[p * a.y_ts + r1 * a.y_rs] = acc[i][1][v] * sc;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- host side
 
-static int64_t gemm_ldh(const lq_geom &g) { return (int64_t)GM_BK * ((g.nu + 1) / 2); }
+// f16 activation rows are padded with zeros to a multiple of 256 values (the
+// tile form's block; a multiple of the row-plane kernel's 128-value step)
+static int64_t gemm_ldh(const lq_geom &g) { return 256 * ((g.cols + 255) / 256); }
 
 int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok) {
     const int64_t xh = (ntok * gemm_ldh(g) * 2 + 255) & ~(int64_t)255;
@@ -361,8 +617,20 @@ static int launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t s) {
     return LOCALAI_OK;
 }
 
-int launch_gemm(const lq_geom &g, const uint8_t *W, const float *X, int64_t ntok, float *Y, int64_t y_ts,
-                int64_t y_rs, void *ws, int64_t ws_bytes, hipStream_t s) {
+template <int MODE, int BN>
+static int launch_gemm_tile_t(const GemmArgs &a, dim3 grid, hipStream_t s) {
+    switch (a.g.type) {
+#define LQ_GT(TT) case TT: hipLaunchKernelGGL((gemm_tile_kernel<TT, BN, MODE>), grid, dim3(256), 0, s, a); break;
+        LQ_GT(LQ_Q4_K) LQ_GT(LQ_Q6_K) LQ_GT(LQ_Q8_0)
+#undef LQ_GT
+        default: return fail(LOCALAI_ETYPE, "matmul: no tile form for this GGML type");
+    }
+    LQ_HIP(hipGetLastError());
+    return LOCALAI_OK;
+}
+
+int launch_gemm(const lq_geom &g, const uint8_t *W, const uint8_t *Wt, const float *X, int64_t ntok, float *Y,
+                int64_t y_ts, int64_t y_rs, void *ws, int64_t ws_bytes, hipStream_t s) {
     if (ntok <= 0) return LOCALAI_OK;
     if (ws_bytes < gemm_workspace_bytes(g, ntok)) return fail(LOCALAI_EARG, "matmul: workspace too small");
     const int64_t ldh = gemm_ldh(g);
@@ -371,6 +639,12 @@ int launch_gemm(const lq_geom &g, const uint8_t *W, const float *X, int64_t ntok
     if (int st = launch_x_to_f16(X, g.cols, g.cols, nullptr, 1, ntok, Xh, ldh, inv, s)) return st;
     GemmArgs a{};
     a.g = g; a.W = W; a.Xh = Xh; a.ldh = (int)ldh; a.inv = inv; a.ntok = ntok; a.Y = Y; a.y_ts = y_ts; a.y_rs = y_rs;
+    a.Wt = Wt;
+    if (Wt) {
+        const int64_t nwg = ((g.rows + GT_WROWS - 1) / GT_WROWS) * ((ntok + GM_BN - 1) / GM_BN);
+        if (nwg > ((int64_t)1 << 30)) return fail(LOCALAI_EARG, "matmul: problem too large");
+        return launch_gemm_tile_t<GM_DENSE, GM_BN>(a, dim3((unsigned)((nwg + 7) / 8 * 8)), s);
+    }
     const int64_t nwg = ((g.rows + GM_BM - 1) / GM_BM) * ((ntok + GM_BN - 1) / GM_BN);
     if (nwg > ((int64_t)1 << 30)) return fail(LOCALAI_EARG, "matmul: problem too large");
     dim3 grid((unsigned)((nwg + 7) / 8 * 8));
@@ -379,15 +653,23 @@ int launch_gemm(const lq_geom &g, const uint8_t *W, const float *X, int64_t ntok
 
 int moe_gemm_tile() { return GM_MOE_BN; }
 
-int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, bool gate_up, const _Float16 *Xh, int64_t ldh,
-                    const float *inv, float *Y, int64_t y_ts, int64_t inter, const int32_t *tile_e,
-                    const int32_t *tile_p0, const int32_t *tile_n, const int32_t *n_tiles, int max_tiles,
-                    hipStream_t s) {
+int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, const uint8_t *Wt_all, int64_t wt_bytes, bool gate_up,
+                    const _Float16 *Xh, int64_t ldh, const float *inv, float *Y, int64_t y_ts, int64_t inter,
+                    const int32_t *tile_e, const int32_t *tile_p0, const int32_t *tile_n, const int32_t *n_tiles,
+                    int max_tiles, hipStream_t s) {
     GemmArgs a{};
     a.g = g; a.W = Wall; a.Xh = Xh; a.ldh = (int)ldh; a.inv = inv; a.Y = Y; a.y_ts = y_ts; a.y_rs = 1;
     a.tile_e = tile_e; a.tile_p0 = tile_p0; a.tile_n = tile_n; a.n_tiles = n_tiles; a.inter = inter;
+    a.Wt = Wt_all; a.wt_bytes = wt_bytes;
     if (max_tiles <= 0) return LOCALAI_OK;
     if (max_tiles > 65535) return fail(LOCALAI_EARG, "moe: too many token tiles");
+    if (Wt_all && (!gate_up || inter % MT_ROWS == 0)) {
+        if (gate_up)
+            return launch_gemm_tile_t<GM_MOE_GATE_UP, GM_MOE_BN>(
+                a, dim3((unsigned)((inter + 63) / 64), (unsigned)max_tiles), s);
+        return launch_gemm_tile_t<GM_MOE_DOWN, GM_MOE_BN>(
+            a, dim3((unsigned)((g.rows + GT_WROWS - 1) / GT_WROWS), (unsigned)max_tiles), s);
+    }
     if (gate_up) {
         dim3 grid((unsigned)((inter + GM_BM / 2 - 1) / (GM_BM / 2)), (unsigned)max_tiles);
         return launch_gemm_t<GM_MOE_GATE_UP, GM_MOE_BN>(a, grid, s);

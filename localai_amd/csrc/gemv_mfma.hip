@@ -10,12 +10,18 @@ namespace lq {
 
 constexpr int MT_MAX_JOBS = 8;        // matrices per fused launch (localai_hip_matvec_many)
 
-// 0 when the matrix gets no tile form (other types, or K beyond the 72
-// super-blocks the launch plan covers): its matvecs then run on gemv.hip.
+// Bytes of one matrix's tile form; 0 for types without one (their matvecs
+// and GEMMs run on the row planes).
 int64_t mt_matrix_bytes(const lq_geom &g) {
-    if ((g.type != LQ_Q4_K && g.type != LQ_Q6_K) || g.nb > 72) return 0;
+    if (g.type != LQ_Q4_K && g.type != LQ_Q6_K && g.type != LQ_Q8_0) return 0;
     const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
-    return lq_align256(tiles * g.nb * mt_block_bytes(g.type));
+    return lq_align256(tiles * mt_nsb(g) * mt_block_bytes(g.type));
+}
+
+// The decode matvec runs on MFMA for Q4_K / Q6_K up to 72 super-blocks per
+// row (the launch plan below); other matrices use gemv.hip.
+bool mt_matvec_ok(const lq_geom &g) {
+    return (g.type == LQ_Q4_K || g.type == LQ_Q6_K) && g.nb <= 72;
 }
 
 // GGML -> tile form, one thread per (matrix, row, super-block). Rows past
@@ -71,14 +77,43 @@ __global__ void mt_repack_q6k(lq_geom g, const uint8_t *__restrict__ src, uint8_
     }
 }
 
+// Q8_0: one thread per (matrix, row, 256-value block); GGML blocks are
+// d (2 B) then 32 int8 quants. Blocks past the row end stay zero.
+__global__ void mt_repack_q80(lq_geom g, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                              int64_t dst_matrix_bytes) {
+    const int64_t nsb = mt_nsb(g);
+    const int64_t total = g.batch * g.rows * nsb;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t e = i / (g.rows * nsb);
+        const int64_t rem = i - e * g.rows * nsb;
+        const int64_t row = rem / nsb, sb = rem - row * nsb;
+        const uint8_t *srow = src + e * g.ggml_matrix_bytes + row * g.ggml_row_bytes;
+        uint8_t *blk = dst + e * dst_matrix_bytes + ((row / MT_ROWS) * nsb + sb) * MT_Q80_BLOCK;
+        const int n = (int)(row % MT_ROWS);
+        for (int j = 0; j < 8; ++j) {
+            const int64_t b = sb * 8 + j;
+            if (b >= g.nb) break;
+            const uint8_t *s = srow + b * 34;
+            blk[4096 + n * 16 + 2 * j] = s[0];
+            blk[4096 + n * 16 + 2 * j + 1] = s[1];
+            for (int c = 0; c < 4; ++c)
+                for (int q = 0; q < 8; ++q)
+                    blk[(j >> 1) * 1024 + (n + 16 * c) * 16 + 8 * (j & 1) + q] = s[2 + 8 * c + q];
+        }
+    }
+}
+
 int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_t dst_matrix_bytes,
                      hipStream_t s) {
-    const int64_t total = g.batch * g.rows * g.nb;
+    const int64_t total = g.batch * g.rows * mt_nsb(g);
     LQ_HIP(hipMemsetAsync(dst, 0, (size_t)(dst_matrix_bytes * g.batch), s));
     if (total <= 0) return LOCALAI_OK;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    if (g.type == LQ_Q6_K)
+    if (g.type == LQ_Q8_0)
+        hipLaunchKernelGGL(mt_repack_q80, dim3((unsigned)blocks), dim3(256), 0, s, g, ggml, dst, dst_matrix_bytes);
+    else if (g.type == LQ_Q6_K)
         hipLaunchKernelGGL(mt_repack_q6k, dim3((unsigned)blocks), dim3(256), 0, s, g, ggml, dst, dst_matrix_bytes);
     else
         hipLaunchKernelGGL(mt_repack_q4k, dim3((unsigned)blocks), dim3(256), 0, s, g, ggml, dst, dst_matrix_bytes);

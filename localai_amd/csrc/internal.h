@@ -49,21 +49,23 @@ int launch_matvec(const lq_geom &g, const uint8_t *packed, const float *x, int64
 
 int64_t mt_matrix_bytes(const lq_geom &g);
 int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_t dst_matrix_bytes, hipStream_t s);
+bool mt_matvec_ok(const lq_geom &g);
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s);
 int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const *Wt, const float *x,
                             float *const *y, hipStream_t s);
 bool mfma_matvec_enabled();
 
 int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok);
-int launch_gemm(const lq_geom &g, const uint8_t *packed, const float *x, int64_t ntok, float *y, int64_t y_ts,
-                int64_t y_rs, void *ws, int64_t ws_bytes, hipStream_t s);
+// Wt: the tile form (mfma_core.h) when the handle has one, else null
+int launch_gemm(const lq_geom &g, const uint8_t *packed, const uint8_t *Wt, const float *x, int64_t ntok, float *y,
+                int64_t y_ts, int64_t y_rs, void *ws, int64_t ws_bytes, hipStream_t s);
 
 int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *rows_map, int k, int64_t ntok,
                     _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s);
-int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, bool gate_up, const _Float16 *Xh, int64_t ldh,
-                    const float *inv, float *Y, int64_t y_ts, int64_t inter, const int32_t *tile_e,
-                    const int32_t *tile_p0, const int32_t *tile_n, const int32_t *n_tiles, int max_tiles,
-                    hipStream_t s);
+int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, const uint8_t *Wt_all, int64_t wt_bytes, bool gate_up,
+                    const _Float16 *Xh, int64_t ldh, const float *inv, float *Y, int64_t y_ts, int64_t inter,
+                    const int32_t *tile_e, const int32_t *tile_p0, const int32_t *tile_n, const int32_t *n_tiles,
+                    int max_tiles, hipStream_t s);
 int moe_gemm_tile();   // tokens per expert GEMM tile
 
 size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I);

@@ -12,6 +12,8 @@
 //   Q6_K block (3360 B): ql piece h [64][16 B] (ql[64h + 8c ..], ql[64h + 32
 //     + 8c ..]), qh [64][16 B] (qh[8c ..], qh[32 + 8c ..]), int8 scales
 //     [16 rows][16 B], d [16 rows][2 B]
+//   Q8_0 block of 8 GGML blocks (4352 B): piece p [64][16 B] (quants 8c ..
+//     8c + 7 of blocks 2p and 2p + 1), d [16 rows][8 x 2 B]
 //
 // Arithmetic, per (tile, super-block):
 //   B = the quants as unsigned bytes (Q4_K: a nibble, 0..15, masked in place;
@@ -43,10 +45,16 @@ typedef int mt_i4 __attribute__((ext_vector_type(4)));
 constexpr int MT_ROWS = 16;
 constexpr int MT_Q4K_BLOCK = 2304;
 constexpr int MT_Q6K_BLOCK = 3360;     // ql 2 x 1 KiB, qh 1 KiB, scales 16 x 16 B, d 16 x 2 B
+constexpr int MT_Q80_BLOCK = 4352;     // 8 Q8_0 blocks: 4 block-pair pieces x 1 KiB, d 16 rows x 8 x 2 B
 constexpr int MT_XBYTES = 1024 + 64;   // Q4_K per super-block: x pieces + 8 x (group sum, 2^-s)
 constexpr int MT6_XBYTES = 1024 + 128; // Q6_K per super-block: x pieces + 16 x (sub-block sum, 2^-s)
 
-__host__ __device__ constexpr int mt_block_bytes(int t) { return t == LQ_Q4_K ? MT_Q4K_BLOCK : MT_Q6K_BLOCK; }
+__host__ __device__ constexpr int mt_block_bytes(int t) {
+    return t == LQ_Q4_K ? MT_Q4K_BLOCK : t == LQ_Q6_K ? MT_Q6K_BLOCK : MT_Q80_BLOCK;
+}
+// 256-value blocks per row in the tile form (Q8_0: eight GGML blocks, the
+// last one zero-padded)
+__host__ __device__ inline int64_t mt_nsb(const lq_geom &g) { return g.type == LQ_Q8_0 ? (g.nb + 7) / 8 : g.nb; }
 __host__ __device__ constexpr int mt_xbytes(int t) { return t == LQ_Q4_K ? MT_XBYTES : MT6_XBYTES; }
 
 // LDS of a workgroup running mt_pass: per-wave x regions, cross-wave partial

@@ -528,7 +528,8 @@ static int64_t moe_max_tiles(int64_t N, int64_t E, int tile_w) {
     return N / tile_w + (E < N ? E : N);
 }
 
-static int64_t f16_stride(int64_t cols) { return 128 * (((cols + 63) / 64 + 1) / 2); }
+// f16 token rows, zero-padded to a multiple of 256 values (gemm.hip)
+static int64_t f16_stride(int64_t cols) { return 256 * ((cols + 255) / 256); }
 
 size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
     const int64_t N = T * k;
@@ -628,7 +629,8 @@ static int launch_grouped(const localai_qmat *m, const MoeTables &tb, const floa
 // super-blocks: one super-block per wave (up to 16 waves) for K <= 16
 // super-blocks, else four per wave (up to 8 waves, room for the registers).
 static bool moe_mfma_ok(const localai_qmat *gu, const localai_qmat *dn, const float *h, int64_t H, int64_t I) {
-    return gu->tiles && dn->tiles && gu->g.type == dn->g.type && gu->g.nb <= 32 && dn->g.nb <= 32 &&
+    return gu->tiles && dn->tiles && gu->g.type == dn->g.type && gu->g.type != LQ_Q8_0 && gu->g.nb <= 32 &&
+           dn->g.nb <= 32 &&
            (reinterpret_cast<uintptr_t>(h) & 15) == 0 && I % MT_ROWS == 0 && gu->g.cols == H && dn->g.cols == I;
 }
 
@@ -698,11 +700,13 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
         const int64_t N = T * k;
         if (gu->g.cols != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe: expert shapes");
         if (int st = launch_x_to_f16(h, H, H, tb.perm, k, N, tb.xh_gu, f16_stride(H), tb.inv_gu, s)) return st;
-        if (int st = launch_moe_gemm(gu->g, gu->data, true, tb.xh_gu, f16_stride(H), tb.inv_gu, tb.act, I, I,
+        if (int st = launch_moe_gemm(gu->g, gu->data, gu->tiles, gu->tile_bytes, true, tb.xh_gu, f16_stride(H),
+                                     tb.inv_gu, tb.act, I, I,
                                      tb.tile_e, tb.tile_p0, tb.tile_n, tb.n_tiles, tb.max_tiles, s))
             return st;
         if (int st = launch_x_to_f16(tb.act, I, I, nullptr, 1, N, tb.xh_dn, f16_stride(I), tb.inv_dn, s)) return st;
-        if (int st = launch_moe_gemm(dn->g, dn->data, false, tb.xh_dn, f16_stride(I), tb.inv_dn, tb.ysl, H, I,
+        if (int st = launch_moe_gemm(dn->g, dn->data, dn->tiles, dn->tile_bytes, false, tb.xh_dn, f16_stride(I),
+                                     tb.inv_dn, tb.ysl, H, I,
                                      tb.tile_e, tb.tile_p0, tb.tile_n, tb.n_tiles, tb.max_tiles, s))
             return st;
     } else if (moe_mfma_ok(gu, dn, h, H, I)) {
