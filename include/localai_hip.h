@@ -135,7 +135,8 @@ int64_t localai_hip_moe_workspace_size(int64_t tokens, int64_t experts, int top_
  *   topk_idx_dev  [tokens, top_k] int32, experts by (logit desc, index asc)
  *   topk_w_dev    [tokens, top_k] fp32, softmax over the selected logits
  * Router logits: exact fp64 products summed in a fixed order, rounded to fp32
- * once, so the selected experts are bit-reproducible.
+ * once, so the selected experts are bit-reproducible. On return the workspace
+ * begins with them: [tokens, experts] fp32, bias included.
  * Limits: experts <= 1024, 1 <= top_k <= min(16, experts), inter % 64 == 0;
  * h_dev and router_w_dev 16-byte aligned, workspace 256-byte aligned. */
 int localai_hip_moe_forward(const float *h_dev, int64_t tokens, int64_t hidden,

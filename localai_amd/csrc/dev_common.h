@@ -7,6 +7,8 @@
 
 namespace lq {
 
+typedef float lq_f4 __attribute__((ext_vector_type(4)));   // one 16-byte register tuple
+
 // IEEE binary16 -> binary32, exact for every input (subnormals, inf, NaN);
 // same values as half_to_float, engine/native_quant.cpp:12-33.
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {

@@ -22,7 +22,6 @@
 namespace lq {
 
 typedef _Float16 lq_h8 __attribute__((ext_vector_type(8)));
-typedef float lq_f4 __attribute__((ext_vector_type(4)));
 
 constexpr int GM_BM = 128;             // weight rows per workgroup
 constexpr int GM_BN = 128;             // tokens per workgroup (dense)

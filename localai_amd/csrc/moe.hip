@@ -10,10 +10,13 @@
 //   silu(g)      = g / (1 + exp(-clip(g, -80, 80)))  (engine/zaya.py:305)
 //
 // Kernels (one stream, in order):
-//   route     one workgroup per token: router logits, top-k, gates (for a
-//             single token also the permutation tables below)
-//   permute   one workgroup: expert histogram, exclusive scan, stable
-//             expert-major permutation of the T*k assignments (LDS)
+//   route     few tokens: one workgroup per token: router logits, top-k,
+//             gates (for a single token also the permutation tables below);
+//             many tokens: register-tiled logits over LDS-streamed rows,
+//             then one wave per token for top-k and gates
+//   permute   one workgroup: ballot-matched ranks per wave, per-expert
+//             scan, stable expert-major permutation of the T*k assignments
+//             and the expert GEMM tile list
 //   gate_up   grouped matvec over the active experts, one workgroup per
 //             (64-row gate tile + matching up tile, expert); SiLU*up fused
 //   down      grouped matvec over the active experts
@@ -55,134 +58,94 @@ struct MoeTables {
 
 // ------------------------------------------------------------------ route
 
-// (logit desc, index asc); a NaN logit ranks below every number, NaNs by
-// index -- the order of np.lexsort((index, -logit)) (oracle/moe.py topk)
-__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
-    const bool na = va != va, nb = vb != vb;
-    if (na || nb) return nb && (!na || ia < ib);
-    return va > vb || (va == vb && ia < ib);
+// Expert order: (logit desc, index asc); a NaN logit ranks below every
+// number, NaNs by index -- the order of np.lexsort((index, -logit))
+// (oracle/moe.py topk). route_key maps a logit to an unsigned key with the
+// same order on values: numbers by their IEEE order (-0 and +0 equal) from
+// 0x007fffff up, NaN 1; 0 is left for experts out of the running.
+__device__ __forceinline__ uint32_t route_key(float v) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t m = b == 0x80000000u ? 0x80000000u : (b & 0x80000000u ? ~b : b | 0x80000000u);
+    return v != v ? 1u : m;
 }
 
-// Widest hidden size whose fp64 copy of h is staged in LDS (64 KiB); wider
-// rows convert h in registers in every wave.
-constexpr int ROUTE_LDS_H = 8192;
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
 
-// One workgroup per token. h is converted to fp64 once (in LDS) and shared by
-// the waves, each of which computes whole expert logits; wave 0 then ranks
-// the experts. With `tables` (a single token) the workgroup also writes the
-// expert-major permutation tables of moe_permute_kernel for its k
-// assignments, so the layer needs no permute launch.
-// LDS: E logits, k selected experts (8-byte aligned), then h as fp64.
-template <bool LDS_H>
-__global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ h, int H,
-                                                         const float *__restrict__ rw,
-                                                         const float *__restrict__ rb, int E, int k,
-                                                         float *__restrict__ logits,
-                                                         int32_t *__restrict__ topk_idx,
-                                                         float *__restrict__ topk_w, MoeTables tb, int tables) {
-    extern __shared__ __attribute__((aligned(16))) float lg[];
-    int *sel = reinterpret_cast<int *>(lg + E);
-    double *h64 = reinterpret_cast<double *>(lg + ((E + k + 3) & ~3));
-    const int t = blockIdx.x;
-    const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
-    const float *ht = h + (int64_t)t * H;
-    constexpr bool lds_h = LDS_H;   // H <= ROUTE_LDS_H
-    if (lds_h) {
-        for (int i = threadIdx.x * 4; i < H; i += blockDim.x * 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(ht + i);
-            *reinterpret_cast<double2 *>(h64 + i) = make_double2(v.x, v.y);
-            *reinterpret_cast<double2 *>(h64 + i + 2) = make_double2(v.z, v.w);
-        }
-        __syncthreads();
+// Wave-wide max / min, on every lane: DPP inside each row of 16 lanes (quad
+// xor 1, quad xor 2, half-row mirror, row mirror), then the four rows.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));
+    v = max(v, dpp_u32<0x4E>(v));
+    v = max(v, dpp_u32<0x141>(v));
+    v = max(v, dpp_u32<0x140>(v));
+    const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return max(max(a, b), max(c, d));
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<0xB1>(v));
+    v = min(v, dpp_u32<0x4E>(v));
+    v = min(v, dpp_u32<0x141>(v));
+    v = min(v, dpp_u32<0x140>(v));
+    const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return min(min(a, b), min(c, d));
+}
+
+// Expert selection for token t by one whole wave from its E logits lg (LDS
+// or global): top-k in expert order, gates = softmax over the k selected
+// logits (normaliser summed in choice order), written to topk_idx / topk_w.
+// Lane l holds the keys of experts l + 64 j; each of the k rounds takes the
+// wave's largest key, the lowest index among the experts holding it, and
+// drops that expert from the running. With `tables` (a single token) the
+// wave also writes the expert-major permutation tables of moe_permute_kernel
+// for the token's k assignments.
+// MJ >= (E + 63) / 64: expert slots per lane.
+template <int MJ>
+__device__ __forceinline__ void route_select(const float *lg, int E, int k, int t, int32_t *__restrict__ topk_idx,
+                                             float *__restrict__ topk_w, const MoeTables &tb, int tables) {
+    const int lane = lane_id();
+    const int nj = (E + 63) >> 6;
+    float v[MJ];
+    uint32_t key[MJ];
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = j < nj && e < E ? lg[e] : 0.0f;   // every load issued before the first key
     }
-    constexpr int CH = 8;                  // 16-byte chunks per lane loaded ahead of the sums
-    for (int e = w; e < E; e += nw) {
-        const float *we = rw + (int64_t)e * H;
-        double s = 0.0;
-        // lane l sums elements 256j + 4l + c (j = 0, 1, ..., c = 0..3) in that
-        // order (exact fp64 products); H is a multiple of 4, so a chunk is
-        // either wholly inside the row or wholly past its end
-        for (int i0 = 0; i0 < H; i0 += 256 * CH) {
-            float4 hv[CH], wv[CH];
 #pragma unroll
-            for (int j = 0; j < CH; ++j) {
-                const int i = i0 + 256 * j + 4 * lane;
-                const int ic = i < H ? i : H - 4;      // unconditional loads: no wait per load
-                wv[j] = *reinterpret_cast<const float4 *>(we + ic);
-                if (!lds_h) hv[j] = *reinterpret_cast<const float4 *>(ht + ic);
-            }
-            __builtin_amdgcn_sched_barrier(0);   // every load issued before the first sum
-#pragma unroll
-            for (int j = 0; j < CH; ++j) {
-                const int i = i0 + 256 * j + 4 * lane;
-                const bool in = i < H;           // chunks past H add exact zero products
-                double2 a, b;
-                if (lds_h) {
-                    const int ic = in ? i : 0;
-                    a = *reinterpret_cast<const double2 *>(h64 + ic);
-                    b = *reinterpret_cast<const double2 *>(h64 + ic + 2);
-                } else {
-                    a = make_double2(hv[j].x, hv[j].y);
-                    b = make_double2(hv[j].z, hv[j].w);
-                }
-                s = __builtin_fma(in ? a.x : 0.0, (double)wv[j].x, s);
-                s = __builtin_fma(in ? a.y : 0.0, (double)wv[j].y, s);
-                s = __builtin_fma(in ? b.x : 0.0, (double)wv[j].z, s);
-                s = __builtin_fma(in ? b.y : 0.0, (double)wv[j].w, s);
-            }
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-        if (lane == 0) {
-            float v = (float)s;
-            if (rb) v = v + rb[e];
-            lg[e] = v;
-            logits[(int64_t)t * E + e] = v;
-        }
-    }
-    __syncthreads();
-    if (w != 0) return;
-    float myv = -INFINITY;
+    for (int j = 0; j < MJ; ++j) key[j] = j < nj && lane + 64 * j < E ? route_key(v[j]) : 0u;
     int myi = 0;
-    if (E <= 64) {
-        // lane e ranks expert e against all E (values broadcast with
-        // readlane): rank = number of experts that beat it; the rank-r expert
-        // is choice r
-        const float v = lane < E ? lg[lane] : 0.0f;
-        int rank = 0;
-        for (int j = 0; j < E; ++j)
-            rank += better(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j)), j,
-                           v, lane);
-        if (lane < E && rank < k) sel[rank] = lane;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        if (lane < k) {
-            myi = sel[lane];
-            myv = lg[myi];
-        }
-    } else {
-        // lane l owns experts l, l+64, ...; bit j of `taken` marks expert l+64j as selected
-        uint32_t taken = 0;
-        for (int r = 0; r < k; ++r) {
-            float bv = __builtin_nanf("");   // ranks below every expert
-            int bi = 0x7fffffff;
-            for (int e = lane, j = 0; e < E; e += 64, ++j)
-                if (!((taken >> j) & 1u) && better(lg[e], e, bv, bi)) { bv = lg[e]; bi = e; }
+    float myv = 0.0f;
+    for (int r = 0; r < k; ++r) {
+        // the lane's best: the largest key, the lower j on equal keys
+        uint32_t lk = 0, lj = 0;
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const float ov = __shfl_xor(bv, off, 64);
-                const int oi = __shfl_xor(bi, off, 64);
-                if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-            }
-            if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-            if (lane == r) { myv = bv; myi = bi; }
+        for (int j = 0; j < MJ; ++j) {
+            const bool up = j < nj && key[j] > lk;
+            lk = up ? key[j] : lk;
+            lj = up ? j : lj;
         }
+        const uint32_t top = wave_max_u32(lk);
+        const uint32_t bi = wave_min_u32(lk == top ? (uint32_t)lane + 64u * lj : 0xffffffffu);
+        const int bj = (int)(bi >> 6);
+        float bv = v[0];
+#pragma unroll
+        for (int j = 1; j < MJ; ++j) bv = j == bj ? v[j] : bv;
+        bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bv), (int)(bi & 63)));
+#pragma unroll
+        for (int j = 0; j < MJ; ++j) key[j] = lane + 64 * j == (int)bi ? 0u : key[j];
+        myi = lane == r ? (int)bi : myi;
+        myv = lane == r ? bv : myv;
     }
-    // gates: softmax over the k selected logits, normaliser summed in choice order
-    const float vmax = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, myv), 0));
+    const float vmax = uniform_f(myv, 0);
     const float ex = lane < k ? expf(myv - vmax) : 0.0f;
     float z = 0.0f;
-    for (int j = 0; j < k; ++j) z += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), j));
+    for (int j = 0; j < k; ++j) z += uniform_f(ex, j);
     if (lane < k) {
         topk_idx[(int64_t)t * k + lane] = myi;
         topk_w[(int64_t)t * k + lane] = ex / z;
@@ -210,77 +173,430 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
     if (lane == 0) tb.n_active[0] = k;
 }
 
-// ---------------------------------------------------------------- permute
+__device__ __forceinline__ void route_select_any(const float *lg, int E, int k, int t, int32_t *__restrict__ topk_idx,
+                                                 float *__restrict__ topk_w, const MoeTables &tb, int tables) {
+    if (E <= 64)
+        route_select<1>(lg, E, k, t, topk_idx, topk_w, tb, tables);
+    else if (E <= 128)
+        route_select<2>(lg, E, k, t, topk_idx, topk_w, tb, tables);
+    else if (E <= 256)
+        route_select<4>(lg, E, k, t, topk_idx, topk_w, tb, tables);
+    else
+        route_select<16>(lg, E, k, t, topk_idx, topk_w, tb, tables);
+}
 
-// Stable counting sort of N assignments by expert in one workgroup of 1024
-// threads: per-wave histograms, exclusive offsets in (expert, wave) order,
-// then each wave places its contiguous range in order.
+// LDS of moe_route_kernel: h is staged as fp64 when it fits with the logits;
+// wider rows convert h in registers in every wave.
+constexpr size_t ROUTE_LDS_BYTES = 65536;
+// From this many tokens on, the logits come from moe_route_logits_kernel and
+// the selection from moe_topk_kernel.
+constexpr int ROUTE_TILE_TOKENS = 16;
+// 16-byte chunks per lane and pass of moe_route_kernel: rows of up to 2048
+// elements in one pass.
+constexpr int ROUTE_CH = 8;
+
+// Router of a few tokens: one workgroup per token. h is converted to fp64
+// once (in LDS) and shared by the waves, each of which computes whole expert
+// logits from one read of the expert's router row (the next row is requested
+// before the current one is summed); wave 0 then selects the experts. LDS: E
+// logits, then the row of h as fp64. PART: H is not a
+// multiple of 256 * ROUTE_CH, so the last pass over a row has chunks past
+// its end.
+template <bool LDS_H, bool PART>
+__global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ h, int H,
+                                                         const float *__restrict__ rw,
+                                                         const float *__restrict__ rb, int E, int k,
+                                                         float *__restrict__ logits,
+                                                         int32_t *__restrict__ topk_idx,
+                                                         float *__restrict__ topk_w, MoeTables tb, int tables) {
+    extern __shared__ __attribute__((aligned(16))) float lds_f[];
+    const int t = blockIdx.x;
+    const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
+    double *h64 = reinterpret_cast<double *>(lds_f + ((E + 3) & ~3));
+    const float *ht = h + (int64_t)t * H;
+    if (LDS_H) {
+        for (int i = threadIdx.x * 4; i < H; i += blockDim.x * 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(ht + i);
+            *reinterpret_cast<double2 *>(h64 + i) = make_double2(v.x, v.y);
+            *reinterpret_cast<double2 *>(h64 + i + 2) = make_double2(v.z, v.w);
+        }
+        __syncthreads();
+    }
+    constexpr int CH = ROUTE_CH;
+    // lane l sums elements 256j + 4l + c (j = 0, 1, ..., c = 0..3) in that
+    // order (exact fp64 products); H is a multiple of 4, so a chunk is either
+    // wholly inside the row or wholly past its end
+    auto dot = [&](const float4 (&wv)[CH], const float4 (&hv)[CH], int i0, double &s) {
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int i = i0 + 256 * j + 4 * lane;
+            const bool in = !PART || i < H;      // chunks past H add exact zero products
+            double2 a, b;
+            if (LDS_H) {
+                const int ic = in ? i : 0;
+                a = *reinterpret_cast<const double2 *>(h64 + ic);
+                b = *reinterpret_cast<const double2 *>(h64 + ic + 2);
+            } else {
+                a = make_double2(hv[j].x, hv[j].y);
+                b = make_double2(hv[j].z, hv[j].w);
+            }
+            s = __builtin_fma(in ? a.x : 0.0, (double)wv[j].x, s);
+            s = __builtin_fma(in ? a.y : 0.0, (double)wv[j].y, s);
+            s = __builtin_fma(in ? b.x : 0.0, (double)wv[j].z, s);
+            s = __builtin_fma(in ? b.y : 0.0, (double)wv[j].w, s);
+        }
+    };
+    auto load = [&](float4 (&v)[CH], const float *row, int i0) {
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int i = i0 + 256 * j + 4 * lane;
+            v[j] = *reinterpret_cast<const float4 *>(row + (i < H ? i : H - 4));   // unconditional
+        }
+    };
+    auto finish = [&](int e, double s) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+        if (lane == 0) {
+            float f = (float)s;
+            if (rb) f = f + rb[e];
+            lds_f[e] = f;
+            logits[(int64_t)t * E + e] = f;
+        }
+    };
+    float4 hv[CH];
+    if (H <= 256 * CH) {
+        if (!LDS_H) load(hv, ht, 0);
+        float4 wv[CH];
+        if (w < E) load(wv, rw + (int64_t)w * H, 0);
+        for (int e = w; e < E; e += nw) {
+            const int en = e + nw < E ? e + nw : e;
+            float4 wn[CH];
+            load(wn, rw + (int64_t)en * H, 0);
+            double s = 0.0;
+            dot(wv, hv, 0, s);
+            finish(e, s);
+#pragma unroll
+            for (int j = 0; j < CH; ++j) wv[j] = wn[j];
+        }
+    } else {
+        for (int e = w; e < E; e += nw) {
+            double s = 0.0;
+            for (int i0 = 0; i0 < H; i0 += 256 * CH) {
+                float4 wv[CH];
+                load(wv, rw + (int64_t)e * H, i0);
+                if (!LDS_H) load(hv, ht, i0);
+                __builtin_amdgcn_sched_barrier(0);   // every load issued before the first sum
+                dot(wv, hv, i0, s);
+            }
+            finish(e, s);
+        }
+    }
+    __syncthreads();
+    if (w != 0) return;
+    route_select_any(lds_f, E, k, t, topk_idx, topk_w, tb, tables);
+}
+
+// Tile of the many-token router: each wave covers RL_T tokens x RL_E
+// experts, a workgroup RL_WT x RL_WE such tiles, i.e. RL_TOK token rows and
+// RL_EXP expert rows.
+constexpr int RL_T = 4, RL_E = 8;
+constexpr int RL_WT = 2, RL_WE = 2;
+constexpr int RL_TOK = RL_T * RL_WT, RL_EXP = RL_E * RL_WE;
+constexpr int RL_ROWS = RL_TOK + RL_EXP;   // rows of a 256-element chunk, 1 KiB each
+constexpr int RL_RPW = RL_ROWS / 4;        // rows each wave copies per chunk
+constexpr int RL_STAGES = 3;               // chunks in LDS: one summed, two in flight
+constexpr int RL_PAIRS = 16;               // (token, expert) pairs reduced per LDS round
+constexpr int RL_LD = 68;                  // LDS row of a pair: 64 lane partials + 4 doubles of bank skew
+static_assert(RL_ROWS % 4 == 0 && RL_RPW == 6, "the chunk wait below counts 6 copies per wave");
+static_assert(4 * RL_PAIRS * RL_LD * 8 <= RL_STAGES * RL_ROWS * 1024, "reduction fits the chunk stages");
+
+// Router logits for many tokens, equal bit for bit to moe_route_kernel's:
+// lane l of each wave accumulates, for each (token, expert) pair of its
+// RL_T x RL_E tile, the exact fp64 products of elements 256 j + 4 l + c in
+// (j, c) order. The workgroup's RL_ROWS rows stream through LDS one 256-
+// element chunk at a time, copied straight from global memory
+// (global_load_lds, no registers) two chunks ahead of the one being summed,
+// so the HBM latency is covered without occupancy. Each element is converted
+// to fp64 once per wave tile and used for RL_E (token) or RL_T (expert)
+// products. The 64 lane partials of a pair then meet in LDS and are added in
+// the tree order of the wave reduction (s[l] += s[l + off], off = 32, 16,
+// ..., 1): lane q of a group of four adds the 16 partials of lanes q, q + 4,
+// ... (offsets 32, 16, 8, 4), then the group's four sums are combined
+// across lanes (offsets 2, 1). Logits go to logits[T, E] as fp32 plus the
+// bias. PART: H is not a multiple of 256 (the last chunk is partial).
+template <bool PART>
+__global__ __launch_bounds__(256) void moe_route_logits_kernel(const float *__restrict__ h, int T, int H,
+                                                               const float *__restrict__ rw,
+                                                               const float *__restrict__ rb, int E,
+                                                               float *__restrict__ logits) {
+    __shared__ __attribute__((aligned(16))) float4 stage[RL_STAGES][RL_ROWS][64];
+    const int lane = lane_id(), w = wave_id();
+    const int wt = w / RL_WE, we = w % RL_WE;
+    const int tb = blockIdx.x * RL_TOK, eb = blockIdx.y * RL_EXP;
+    // copies: wave w fills rows w, w + 4, ...; rows past T or E repeat the last one
+    const float *src[RL_RPW];
+#pragma unroll
+    for (int i = 0; i < RL_RPW; ++i) {
+        const int r = w + 4 * i;
+        src[i] = (r < RL_TOK ? h + (int64_t)min(tb + r, T - 1) * H : rw + (int64_t)min(eb + r - RL_TOK, E - 1) * H) +
+                 4 * lane;
+    }
+    const int nch = (H + 255) >> 8;
+    auto issue = [&](int j, int b) {
+        const int off = j << 8;
+        // lanes past the end of a partial chunk copy the row's last 16 bytes
+        const int o = !PART || off + 4 * lane < H ? off : H - 4 - 4 * lane;
+#pragma unroll
+        for (int i = 0; i < RL_RPW; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(src[i] + o),
+                                             (__attribute__((address_space(3))) void *)&stage[b][w + 4 * i][0], 16,
+                                             0, 0);
+    };
+    double acc[RL_T][RL_E];
+#pragma unroll
+    for (int a = 0; a < RL_T; ++a)
+#pragma unroll
+        for (int b = 0; b < RL_E; ++b) acc[a][b] = 0.0;
+    issue(0, 0);
+    if (nch > 1) issue(1, 1);
+    int b = 0;   // stage of chunk j
+    for (int j = 0; j < nch; ++j) {
+        // this wave's copies of chunk j are done once only chunk j + 1's remain
+        if (j + 1 < nch)
+            asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // every wave's copies of chunk j have landed, and every wave has read
+        // chunk j - 1 (its reads completed before its sums), whose stage is
+        // refilled next. A bare barrier: __syncthreads' fence would also wait
+        // for the copies still in flight.
+        asm volatile("s_barrier" ::: "memory");
+        if (j + 2 < nch) issue(j + 2, b == 0 ? 2 : b - 1);
+        // the chunk's rows, read in one block that waits for its own results
+        // (the compiler would otherwise wait for every copy in flight first);
+        // early-clobber outputs keep the addresses alive through the block
+        lq_f4 hv[RL_T], wv[RL_E];
+        const uint32_t ah = (uint32_t)(uintptr_t)&stage[b][wt * RL_T][lane];
+        const uint32_t aw = (uint32_t)(uintptr_t)&stage[b][RL_TOK + we * RL_E][lane];
+        static_assert(RL_T == 4 && RL_E == 8, "the read block below names 4 token and 8 expert rows");
+        asm volatile(
+            "ds_read_b128 %0, %12\n"
+            "ds_read_b128 %1, %12 offset:1024\n"
+            "ds_read_b128 %2, %12 offset:2048\n"
+            "ds_read_b128 %3, %12 offset:3072\n"
+            "ds_read_b128 %4, %13\n"
+            "ds_read_b128 %5, %13 offset:1024\n"
+            "ds_read_b128 %6, %13 offset:2048\n"
+            "ds_read_b128 %7, %13 offset:3072\n"
+            "ds_read_b128 %8, %13 offset:4096\n"
+            "ds_read_b128 %9, %13 offset:5120\n"
+            "ds_read_b128 %10, %13 offset:6144\n"
+            "ds_read_b128 %11, %13 offset:7168\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(hv[0]), "=&v"(hv[1]), "=&v"(hv[2]), "=&v"(hv[3]), "=&v"(wv[0]), "=&v"(wv[1]),
+              "=&v"(wv[2]), "=&v"(wv[3]), "=&v"(wv[4]), "=&v"(wv[5]), "=&v"(wv[6]), "=&v"(wv[7])
+            : "v"(ah), "v"(aw)
+            : "memory");
+        if (PART && j == nch - 1 && (j << 8) + 4 * lane >= H) {
+            // past the end of the row: exact zero products
+            const lq_f4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < RL_T; ++i) hv[i] = z;
+#pragma unroll
+            for (int i = 0; i < RL_E; ++i) wv[i] = z;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            double hd[RL_T], wd[RL_E];
+#pragma unroll
+            for (int i = 0; i < RL_T; ++i) hd[i] = (double)hv[i][c];
+#pragma unroll
+            for (int i = 0; i < RL_E; ++i) wd[i] = (double)wv[i][c];
+#pragma unroll
+            for (int a = 0; a < RL_T; ++a)
+#pragma unroll
+                for (int e = 0; e < RL_E; ++e) acc[a][e] = __builtin_fma(hd[a], wd[e], acc[a][e]);
+        }
+        b = b == RL_STAGES - 1 ? 0 : b + 1;
+    }
+    __syncthreads();   // the stages become the reduction buffer
+    double *rd = reinterpret_cast<double *>(&stage[0][0][0]) + w * RL_PAIRS * RL_LD;
+    const int q = lane & 3, p = lane >> 2;
+#pragma unroll
+    for (int r = 0; r < RL_T * RL_E / RL_PAIRS; ++r) {
+#pragma unroll
+        for (int i = 0; i < RL_PAIRS; ++i) {
+            const int pr = r * RL_PAIRS + i;
+            rd[i * RL_LD + lane] = acc[pr / RL_E][pr % RL_E];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        double v[16];
+#pragma unroll
+        for (int m = 0; m < 16; ++m) v[m] = rd[p * RL_LD + q + 4 * m];
+#pragma unroll
+        for (int half = 8; half >= 1; half >>= 1)
+#pragma unroll
+            for (int m = 0; m < half; ++m) v[m] += v[m + half];
+        double s = v[0];
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 1, 64);
+        const int pr = r * RL_PAIRS + p;
+        const int t = tb + wt * RL_T + pr / RL_E, e = eb + we * RL_E + pr % RL_E;
+        if (q == 0 && t < T && e < E) {
+            float f = (float)s;
+            if (rb) f = f + rb[e];
+            logits[(int64_t)t * E + e] = f;
+        }
+        __builtin_amdgcn_wave_barrier();   // the partials are read before the next round overwrites them
+    }
+}
+
+// Expert selection for many tokens from logits[T, E]: one wave per token.
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float *__restrict__ logits, int T, int E, int k,
+                                                       int32_t *__restrict__ topk_idx,
+                                                       float *__restrict__ topk_w) {
+    const int t = blockIdx.x * 4 + wave_id();
+    if (t >= T) return;
+    route_select_any(logits + (int64_t)t * E, E, k, t, topk_idx, topk_w, MoeTables{}, 0);
+}
+
+// Lanes of the wave whose (live) expert equals this lane's: one ballot per
+// bit of the expert index (nbits = bits of E - 1), each lane keeping the
+// lanes that agree with it on that bit.
+__device__ __forceinline__ uint64_t match_lanes(int e, bool live, int nbits) {
+    uint64_t m = __ballot(live);
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t on = __ballot(bit);
+        m &= bit ? on : ~on;
+    }
+    return m;
+}
+
+// Stable counting sort of the N assignments by expert in one workgroup of
+// 1024 threads. Wave w owns the contiguous range [w per, (w+1) per):
+//   1. per 64 assignments, the lanes with equal experts are matched by
+//      ballots; an assignment's rank among its expert's assignments so far in
+//      the wave is kept (in registers, or in pos[] as scratch until step 4
+//      for long ranges) and the wave's per-expert counts advance in LDS;
+//   2. each expert's wave counts become exclusive bases in wave order;
+//   3. wave 0 scans the expert totals (lane l owns a contiguous run of
+//      experts): offsets, counts, the active list and, for the expert GEMMs,
+//      the tile list (tiles of tile_w consecutive perm positions per expert);
+//   4. every assignment lands at offset[e] + wave base + rank.
+// The result lists the assignments in (expert, a) order.
 __global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__restrict__ idx, int N, int E,
                                                            MoeTables tb) {
-    extern __shared__ int ws[];            // cnt[16][E], run[16][E], total[E], off[E+1]
+    extern __shared__ int ws[];            // cnt[16][E], off[E + 1]
+    constexpr int U = 8;                   // assignments per lane per batch of loads
     const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
     int *cnt = ws;
-    int *run = ws + 16 * E;
-    int *total = ws + 32 * E;
-    int *off = ws + 33 * E;
-    for (int i = threadIdx.x; i < 33 * E + E + 1; i += blockDim.x) ws[i] = 0;
+    int *off = ws + 16 * E;
+    for (int i = threadIdx.x; i < 16 * E; i += blockDim.x) cnt[i] = 0;
     __syncthreads();
+    const int nbits = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 0;
     const int per = (N + nw - 1) / nw;
-    const int a0 = w * per, a1 = min(N, a0 + per);
-    for (int a = a0 + lane; a < a1; a += 64) atomicAdd(&cnt[w * E + idx[a]], 1);
+    const int a0 = min(N, w * per), a1 = min(N, a0 + per);
+    int *wc = cnt + w * E;
+    // a wave range of at most 64 U assignments stays in registers (ev, rv)
+    // until step 4; longer ranges keep the ranks in pos[]
+    const bool held = a1 - a0 <= 64 * U;
+    int ev[U], rv[U];
+    for (int base = a0; base < a1; base += 64 * U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int a = base + 64 * u + lane;
+            ev[u] = a < a1 ? idx[a] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (base + 64 * u >= a1) break;   // uniform
+            const int a = base + 64 * u + lane;
+            const bool live = a < a1;
+            const uint64_t m = match_lanes(ev[u], live, nbits);
+            const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+            const int before = live ? wc[ev[u]] : 0;
+            rv[u] = before + rank;
+            if (live && !held) tb.pos[a] = rv[u];
+            __builtin_amdgcn_wave_barrier();
+            // the highest matching lane advances the expert's count
+            if (live && (m >> lane) == 1) wc[ev[u]] = rv[u] + 1;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
     __syncthreads();
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
         int r = 0;
         for (int ww = 0; ww < nw; ++ww) {
-            int c = cnt[ww * E + e];
-            cnt[ww * E + e] = r;           // exclusive within the expert
+            const int c = cnt[ww * E + e];
+            cnt[ww * E + e] = r;           // exclusive within the expert, wave order
             r += c;
         }
-        total[e] = r;
+        off[e] = r;                        // the expert's total until the scan below
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int o = 0, na = 0, nt = 0;
-        for (int e = 0; e < E; ++e) {
+    if (w == 0) {
+        const int tw = tb.tile_w;
+        const int pe = (E + 63) / 64;
+        const int e0 = min(E, lane * pe), e1 = min(E, e0 + pe);
+        int so = 0, sa = 0, st = 0;
+        for (int e = e0; e < e1; ++e) {
+            const int c = off[e];
+            so += c;
+            sa += c > 0;
+            if (tw > 0) st += (c + tw - 1) / tw;
+        }
+        // inclusive scan over the lanes, then exclusive starts of this lane's run
+        int io = so, ia = sa, it = st;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int po = __shfl_up(io, d, 64), pa = __shfl_up(ia, d, 64), pt = __shfl_up(it, d, 64);
+            if (lane >= d) { io += po; ia += pa; it += pt; }
+        }
+        int o = io - so, na = ia - sa, nt = it - st;
+        for (int e = e0; e < e1; ++e) {
+            const int c = off[e];
             off[e] = o;
             tb.offsets[e] = o;
-            tb.counts[e] = total[e];
-            if (total[e] > 0) tb.active[na++] = e;
-            if (tb.tile_w > 0)
-                for (int p = 0; p < total[e]; p += tb.tile_w) {
+            tb.counts[e] = c;
+            if (c > 0) tb.active[na++] = e;
+            if (tw > 0)
+                for (int p = 0; p < c; p += tw, ++nt) {
                     tb.tile_e[nt] = e;
                     tb.tile_p0[nt] = o + p;
-                    tb.tile_n[nt] = min(tb.tile_w, total[e] - p);
-                    ++nt;
+                    tb.tile_n[nt] = min(tw, c - p);
                 }
-            o += total[e];
+            o += c;
         }
-        off[E] = o;
-        tb.offsets[E] = o;
-        tb.n_active[0] = na;
-        if (tb.tile_w > 0) tb.n_tiles[0] = nt;
+        if (lane == 63) {
+            off[E] = io;
+            tb.offsets[E] = io;
+            tb.n_active[0] = ia;
+            if (tw > 0) tb.n_tiles[0] = it;
+        }
     }
     __syncthreads();
-    for (int base = a0; base < a1; base += 64) {
-        const int a = base + lane;
-        const bool live = a < a1;
-        const int e = live ? idx[a] : -1;
-        int rank = 0;
-        bool last_of_e = true;
-        for (int j = 0; j < 64; ++j) {
-            int ej = __shfl(e, j, 64);
-            if (ej == e && j < lane) ++rank;
-            if (ej == e && j > lane) last_of_e = false;
+    for (int base = a0; base < a1; base += 64 * U) {
+        if (!held) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int a = base + 64 * u + lane;
+                ev[u] = a < a1 ? idx[a] : 0;
+                rv[u] = a < a1 ? tb.pos[a] : 0;
+            }
         }
-        if (live) {
-            const int p = off[e] + cnt[w * E + e] + run[w * E + e] + rank;
-            tb.perm[p] = a;
-            tb.pos[a] = p;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int a = base + 64 * u + lane;
+            if (a < a1) {
+                const int p = off[ev[u]] + wc[ev[u]] + rv[u];
+                tb.perm[p] = a;
+                tb.pos[a] = p;
+            }
         }
-        __builtin_amdgcn_wave_barrier();
-        if (live && last_of_e) run[w * E + e] += rank + 1;
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -679,18 +995,36 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
                void *ws, hipStream_t s) {
     const int64_t I = gu->g.rows / 2;
     MoeTables tb = carve(ws, T, E, k, H, I);
-    const int64_t hpad = H <= ROUTE_LDS_H ? H : 0;   // fp64 copy of h in LDS
-    size_t sh = (size_t)((E + k + 3) & ~3) * 4 + (size_t)hpad * 8;
     const int one = T == 1 && tb.tile_w == 0;   // single token: the router writes the tables
-    if (hpad)
-        hipLaunchKernelGGL(moe_route_kernel<true>, dim3((unsigned)T), dim3(1024), sh, s, h, (int)H, rw, rb, (int)E, k,
-                           tb.logits, topk_idx, topk_w, tb, one);
-    else
-        hipLaunchKernelGGL(moe_route_kernel<false>, dim3((unsigned)T), dim3(1024), sh, s, h, (int)H, rw, rb, (int)E,
-                           k, tb.logits, topk_idx, topk_w, tb, one);
+    if (T >= ROUTE_TILE_TOKENS) {
+        const bool part = H % 256 != 0;
+        const dim3 lgrid((unsigned)((T + RL_TOK - 1) / RL_TOK), (unsigned)((E + RL_EXP - 1) / RL_EXP));
+        if (part)
+            hipLaunchKernelGGL(moe_route_logits_kernel<true>, lgrid, dim3(256), 0, s, h, (int)T, (int)H, rw, rb,
+                               (int)E, tb.logits);
+        else
+            hipLaunchKernelGGL(moe_route_logits_kernel<false>, lgrid, dim3(256), 0, s, h, (int)T, (int)H, rw, rb,
+                               (int)E, tb.logits);
+        LQ_HIP(hipGetLastError());
+        hipLaunchKernelGGL(moe_topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, tb.logits, (int)T,
+                           (int)E, k, topk_idx, topk_w);
+    } else {
+        const size_t head = (size_t)((E + 3) & ~3) * 4;   // logits
+        const bool lds_h = head + (size_t)H * 8 <= ROUTE_LDS_BYTES;
+        const size_t sh = head + (lds_h ? (size_t)H * 8 : 0);
+        const bool part = H % (256 * ROUTE_CH) != 0;
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3((unsigned)T), dim3(1024), sh, s, h, (int)H, rw, rb, (int)E, k, tb.logits,
+                               topk_idx, topk_w, tb, one);
+        };
+        if (lds_h)
+            part ? go(moe_route_kernel<true, true>) : go(moe_route_kernel<true, false>);
+        else
+            part ? go(moe_route_kernel<false, true>) : go(moe_route_kernel<false, false>);
+    }
     LQ_HIP(hipGetLastError());
     if (!one) {
-        size_t sh2 = (size_t)(34 * E + 1) * 4;
+        size_t sh2 = (size_t)(17 * E + 1) * 4;
         hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), sh2, s, topk_idx, (int)(T * k), (int)E, tb);
         LQ_HIP(hipGetLastError());
     }

@@ -76,6 +76,14 @@ class MoELayer:
             device.ptr(ws), ws.numel(), ctypes.c_void_p(device.stream_ptr(stream))))
         return out, idx, gates
 
+    def last_router_logits(self, tokens):
+        """Router logits [tokens, E] (fp32, bias included) of the last forward
+        over `tokens` tokens: the layer's workspace starts with them."""
+        ws = self._ws.get(tokens)
+        if ws is None:
+            raise ValueError(f'no forward over {tokens} tokens yet')
+        return ws[:tokens * self.E * 4].view(device.torch().float32).reshape(tokens, self.E)
+
     def forward(self, h):
         """numpy [T, H] -> numpy (out [T, H], topk_idx [T, k], gates [T, k])."""
         o, i, g = self.forward_device(device.to_device_f32(np.atleast_2d(h)))

@@ -61,10 +61,11 @@ def test_qwen3_moe_style_small_prefill():
 
 
 @pytest.mark.parametrize('t', (12, 14, 8))
-@pytest.mark.parametrize('T', (31, 32, 200))
+@pytest.mark.parametrize('T', (31, 32, 67, 200))
 def test_gemm_path_threshold_and_ragged_tiles(t, T):
     """Both sides of the 32-token switch to the expert GEMM path, with expert
-    token counts that are not multiples of the 64-token tile."""
+    token counts that are not multiples of the 64-token tile (67 and 200
+    tokens: the eight-token router tiles end with a partial one)."""
     from localai_amd import synth
     rng = np.random.default_rng(T * 3 + t)
     E, H, I, k = 16, 512, 256, 4
@@ -159,3 +160,42 @@ def test_mfma_decode_path_shapes(t, k, H, I, T):
     np.testing.assert_array_equal(idx, ridx)
     np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
     assert normwise_rel(out, rout) < 1e-5
+
+
+@pytest.mark.parametrize('T,E,H,k', [
+    (1, 8, 288, 2),       # one token: the per-token router; H ends in a partial 256-chunk
+    (15, 20, 256, 3),     # just below the tiled router
+    (16, 20, 288, 3),     # tiled router, partial chunk, experts not a multiple of 16
+    (37, 80, 320, 5),     # E > 64: DPP top-k; tokens not a multiple of 8
+    (67, 130, 512, 8),    # three expert tiles, the last with 2 experts
+    (40, 1, 256, 1),      # one expert: every assignment matches in the permutation
+])
+def test_router_logits_bit_exact(T, E, H, k):
+    """Router logits (read back from the workspace) equal the canonical sum of
+    oracle/moe.py bit for bit, with a bias, and the selection equals
+    np.lexsort's, including ties planted between experts e and e + 64 (the same
+    lane of the DPP reduction) and between neighbouring experts."""
+    from localai_amd import synth
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(T * 7 + E + H)
+    I, t = 128, 8
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    if E > 2:
+        rw[E - 1] = rw[1]            # tie between 1 and E - 1
+    if E > 64:
+        rw[66] = rw[2]               # tie between lanes' first and second experts
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    if E > 2:
+        bias[E - 1] = bias[1]
+    if E > 64:
+        bias[66] = bias[2]
+    h = synth.activations(rng, T, H)
+    layer = MoELayer(rw, gu, dn, t, E, H, I, k, router_b=bias)
+    out, idx, g = layer.forward(h)
+    got = layer.last_router_logits(T).cpu().numpy()
+    want = (omoe.router_logits(h, rw) + bias[None, :]).astype(np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    ridx, sel = omoe.topk(want, k)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(g, omoe.gates(sel), rtol=1e-5, atol=1e-6)
+    assert np.isfinite(out).all()
