@@ -32,23 +32,68 @@ constexpr int GM_LD = GM_BK + 8;       // LDS row stride in halves (272 B: 16 la
 
 // ---------------------------------------------------------------- activations
 
-// One workgroup per token row. src row = rows_map ? rows_map[t] / k : t.
-// Xh[t, 0..ldh) = f16(X[src, c] * 2^s) (zero past cols); inv[t] = 2^-s.
+// One wave per token row, four rows per workgroup. Row t reads X row
+// src = rows_map ? rows_map[t] / k : t and writes
+//   Xh[t, 0..ldh) = f16(X[src, c] * 2^s) (zero past cols),  inv[t] = 2^-s,
+// with 2^s bringing the row's largest finite magnitude into [2^14, 2^15)
+// (s = 0 for an all-zero or non-finite maximum). Lanes move 8-value groups
+// (two 16-byte loads, one 16-byte store); NG > 0: the lane's NG groups stay
+// in registers between the max and the conversion, NG = 0: the row is read
+// twice. cols is a multiple of 8; vec: X rows are 16-byte aligned.
+template <int NG>
 __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__ X, int64_t ldx, int cols,
-                                                       const int32_t *__restrict__ rows_map, int k,
+                                                       const int32_t *__restrict__ rows_map, int k, int64_t ntok,
                                                        _Float16 *__restrict__ Xh, int ldh,
-                                                       float *__restrict__ inv) {
-    __shared__ float red[4];
-    const int t = blockIdx.x, tid = threadIdx.x;
-    const int64_t src = rows_map ? (int64_t)(rows_map[t] / k) : (int64_t)t;
+                                                       float *__restrict__ inv, int vec) {
+    const int lane = lane_id();
+    const int64_t t = (int64_t)blockIdx.x * 4 + wave_id();
+    if (t >= ntok) return;
+    const int64_t src = rows_map ? (int64_t)(rows_map[t] / k) : t;
     const float *x = X + src * ldx;
-    float m = 0.0f;
-    for (int c = tid; c < cols; c += 256) m = fmaxf(m, fabsf(x[c]));
+    const int ngx = cols >> 3, ng = ldh >> 3;
+    auto load = [&](int gi, lq_f4 &lo, lq_f4 &hi) {
+        if (vec) {
+            lo = *reinterpret_cast<const lq_f4 *>(x + 8 * gi);
+            hi = *reinterpret_cast<const lq_f4 *>(x + 8 * gi + 4);
+        } else {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if ((tid & 63) == 0) red[tid >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+            for (int c = 0; c < 4; ++c) {
+                lo[c] = x[8 * gi + c];
+                hi[c] = x[8 * gi + 4 + c];
+            }
+        }
+    };
+    // the largest magnitude as ordered bits; NaN counts as zero (fmaxf's rule)
+    auto mag = [](const lq_f4 &v) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float f = v[c];   // bit_cast of a vector element would read element 0
+            const uint32_t u = __builtin_bit_cast(uint32_t, f) & 0x7fffffffu;
+            m = max(m, u > 0x7f800000u ? 0u : u);
+        }
+        return m;
+    };
+    constexpr int NR = NG > 0 ? NG : 1;
+    lq_f4 lo[NR], hi[NR];
+    uint32_t mb = 0;
+    if (NG > 0) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int gi = lane + 64 * i;
+            lo[i] = hi[i] = lq_f4{0.f, 0.f, 0.f, 0.f};
+            if (gi < ngx) load(gi, lo[i], hi[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < NR; ++i) mb = max(mb, max(mag(lo[i]), mag(hi[i])));
+    } else {
+        for (int gi = lane; gi < ngx; gi += 64) {
+            lq_f4 l, h;
+            load(gi, l, h);
+            mb = max(mb, max(mag(l), mag(h)));
+        }
+    }
+    const float m = __builtin_bit_cast(float, wave_max_u32(mb));
     int s = 0;
     if (m > 0.0f && m <= 3.4e38f) {
         int e;
@@ -56,9 +101,32 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__
         s = 15 - e;             // m * 2^s in [2^14, 2^15)
         s = s > 120 ? 120 : s < -120 ? -120 : s;
     }
-    _Float16 *xh = Xh + (int64_t)t * ldh;
-    for (int c = tid; c < ldh; c += 256) xh[c] = (_Float16)(c < cols ? ldexpf(x[c], s) : 0.0f);
-    if (tid == 0) inv[t] = ldexpf(1.0f, -s);
+    const float sc = ldexpf(1.0f, s);   // exact power of two: x * sc == ldexpf(x, s) in the f16 range
+    _Float16 *xh = Xh + t * ldh;
+    auto store = [&](int gi, const lq_f4 &l, const lq_f4 &h) {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        h8 o;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            o[c] = (_Float16)(l[c] * sc);
+            o[4 + c] = (_Float16)(h[c] * sc);
+        }
+        *reinterpret_cast<h8 *>(xh + 8 * gi) = o;
+    };
+    if (NG > 0) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int gi = lane + 64 * i;
+            if (gi < ng) store(gi, lo[i], hi[i]);
+        }
+    } else {
+        for (int gi = lane; gi < ng; gi += 64) {
+            lq_f4 l = {0.f, 0.f, 0.f, 0.f}, h = l;
+            if (gi < ngx) load(gi, l, h);
+            store(gi, l, h);
+        }
+    }
+    if (lane == 0) inv[t] = ldexpf(1.0f, -s);
 }
 
 // ---------------------------------------------------------------- weights
@@ -169,7 +237,14 @@ struct GemmArgs {
     int64_t inter;
     const uint8_t *Wt;         // tile form (mfma_core.h) or null; MoE: expert 0
     int64_t wt_bytes;          // tile-form bytes per matrix
+    const int32_t *rows_map;   // null, or: token p reads Xh / inv row rows_map[p] / rows_k
+    int rows_k;
 };
+
+// Xh / inv row of token position p
+__device__ __forceinline__ int64_t gemm_xrow(const GemmArgs &a, int64_t p) {
+    return a.rows_map ? (int64_t)(a.rows_map[p] / a.rows_k) : p;
+}
 
 template <int T, int BN, int MODE>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
@@ -225,7 +300,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     constexpr int XT = 256 / BN;              // threads per token row (2 or 4 or 8)
     constexpr int XV = 128 / XT;              // halves per thread
     const int xr = tid / XT, xp = tid % XT;
-    const int64_t xrow = p0 + (xr < tn ? xr : 0);
+    const int64_t xrow = gemm_xrow(a, p0 + (xr < tn ? xr : 0));
     const _Float16 *xsrc = a.Xh + xrow * a.ldh + XV * xp;
 
     UnitW wreg;
@@ -314,7 +389,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
             const int lt = (BN / 2) * tb + 16 * i + 4 * (lane >> 4) + v;
             if (lt >= tn) continue;
             const int64_t p = p0 + lt;
-            const float sc = a.inv[p];
+            const float sc = a.inv[gemm_xrow(a, p)];
             if constexpr (MODE == GM_MOE_GATE_UP) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
@@ -519,7 +594,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < XN; ++i) {
         const int row = (4 * i + wave) * 4 + (lane >> 4), c = (lane & 15) ^ (row & 15);
-        xsrc[i] = a.Xh + (p0 + (row < tn ? row : 0)) * a.ldh + 8 * c;
+        xsrc[i] = a.Xh + gemm_xrow(a, p0 + (row < tn ? row : 0)) * a.ldh + 8 * c;
     }
     auto load_x = [&](int buf, int64_t step) {
 #pragma unroll
@@ -571,7 +646,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
             const int lt = 16 * i + 4 * (lane >> 4) + v;
             if (lt >= tn) continue;
             const int64_t p = p0 + lt;
-            const float sc = a.inv[p];
+            const float sc = a.inv[gemm_xrow(a, p)];
             if constexpr (MODE == GM_MOE_GATE_UP) {
                 const int64_t r = t0 * MT_ROWS + fr;
                 if (r < a.inter) a.Y[p * a.y_ts + r] = silu(acc[i][0][v] * sc) * (acc[i][1][v] * sc);
@@ -598,8 +673,23 @@ int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok) {
 int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *rows_map, int k, int64_t ntok,
                     _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s) {
     if (ntok <= 0) return LOCALAI_OK;
-    hipLaunchKernelGGL(x_to_f16_kernel, dim3((unsigned)ntok), dim3(256), 0, s, X, ldx, (int)cols, rows_map, k, Xh,
-                       (int)ldh, inv);
+    if (cols % 8 || ldh % 8 || ldh < cols) return fail(LOCALAI_EARG, "f16 rows: cols % 8 != 0");
+    const int vec = (uintptr_t)X % 16 == 0 && ldx % 4 == 0;
+    const int per = (int)((ldh / 8 + 63) / 64);   // 8-value groups per lane
+    const dim3 grid((unsigned)((ntok + 3) / 4));
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, X, ldx, (int)cols, rows_map, k, ntok, Xh, (int)ldh, inv, vec);
+    };
+    if (per <= 1)
+        go(x_to_f16_kernel<1>);
+    else if (per <= 2)
+        go(x_to_f16_kernel<2>);
+    else if (per <= 4)
+        go(x_to_f16_kernel<4>);
+    else if (per <= 8)
+        go(x_to_f16_kernel<8>);
+    else
+        go(x_to_f16_kernel<0>);
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
 }
@@ -653,11 +743,12 @@ int launch_gemm(const lq_geom &g, const uint8_t *W, const uint8_t *Wt, const flo
 int moe_gemm_tile() { return GM_MOE_BN; }
 
 int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, const uint8_t *Wt_all, int64_t wt_bytes, bool gate_up,
-                    const _Float16 *Xh, int64_t ldh, const float *inv, float *Y, int64_t y_ts, int64_t inter,
-                    const int32_t *tile_e, const int32_t *tile_p0, const int32_t *tile_n, const int32_t *n_tiles,
-                    int max_tiles, hipStream_t s) {
+                    const _Float16 *Xh, int64_t ldh, const float *inv, const int32_t *rows_map, int rows_k,
+                    float *Y, int64_t y_ts, int64_t inter, const int32_t *tile_e, const int32_t *tile_p0,
+                    const int32_t *tile_n, const int32_t *n_tiles, int max_tiles, hipStream_t s) {
     GemmArgs a{};
     a.g = g; a.W = Wall; a.Xh = Xh; a.ldh = (int)ldh; a.inv = inv; a.Y = Y; a.y_ts = y_ts; a.y_rs = 1;
+    a.rows_map = rows_map; a.rows_k = rows_k;
     a.tile_e = tile_e; a.tile_p0 = tile_p0; a.tile_n = tile_n; a.n_tiles = n_tiles; a.inter = inter;
     a.Wt = Wt_all; a.wt_bytes = wt_bytes;
     if (max_tiles <= 0) return LOCALAI_OK;

@@ -48,8 +48,8 @@ struct MoeTables {
     int32_t *tile_p0;   // [max_tiles] first perm position of the tile
     int32_t *tile_n;    // [max_tiles] tokens in the tile (<= tile width)
     int32_t *n_tiles;   // [1]
-    _Float16 *xh_gu;    // [N, ldh(H)] f16 token rows of h in perm order
-    float *inv_gu;      // [N]
+    _Float16 *xh_gu;    // [T, ldh(H)] f16 token rows of h
+    float *inv_gu;      // [T]
     _Float16 *xh_dn;    // [N, ldh(I)] f16 act rows
     float *inv_dn;      // [N]
     int max_tiles;
@@ -67,33 +67,6 @@ __device__ __forceinline__ uint32_t route_key(float v) {
     const uint32_t b = __builtin_bit_cast(uint32_t, v);
     const uint32_t m = b == 0x80000000u ? 0x80000000u : (b & 0x80000000u ? ~b : b | 0x80000000u);
     return v != v ? 1u : m;
-}
-
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
-}
-
-// Wave-wide max / min, on every lane: DPP inside each row of 16 lanes (quad
-// xor 1, quad xor 2, half-row mirror, row mirror), then the four rows.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, dpp_u32<0xB1>(v));
-    v = max(v, dpp_u32<0x4E>(v));
-    v = max(v, dpp_u32<0x141>(v));
-    v = max(v, dpp_u32<0x140>(v));
-    const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-    const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-    return max(max(a, b), max(c, d));
-}
-
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-    v = min(v, dpp_u32<0xB1>(v));
-    v = min(v, dpp_u32<0x4E>(v));
-    v = min(v, dpp_u32<0x141>(v));
-    v = min(v, dpp_u32<0x140>(v));
-    const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-    const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-    return min(min(a, b), min(c, d));
 }
 
 // Expert selection for token t by one whole wave from its E logits lg (LDS
@@ -858,8 +831,8 @@ size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I
     if (T >= MOE_GEMM_TOKENS) {
         const int64_t mt = moe_max_tiles(N, E, moe_gemm_tile());
         s += align256(mt * 4) * 3 + align256(4);
-        s += align256(N * f16_stride(H) * 2) + align256(N * 4);
-        s += align256(N * f16_stride(I) * 2) + align256(N * 4);
+        s += align256(T * f16_stride(H) * 2) + align256(T * 4);      // f16 rows of h
+        s += align256(N * f16_stride(I) * 2) + align256(N * 4);      // f16 act rows
     }
     return s;
 }
@@ -886,8 +859,8 @@ static MoeTables carve(void *ws, int64_t T, int64_t E, int64_t k, int64_t H, int
         tb.tile_p0 = (int32_t *)take(tb.max_tiles * 4);
         tb.tile_n = (int32_t *)take(tb.max_tiles * 4);
         tb.n_tiles = (int32_t *)take(4);
-        tb.xh_gu = (_Float16 *)take(N * f16_stride(H) * 2);
-        tb.inv_gu = (float *)take(N * 4);
+        tb.xh_gu = (_Float16 *)take(T * f16_stride(H) * 2);
+        tb.inv_gu = (float *)take(T * 4);
         tb.xh_dn = (_Float16 *)take(N * f16_stride(I) * 2);
         tb.inv_dn = (float *)take(N * 4);
     }
@@ -1033,15 +1006,16 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
         // prefill: gathered f16 token rows -> expert GEMMs on MFMA
         const int64_t N = T * k;
         if (gu->g.cols != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe: expert shapes");
-        if (int st = launch_x_to_f16(h, H, H, tb.perm, k, N, tb.xh_gu, f16_stride(H), tb.inv_gu, s)) return st;
+        // gate_up reads the f16 rows of h through the permutation (perm[p] / k)
+        if (int st = launch_x_to_f16(h, H, H, nullptr, 1, T, tb.xh_gu, f16_stride(H), tb.inv_gu, s)) return st;
         if (int st = launch_moe_gemm(gu->g, gu->data, gu->tiles, gu->tile_bytes, true, tb.xh_gu, f16_stride(H),
-                                     tb.inv_gu, tb.act, I, I,
-                                     tb.tile_e, tb.tile_p0, tb.tile_n, tb.n_tiles, tb.max_tiles, s))
+                                     tb.inv_gu, tb.perm, k, tb.act, I, I, tb.tile_e, tb.tile_p0, tb.tile_n,
+                                     tb.n_tiles, tb.max_tiles, s))
             return st;
         if (int st = launch_x_to_f16(tb.act, I, I, nullptr, 1, N, tb.xh_dn, f16_stride(I), tb.inv_dn, s)) return st;
         if (int st = launch_moe_gemm(dn->g, dn->data, dn->tiles, dn->tile_bytes, false, tb.xh_dn, f16_stride(I),
-                                     tb.inv_dn, tb.ysl, H, I,
-                                     tb.tile_e, tb.tile_p0, tb.tile_n, tb.n_tiles, tb.max_tiles, s))
+                                     tb.inv_dn, nullptr, 1, tb.ysl, H, I, tb.tile_e, tb.tile_p0, tb.tile_n,
+                                     tb.n_tiles, tb.max_tiles, s))
             return st;
     } else if (moe_mfma_ok(gu, dn, h, H, I)) {
         // decode on MFMA; one token with k <= 2 folds the combine into down
