@@ -198,14 +198,23 @@ __device__ __forceinline__ int window_pos(int u, int j) {
 
 typedef _Float16 lq_h2 __attribute__((ext_vector_type(2)));
 
+// Bytes 0, 1 (lo) or 2, 3 (hi) of w below the exponent byte 0x64: two f16
+// values 1024 + byte (one v_perm_b32; selector bytes 0..3 pick w's bytes,
+// 4 picks the first byte of 0x64646464).
+__device__ __forceinline__ uint32_t f16_bytes_lo(uint32_t w) {
+    return __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);
+}
+__device__ __forceinline__ uint32_t f16_bytes_hi(uint32_t w) {
+    return __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);
+}
+
 // Q8_0 weights straight to f16 pairs: byte q + 128 under the f16 exponent of
 // 1024 reads as 1152 + q (exact), minus 1152 gives q exactly, and one f16
 // multiply by d rounds d * q once (the same value as rounding the exact fp32
 // product). Four int8 quants in `w` -> two f16 pairs.
 __device__ __forceinline__ void q8_pairs(uint32_t w, lq_h2 d2, uint32_t &lo, uint32_t &hi) {
     const uint32_t b = w ^ 0x80808080u;
-    const uint32_t l = (b & 0xFFu) | ((b & 0xFF00u) << 8) | 0x64006400u;
-    const uint32_t h = ((b >> 16) & 0xFFu) | ((b >> 8) & 0xFF0000u) | 0x64006400u;
+    const uint32_t l = f16_bytes_lo(b), h = f16_bytes_hi(b);
     const lq_h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
     lo = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(lq_h2, l) - off) * d2);
     hi = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(lq_h2, h) - off) * d2);
@@ -451,12 +460,6 @@ __device__ __forceinline__ GtRaw<T> gt_load(const uint8_t *blk, int half, int la
     return r;
 }
 
-__device__ __forceinline__ uint32_t gt_pk(float a, float b) {
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
-}
-
 // B operand (8 f16) of slice kk (0..3) of half HALF of the block, lane group q
 template <int T, int HALF, int KK>
 __device__ __forceinline__ lq_h8 gt_b(const GtRaw<T> &r, int q) {
@@ -474,13 +477,23 @@ __device__ __forceinline__ lq_h8 gt_b(const GtRaw<T> &r, int q) {
             sc = ((s8 >> (8 * j)) & 15u) | (((s0 >> (8 * j + 6)) & 3u) << 4);
             mn = ((s8 >> (8 * j + 4)) & 15u) | (((s4 >> (8 * j + 6)) & 3u) << 4);
         }
-        const float a = f16_to_f32(r.hd.x) * (float)sc, b = f16_to_f32(r.hd.x >> 16) * (float)mn;
+        // packed f16: {sc, mn} exactly (0x6400 | n reads as 1024 + n), times
+        // {d, dmin} rounds d * sc and dmin * mn once each; a value is then
+        // round(a * q - b) from the exact q (one fused multiply-add)
+        const lq_h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const lq_h2 scmn = __builtin_bit_cast(lq_h2, sc | (mn << 16) | 0x64006400u) - k1024;
+        const lq_h2 ab = __builtin_bit_cast(lq_h2, r.hd.x) * scmn;
+        const lq_h2 a2 = {ab.x, ab.x}, nb2 = {-ab.y, -ab.y};
         const uint32_t w0 = ((hb ? r.qs.z : r.qs.x) >> (4 * nib)) & 0x0F0F0F0Fu;
         const uint32_t w1 = ((hb ? r.qs.w : r.qs.y) >> (4 * nib)) & 0x0F0F0F0Fu;
-        o.x = gt_pk(__builtin_fmaf(a, (float)(w0 & 255u), -b), __builtin_fmaf(a, (float)((w0 >> 8) & 255u), -b));
-        o.y = gt_pk(__builtin_fmaf(a, (float)((w0 >> 16) & 255u), -b), __builtin_fmaf(a, (float)(w0 >> 24), -b));
-        o.z = gt_pk(__builtin_fmaf(a, (float)(w1 & 255u), -b), __builtin_fmaf(a, (float)((w1 >> 8) & 255u), -b));
-        o.w = gt_pk(__builtin_fmaf(a, (float)((w1 >> 16) & 255u), -b), __builtin_fmaf(a, (float)(w1 >> 24), -b));
+        auto pair = [&](uint32_t bits) {
+            const lq_h2 q = __builtin_bit_cast(lq_h2, bits) - k1024;
+            return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a2, nb2));
+        };
+        o.x = pair(f16_bytes_lo(w0));
+        o.y = pair(f16_bytes_hi(w0));
+        o.z = pair(f16_bytes_lo(w1));
+        o.w = pair(f16_bytes_hi(w1));
     } else if constexpr (T == LQ_Q6_K) {
         // slice g = 4 HALF + KK: values 128 HALF + 32 KK + 8q .. ; ql nibble KK / 2 of
         // bytes 8 (KK % 2) ..; qh bits 2 KK of bytes 8 HALF ..; sub-block 2g + q / 2
@@ -493,12 +506,18 @@ __device__ __forceinline__ lq_h8 gt_b(const GtRaw<T> &r, int q) {
         // sub-blocks 2g and 2g + 1 share scale dword g / 2
         const uint32_t sw = (g >> 1) == 0 ? r.sc.x : (g >> 1) == 1 ? r.sc.y : (g >> 1) == 2 ? r.sc.z : r.sc.w;
         const int sbyte = ((2 * g) & 3) + (q >> 1);
-        const float dsc = f16_to_f32(r.d) * (float)(int)__builtin_amdgcn_sbfe((int)sw, 8 * sbyte, 8);
-        const float off = -32.0f * dsc;
-        o.x = gt_pk(__builtin_fmaf(dsc, (float)(w0 & 255u), off), __builtin_fmaf(dsc, (float)((w0 >> 8) & 255u), off));
-        o.y = gt_pk(__builtin_fmaf(dsc, (float)((w0 >> 16) & 255u), off), __builtin_fmaf(dsc, (float)(w0 >> 24), off));
-        o.z = gt_pk(__builtin_fmaf(dsc, (float)(w1 & 255u), off), __builtin_fmaf(dsc, (float)((w1 >> 8) & 255u), off));
-        o.w = gt_pk(__builtin_fmaf(dsc, (float)((w1 >> 16) & 255u), off), __builtin_fmaf(dsc, (float)(w1 >> 24), off));
+        // packed f16: 1024 + q minus 1056 is q - 32 exactly; times d * sc
+        // (rounded once) rounds each value once
+        const _Float16 dsc = __builtin_bit_cast(_Float16, (uint16_t)(r.d & 0xFFFFu)) *
+                             (_Float16)(int)__builtin_amdgcn_sbfe((int)sw, 8 * sbyte, 8);
+        const lq_h2 d2 = {dsc, dsc}, k1056 = {(_Float16)1056.0f, (_Float16)1056.0f};
+        auto pair = [&](uint32_t bits) {
+            return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(lq_h2, bits) - k1056) * d2);
+        };
+        o.x = pair(f16_bytes_lo(w0));
+        o.y = pair(f16_bytes_hi(w0));
+        o.z = pair(f16_bytes_lo(w1));
+        o.w = pair(f16_bytes_hi(w1));
     } else {
         // GGML block 4 HALF + KK: piece KK / 2 of the half, bytes 8 (KK % 2) ..
         const uint4 pc = (KK >> 1) ? r.p1 : r.p0;
