@@ -120,7 +120,8 @@ int localai_hip_matmul(const localai_qmat *m, int64_t expert, const float *x_dev
 
 /* ---- MoE expert layer ---------------------------------------------------- */
 
-/* Bytes of device workspace localai_hip_moe_forward needs for these sizes. */
+/* Bytes of device workspace localai_hip_moe_forward needs for these sizes.
+ * Calls that run at the same time need separate workspaces. */
 int64_t localai_hip_moe_workspace_size(int64_t tokens, int64_t experts, int top_k,
                                        int64_t hidden, int64_t inter);
 

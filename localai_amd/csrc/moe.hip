@@ -54,6 +54,21 @@ struct MoeTables {
     float *inv_dn;      // [N]
     int max_tiles;
     int tile_w;         // tokens per tile (0: matvec path, no tile list)
+    uint32_t *sync;     // counters of the fused one-token layer (1 KiB)
+};
+
+// Counter block of the fused one-token expert kernel (moe_decode1_kernel),
+// in the workspace, zeroed by the router kernel that runs before it:
+// D1_NCNT gate_up completion counters (gate_up tile r counts on r % D1_NCNT,
+// so no counter takes more than a few dozen atomics), a counter of full
+// counters, the all-done flag the down tiles poll, and an error word, each
+// on a 128-byte line of its own.
+constexpr int D1_NCNT = 16, D1_LINE = 32;
+enum {
+    D1_FULL = D1_NCNT * D1_LINE,
+    D1_DONE = D1_FULL + D1_LINE,
+    D1_ERROR = D1_DONE + D1_LINE,
+    D1_WORDS = D1_ERROR + D1_LINE
 };
 
 // ------------------------------------------------------------------ route
@@ -168,25 +183,36 @@ constexpr int ROUTE_TILE_TOKENS = 16;
 // elements in one pass.
 constexpr int ROUTE_CH = 8;
 
-// Router of a few tokens: one workgroup per token. h is converted to fp64
+// Router of one token t by a whole workgroup (route_token; moe_route_kernel
+// runs one workgroup per token for a few tokens). h is converted to fp64
 // once (in LDS) and shared by the waves, each of which computes whole expert
 // logits from one read of the expert's router row (the next row is requested
 // before the current one is summed); wave 0 then selects the experts. LDS: E
 // logits, then the row of h as fp64. PART: H is not a
 // multiple of 256 * ROUTE_CH, so the last pass over a row has chunks past
 // its end.
-template <bool LDS_H, bool PART>
-__global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ h, int H,
-                                                         const float *__restrict__ rw,
-                                                         const float *__restrict__ rb, int E, int k,
-                                                         float *__restrict__ logits,
-                                                         int32_t *__restrict__ topk_idx,
-                                                         float *__restrict__ topk_w, MoeTables tb, int tables) {
-    extern __shared__ __attribute__((aligned(16))) float lds_f[];
-    const int t = blockIdx.x;
+template <bool LDS_H, bool PART, bool LEAN = false>
+__device__ __forceinline__ void route_token(const float *__restrict__ h, int H, const float *__restrict__ rw,
+                                            const float *__restrict__ rb, int E, int k, float *__restrict__ logits,
+                                            int32_t *__restrict__ topk_idx, float *__restrict__ topk_w,
+                                            const MoeTables &tb, int tables, int t, float *lds_f) {
     const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
     double *h64 = reinterpret_cast<double *>(lds_f + ((E + 3) & ~3));
     const float *ht = h + (int64_t)t * H;
+    constexpr int CH = ROUTE_CH;
+    // one pass per expert (H <= 256 CH) with the next expert's row requested
+    // before the current one is summed; LEAN (fewer registers) or longer
+    // rows: passes of 256 CH elements, one row at a time
+    const bool onepass = !LEAN && H <= 256 * CH;
+    auto load = [&](float4 (&v)[CH], const float *row, int i0) {
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int i = i0 + 256 * j + 4 * lane;
+            v[j] = *reinterpret_cast<const float4 *>(row + (i < H ? i : H - 4));   // unconditional
+        }
+    };
+    float4 wv[CH];
+    if (onepass && w < E) load(wv, rw + (int64_t)w * H, 0);   // in flight while h is staged
     if (LDS_H) {
         for (int i = threadIdx.x * 4; i < H; i += blockDim.x * 4) {
             const float4 v = *reinterpret_cast<const float4 *>(ht + i);
@@ -195,7 +221,6 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
         }
         __syncthreads();
     }
-    constexpr int CH = ROUTE_CH;
     // lane l sums elements 256j + 4l + c (j = 0, 1, ..., c = 0..3) in that
     // order (exact fp64 products); H is a multiple of 4, so a chunk is either
     // wholly inside the row or wholly past its end
@@ -219,13 +244,6 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
             s = __builtin_fma(in ? b.y : 0.0, (double)wv[j].w, s);
         }
     };
-    auto load = [&](float4 (&v)[CH], const float *row, int i0) {
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-            const int i = i0 + 256 * j + 4 * lane;
-            v[j] = *reinterpret_cast<const float4 *>(row + (i < H ? i : H - 4));   // unconditional
-        }
-    };
     auto finish = [&](int e, double s) {
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
@@ -237,10 +255,8 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
         }
     };
     float4 hv[CH];
-    if (H <= 256 * CH) {
+    if (onepass) {
         if (!LDS_H) load(hv, ht, 0);
-        float4 wv[CH];
-        if (w < E) load(wv, rw + (int64_t)w * H, 0);
         for (int e = w; e < E; e += nw) {
             const int en = e + nw < E ? e + nw : e;
             float4 wn[CH];
@@ -255,7 +271,6 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
         for (int e = w; e < E; e += nw) {
             double s = 0.0;
             for (int i0 = 0; i0 < H; i0 += 256 * CH) {
-                float4 wv[CH];
                 load(wv, rw + (int64_t)e * H, i0);
                 if (!LDS_H) load(hv, ht, i0);
                 __builtin_amdgcn_sched_barrier(0);   // every load issued before the first sum
@@ -265,8 +280,20 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
         }
     }
     __syncthreads();
-    if (w != 0) return;
-    route_select_any(lds_f, E, k, t, topk_idx, topk_w, tb, tables);
+    if (w == 0) route_select_any(lds_f, E, k, t, topk_idx, topk_w, tb, tables);
+}
+
+template <bool LDS_H, bool PART>
+__global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ h, int H,
+                                                         const float *__restrict__ rw,
+                                                         const float *__restrict__ rb, int E, int k,
+                                                         float *__restrict__ logits,
+                                                         int32_t *__restrict__ topk_idx,
+                                                         float *__restrict__ topk_w, MoeTables tb, int tables) {
+    extern __shared__ __attribute__((aligned(16))) float lds_f[];
+    if (tables)   // one token: the counter block of the fused expert kernel that follows
+        for (int i = threadIdx.x; i < D1_WORDS; i += blockDim.x) tb.sync[i] = 0u;
+    route_token<LDS_H, PART>(h, H, rw, rb, E, k, logits, topk_idx, topk_w, tb, tables, blockIdx.x, lds_f);
 }
 
 // Tile of the many-token router: each wave covers RL_T tokens x RL_E
@@ -806,6 +833,143 @@ __global__ void moe_combine_kernel(const float *__restrict__ ysl, const int32_t 
     out[(int64_t)t * H + hcol] = s;
 }
 
+// ------------------------------------------------- one-token decode, fused
+
+// Bound on every wait of the fused layer (seconds of polling): a wait that
+// runs out sets D1_ERROR and its workgroup skips its stores (wrong output
+// instead of a hang).
+constexpr int D1_SPIN_LIMIT = 1 << 22;
+
+// Data handed between workgroups of the fused layer moves with device-
+// coherent (relaxed, device-scope atomic) loads and stores, which bypass the
+// per-XCD caches; a store of a flag follows the data stores' completion
+// (vmcnt(0)). No acquire or release fences: on this GPU each would
+// invalidate or write back a whole XCD's L2.
+template <typename V>
+__device__ __forceinline__ V d1_get(const V *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V>
+__device__ __forceinline__ void d1_put(V *p, V v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void d1_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Whole workgroup: wait until the all-done flag is set. One thread polls: a
+// first sleep of about 8000 cycles (the gate_up tiles take several times
+// that), then about 1000 cycles between polls; the others wait at the
+// barrier. false: the wait ran out. flag: one int of LDS.
+__device__ __forceinline__ bool d1_wait_done(uint32_t *sync, int *flag) {
+    if (threadIdx.x == 0) {
+        int ok = 0;
+        __builtin_amdgcn_s_sleep(127);
+        for (int n = 0; n < D1_SPIN_LIMIT; ++n) {
+            if (d1_get(sync + D1_DONE) != 0u) {
+                ok = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(15);
+        }
+        if (!ok) d1_put(sync + D1_ERROR, 1u);
+        *flag = ok;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
+// gate_up tile r of n_gu: count it done. The tile that fills its counter
+// (its share: the tiles r' < n_gu with r' % D1_NCNT == r % D1_NCNT) counts a
+// full counter; the tile that fills the last counter sets the flag.
+__device__ __forceinline__ void d1_count_gu(uint32_t *sync, int r, int n_gu) {
+    const int c = r % D1_NCNT;
+    const uint32_t share = (uint32_t)((n_gu - c + D1_NCNT - 1) / D1_NCNT);
+    const int ncnt = n_gu < D1_NCNT ? n_gu : D1_NCNT;
+    const uint32_t before =
+        __hip_atomic_fetch_add(sync + c * D1_LINE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before + 1 == share) {
+        const uint32_t full =
+            __hip_atomic_fetch_add(sync + D1_FULL, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (full + 1 == (uint32_t)ncnt) d1_put(sync + D1_DONE, 1u);
+    }
+}
+
+// x of the wave's super-blocks (as mt_load_x) with device-coherent loads
+template <int SPW>
+__device__ __forceinline__ void d1_load_x(float4 (&xv)[SPW], const float *x, int nb, int sb0, int lane) {
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+        const int sb = sb0 + k < nb ? sb0 + k : nb - 1;
+        const uint64_t *p = reinterpret_cast<const uint64_t *>(x + 256 * (int64_t)sb + 4 * lane);
+        const uint64_t lo = d1_get(p), hi = d1_get(p + 1);
+        xv[k] = make_float4(__builtin_bit_cast(float, (uint32_t)lo), __builtin_bit_cast(float, (uint32_t)(lo >> 32)),
+                            __builtin_bit_cast(float, (uint32_t)hi), __builtin_bit_cast(float, (uint32_t)(hi >> 32)));
+    }
+}
+
+// The expert part of the MoE layer for one token with k <= 2 in one launch,
+// after the router (moe_route_kernel, which wrote topk_idx / topk_w and
+// zeroed the counter block). Workgroup r:
+//   r < n_gu          gate_up tile i of slot s (n_gu = k * inter / 16): the
+//                     expert's weights, act[s] rows; clears its share of out;
+//                     counts itself done
+//   r >= n_gu         down tile i of slot s: weights requested at once (they
+//                     stream beside gate_up's), then waits for every gate_up
+//                     tile; out += gate * y
+// Workgroups start in id order, so every gate_up tile has started before a
+// down tile waits (and every wait is bounded). Two additions onto zero give
+// the same sum in either order, so out does not depend on which down tile
+// lands first. 8 waves; SPWG / SPWD super-blocks per wave for gate_up / down.
+// LDS: the mt_pass regions.
+template <int TYPE, int SPWG, int SPWD>
+__global__ __launch_bounds__(512) void moe_decode1_kernel(
+    const float *__restrict__ h, int H, int E, int k, const uint8_t *__restrict__ gu_t, int64_t gu_bytes, int nbg,
+    int64_t inter, const uint8_t *__restrict__ dn_t, int64_t dn_bytes, int nbd,
+    const int32_t *__restrict__ topk_idx, const float *__restrict__ topk_w, float *__restrict__ out, MoeTables tb,
+    uint32_t *__restrict__ sync) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int flag;
+    const int r = blockIdx.x;
+    const int lane = lane_id(), w = wave_id();
+    const int gtiles = (int)(inter / MT_ROWS), dtiles = (H + MT_ROWS - 1) / MT_ROWS;
+    const int n_gu = k * gtiles;
+    if (r < n_gu) {
+        const int s = r / gtiles, i = r % gtiles;
+        const int sb0 = w * SPWG, nsb = mt_nsb(nbg, sb0, SPWG);
+        const int e = min(max(topk_idx[s], 0), E - 1);
+        const uint8_t *We = gu_t + (int64_t)e * gu_bytes;
+        const int64_t tb_bytes = (int64_t)nbg * mt_block_bytes(TYPE);
+        MtW<TYPE> wt[2][SPWG];
+        mt_load_tile<TYPE, SPWG>(wt[0], We + i * tb_bytes, nbg, sb0, nsb, lane);
+        mt_load_tile<TYPE, SPWG>(wt[1], We + (gtiles + i) * tb_bytes, nbg, sb0, nsb, lane);
+        float4 xv[1][SPWG];
+        mt_load_x<SPWG>(xv[0], h, nbg, sb0, lane);
+        float *fin;
+        mt_pass<TYPE, SPWG, 2, 1>(wt, xv, nsb, smem, fin);
+        const int n = threadIdx.x;
+        if (n < MT_ROWS) d1_put(tb.act + (int64_t)s * inter + i * MT_ROWS + n, silu(fin[n]) * fin[MT_ROWS + n]);
+        const int per = (H + n_gu - 1) / n_gu;   // this tile's share of out
+        for (int c = r * per + n; c < (r + 1) * per && c < H; c += blockDim.x) d1_put(out + c, 0.0f);
+        d1_drain();
+        __syncthreads();
+        if (threadIdx.x == 0) d1_count_gu(sync, r, n_gu);
+        return;
+    }
+    const int j = r - n_gu, s = j / dtiles, i = j % dtiles;
+    const int sb0 = w * SPWD, nsb = mt_nsb(nbd, sb0, SPWD);
+    const int e = min(max(topk_idx[s], 0), E - 1);
+    const float gate = topk_w[s];
+    MtW<TYPE> wt[1][SPWD];
+    mt_load_tile<TYPE, SPWD>(wt[0], dn_t + (int64_t)e * dn_bytes + i * (int64_t)nbd * mt_block_bytes(TYPE), nbd, sb0,
+                             nsb, lane);
+    const bool ok = d1_wait_done(sync, &flag);
+    float4 xv[1][SPWD];
+    d1_load_x<SPWD>(xv[0], tb.act + (int64_t)s * inter, nbd, sb0, lane);
+    float *fin;
+    mt_pass<TYPE, SPWD, 1, 1>(wt, xv, nsb, smem, fin);
+    const int n = threadIdx.x;
+    if (n < MT_ROWS && i * MT_ROWS + n < H && ok) atomicAdd(out + i * MT_ROWS + n, gate * fin[n]);
+}
+
 // ---------------------------------------------------------------- host side
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -824,6 +988,7 @@ size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I
     const int64_t N = T * k;
     size_t s = 0;
     s += align256(T * E * 4);                                        // logits
+    s += 1024;                                                       // fused-layer counters
     s += align256(E * 4) * 2 + align256((E + 1) * 4) + align256(4);  // counts, offsets, active, n_active
     s += align256(N * 4) * 2;                                        // perm, pos
     s += align256(N * I * 4);                                        // act
@@ -843,6 +1008,7 @@ static MoeTables carve(void *ws, int64_t T, int64_t E, int64_t k, int64_t H, int
     MoeTables tb{};
     auto take = [&](size_t n) { uint8_t *q = p; p += align256(n); return q; };
     tb.logits = (float *)take(T * E * 4);
+    tb.sync = (uint32_t *)take(D1_WORDS * 4);
     tb.counts = (int32_t *)take(E * 4);
     tb.offsets = (int32_t *)take((E + 1) * 4);
     tb.active = (int32_t *)take(E * 4);
@@ -963,6 +1129,38 @@ static int launch_moe_mfma_t(const localai_qmat *gu, const localai_qmat *dn, con
     return LOCALAI_OK;
 }
 
+// super-blocks per wave of an 8-wave workgroup over nb blocks (nb <= 32)
+static int d1_spw(int64_t nb) {
+    const int64_t v = (nb + 7) / 8;
+    return v <= 1 ? 1 : v <= 2 ? 2 : 4;
+}
+
+template <int TYPE, int SG, int SD>
+static void launch_decode1_k(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
+                             int64_t H, int64_t E, int k, int64_t I, const int32_t *topk_idx, const float *topk_w,
+                             float *out, hipStream_t s) {
+    const size_t a = mt_lds_bytes(TYPE, 8, SG, 1, 2), b = mt_lds_bytes(TYPE, 8, SD, 1, 1);
+    const unsigned grid = (unsigned)(k * (I / MT_ROWS) + k * ((H + MT_ROWS - 1) / MT_ROWS));
+    hipLaunchKernelGGL((moe_decode1_kernel<TYPE, SG, SD>), dim3(grid), dim3(512), a > b ? a : b, s, h, (int)H,
+                       (int)E, k, gu->tiles, gu->tile_bytes, (int)gu->g.nb, I, dn->tiles, dn->tile_bytes,
+                       (int)dn->g.nb, topk_idx, topk_w, out, tb, tb.sync);
+}
+
+template <int TYPE>
+static int launch_decode1_t(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
+                            int64_t H, int64_t E, int k, int64_t I, const int32_t *topk_idx, const float *topk_w,
+                            float *out, hipStream_t s) {
+    const int sg = d1_spw(gu->g.nb), sd = d1_spw(dn->g.nb);
+#define LQ_D1(SG, SD)                                                                                       \
+    if (sg == SG && sd == SD)                                                                               \
+        launch_decode1_k<TYPE, SG, SD>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
+    LQ_D1(1, 1) else LQ_D1(1, 2) else LQ_D1(1, 4) else LQ_D1(2, 1) else LQ_D1(2, 2) else LQ_D1(2, 4)
+    else LQ_D1(4, 1) else LQ_D1(4, 2) else LQ_D1(4, 4)
+#undef LQ_D1
+    LQ_HIP(hipGetLastError());
+    return LOCALAI_OK;
+}
+
 int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const float *rb, int64_t E, int k,
                const localai_qmat *gu, const localai_qmat *dn, float *out, int32_t *topk_idx, float *topk_w,
                void *ws, hipStream_t s) {
@@ -1018,8 +1216,13 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
                                      tb.n_tiles, tb.max_tiles, s))
             return st;
     } else if (moe_mfma_ok(gu, dn, h, H, I)) {
-        // decode on MFMA; one token with k <= 2 folds the combine into down
-        const bool fused = T == 1 && k <= 2;
+        // decode on MFMA; one token with k <= 2: gate_up and down in one
+        // launch, the combine folded into down
+        if (T == 1 && k <= 2)
+            return gu->g.type == LQ_Q6_K
+                       ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s)
+                       : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
+        const bool fused = false;
         const int st = gu->g.type == LQ_Q6_K
                            ? launch_moe_mfma_t<LQ_Q6_K>(gu, dn, tb, h, T, H, I, k, slots, topk_idx, topk_w, out, fused, s)
                            : launch_moe_mfma_t<LQ_Q4_K>(gu, dn, tb, h, T, H, I, k, slots, topk_idx, topk_w, out, fused, s);

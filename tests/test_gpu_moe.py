@@ -199,3 +199,52 @@ def test_router_logits_bit_exact(T, E, H, k):
     np.testing.assert_array_equal(idx, ridx)
     np.testing.assert_allclose(g, omoe.gates(sel), rtol=1e-5, atol=1e-6)
     assert np.isfinite(out).all()
+
+
+def test_one_token_layer_repeated_and_graph_replayed():
+    """The one-token layer runs as one launch whose workgroups hand work to
+    each other through counters in the workspace; every call must leave them
+    ready for the next: back-to-back calls with new tokens, a call of another
+    size in between, and replays of a captured HIP graph (the token copied in
+    between replays) all match the oracle."""
+    import torch
+    from localai_amd import synth, device
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(77)
+    E, H, I, k, t = 16, 1024, 512, 2, 14
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    layer = MoELayer(rw, gu, dn, t, E, H, I, k)
+
+    def check(h, out, idx, g):
+        rout, ridx, rg, _ = omoe.moe_forward(h, rw, gu, dn, t, E, k, I)
+        np.testing.assert_array_equal(idx, ridx)
+        np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
+        assert normwise_rel(out, rout) < 1e-5
+
+    for _ in range(3):
+        h = synth.activations(rng, 1, H)
+        check(h, *layer.forward(h))
+    h3 = synth.activations(rng, 3, H)
+    check(h3, *layer.forward(h3))
+    h = synth.activations(rng, 1, H)
+    check(h, *layer.forward(h))
+
+    stream = torch.cuda.Stream()
+    hd = device.to_device_f32(synth.activations(rng, 1, H))
+    out = torch.empty((1, H), dtype=torch.float32, device=hd.device)
+    idx = torch.empty((1, k), dtype=torch.int32, device=hd.device)
+    gates = torch.empty((1, k), dtype=torch.float32, device=hd.device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        layer.forward_device(hd, out=out, idx=idx, gates=gates, stream=stream)
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            layer.forward_device(hd, out=out, idx=idx, gates=gates, stream=stream)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        h = synth.activations(rng, 1, H)
+        hd.copy_(torch.from_numpy(h).to(hd.device))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        check(h, out.cpu().numpy(), idx.cpu().numpy(), gates.cpu().numpy())
