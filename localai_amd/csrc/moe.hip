@@ -21,6 +21,10 @@
 //             (64-row gate tile + matching up tile, expert); SiLU*up fused
 //   down      grouped matvec over the active experts
 //   combine   gate-weighted sum of each token's k expert outputs (fixed order)
+// One token with k <= 2 on MFMA: route, then gate_up and down in a single
+// launch (moe_decode1_kernel: the down tiles' weights stream beside
+// gate_up's, the combine folded into down). From 32 tokens: the expert
+// GEMMs on MFMA (gemm.hip) between the permute and the combine.
 //
 // Router logits are bit-reproducible: each is a sum of exact fp64 products
 // h*w in a fixed order (lane l sums elements 256j + 4l + c, j-major; then a
@@ -676,27 +680,14 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(const uint8_t *__restr
 // gate_up: workgroup (i, slot) = gate tile i (rows 16i ..) and up tile
 // inter / 16 + i of the slot's expert; act[p, 16i + n] = silu(g) * u
 // (engine/zaya.py:303-306) for every perm position p of the expert.
-// `single` (one token): slot = assignment a, expert topk_idx[a], act row a --
-// the weights are requested after one dependent load.
 template <int TYPE, int SPW, int MAXT>
 __global__ __launch_bounds__(MAXT) void moe_mfma_gate_up(const uint8_t *__restrict__ Wt, int64_t mat_bytes, int nb,
                                                          int64_t inter, MoeTables tb, const float *__restrict__ h,
-                                                         int64_t H, int k, const int32_t *__restrict__ topk_idx,
-                                                         int single, float *__restrict__ out) {
+                                                         int64_t H, int k) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int slot = blockIdx.y;
-    int e;
-    if (single) {
-        e = topk_idx[slot];
-        if (slot == 0) {   // clear the token's output for moe_mfma_down_single
-            const int64_t per = (H + gridDim.x - 1) / gridDim.x;
-            for (int64_t c = blockIdx.x * per + threadIdx.x; c < (blockIdx.x + 1) * per && c < H; c += blockDim.x)
-                out[c] = 0.0f;
-        }
-    } else {
-        if (slot >= tb.n_active[0]) return;
-        e = tb.active[slot];
-    }
+    if (slot >= tb.n_active[0]) return;
+    const int e = tb.active[slot];
     const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
     const int64_t i = blockIdx.x, tile_bytes = (int64_t)nb * mt_block_bytes(TYPE);
     const uint8_t *We = Wt + (int64_t)e * mat_bytes;
@@ -706,8 +697,8 @@ __global__ __launch_bounds__(MAXT) void moe_mfma_gate_up(const uint8_t *__restri
     __builtin_amdgcn_sched_barrier(0);
     // the expert's tokens; each next token's row is requested before the
     // current token's arithmetic
-    const int n = single ? 1 : tb.counts[e], base = single ? slot : tb.offsets[e];
-    const int tok0 = single ? 0 : tb.perm[base] / k;
+    const int n = tb.counts[e], base = tb.offsets[e];
+    const int tok0 = tb.perm[base] / k;
     float4 xv[1][SPW];
     mt_load_x<SPW>(xv[0], h + (int64_t)tok0 * H, nb, sb0, lane);
     __builtin_amdgcn_sched_barrier(0);
@@ -755,65 +746,6 @@ __global__ __launch_bounds__(MAXT) void moe_mfma_down(const uint8_t *__restrict_
 #pragma unroll
             for (int kk = 0; kk < SPW; ++kk) xv[0][kk] = xn[0][kk];
         }
-    }
-}
-
-// One token (decode), k <= 2: workgroup (i, s) = hidden tile i of expert
-// topk_idx[s]; out[16i + n] += topk_w[s] * y (out cleared by gate_up). Two
-// additions onto zero give the same sum in either order, so the result does
-// not depend on which workgroup lands first.
-template <int TYPE, int SPW, int MAXT>
-__global__ __launch_bounds__(MAXT) void moe_mfma_down_single(const uint8_t *__restrict__ Wt, int64_t mat_bytes,
-                                                             int nb, int64_t hidden, MoeTables tb, int64_t inter,
-                                                             const int32_t *__restrict__ topk_idx,
-                                                             const float *__restrict__ topk_w,
-                                                             float *__restrict__ out) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
-    const int64_t i = blockIdx.x;
-    const int s = blockIdx.y;
-    float4 xv[1][SPW];
-    mt_load_x<SPW>(xv[0], tb.act + (int64_t)s * inter, nb, sb0, lane);
-    MtW<TYPE> w[1][SPW];
-    mt_load_tile<TYPE, SPW>(w[0], Wt + (int64_t)topk_idx[s] * mat_bytes + i * nb * mt_block_bytes(TYPE), nb, sb0,
-                            nsb, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    float *fin;
-    mt_pass<TYPE, SPW, 1, 1>(w, xv, nsb, smem, fin);
-    const int r = threadIdx.x;
-    if (r < MT_ROWS && i * MT_ROWS + r < hidden) atomicAdd(out + i * MT_ROWS + r, topk_w[s] * fin[r]);
-}
-
-// One token (decode): hidden tile i of each of its K experts, with the gate
-// weighted sum of moe_combine_kernel in the epilogue (same order, same fma
-// chain, so the result equals down + combine). act rows are in assignment
-// order (gate_up `single`).
-template <int TYPE, int SPW, int K, int MAXT>
-__global__ __launch_bounds__(MAXT) void moe_mfma_down_combine(const uint8_t *__restrict__ Wt, int64_t mat_bytes,
-                                                              int nb, int64_t hidden, MoeTables tb, int64_t inter,
-                                                              const int32_t *__restrict__ topk_idx,
-                                                              const float *__restrict__ topk_w,
-                                                              float *__restrict__ out) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
-    const int64_t i = blockIdx.x;
-    float4 xv[K][SPW];
-    MtW<TYPE> w[K][SPW];
-#pragma unroll
-    for (int s = 0; s < K; ++s) mt_load_x<SPW>(xv[s], tb.act + (int64_t)s * inter, nb, sb0, lane);
-#pragma unroll
-    for (int s = 0; s < K; ++s)
-        mt_load_tile<TYPE, SPW>(w[s], Wt + (int64_t)topk_idx[s] * mat_bytes + i * nb * mt_block_bytes(TYPE), nb,
-                                sb0, nsb, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    float *fin;
-    mt_pass<TYPE, SPW, K, K>(w, xv, nsb, smem, fin);
-    const int r = threadIdx.x;
-    if (r < MT_ROWS && i * MT_ROWS + r < hidden) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int s = 0; s < K; ++s) acc = __builtin_fmaf(topk_w[s], fin[s * MT_ROWS + r], acc);
-        out[i * MT_ROWS + r] = acc;
     }
 }
 
@@ -1091,40 +1023,28 @@ static bool moe_mfma_ok(const localai_qmat *gu, const localai_qmat *dn, const fl
 
 template <int TYPE>
 static int launch_moe_mfma_t(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
-                             int64_t T, int64_t H, int64_t I, int k, int slots, const int32_t *topk_idx,
-                             const float *topk_w, float *out, bool fused_combine, hipStream_t s) {
+                             int64_t H, int64_t I, int k, int slots, hipStream_t s) {
     {
         const int nb = (int)gu->g.nb, spw = nb <= 16 ? 1 : 4, waves = (nb + spw - 1) / spw;
         dim3 grid((unsigned)(I / MT_ROWS), slots), block(64 * waves);
         const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 2);
-        const int single = fused_combine;   // one token: assignment-ordered act rows
         if (spw == 1)
             hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, 1, 1024>), grid, block, lds, s, gu->tiles, gu->tile_bytes, nb,
-                               I, tb, h, H, k, topk_idx, single, out);
+                               I, tb, h, H, k);
         else
             hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, 4, 512>), grid, block, lds, s, gu->tiles, gu->tile_bytes, nb,
-                               I, tb, h, H, k, topk_idx, single, out);
+                               I, tb, h, H, k);
         LQ_HIP(hipGetLastError());
     }
     const int nb = (int)dn->g.nb, spw = nb <= 16 ? 1 : 4, waves = (nb + spw - 1) / spw;
     const unsigned tiles = (unsigned)((H + MT_ROWS - 1) / MT_ROWS);
-    if (fused_combine) {
-        const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 1);
-        if (spw == 1)
-            hipLaunchKernelGGL((moe_mfma_down_single<TYPE, 1, 1024>), dim3(tiles, k), dim3(64 * waves), lds, s,
-                               dn->tiles, dn->tile_bytes, nb, H, tb, I, topk_idx, topk_w, out);
-        else
-            hipLaunchKernelGGL((moe_mfma_down_single<TYPE, 4, 512>), dim3(tiles, k), dim3(64 * waves), lds, s,
-                               dn->tiles, dn->tile_bytes, nb, H, tb, I, topk_idx, topk_w, out);
-    } else {
-        const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 1);
-        if (spw == 1)
-            hipLaunchKernelGGL((moe_mfma_down<TYPE, 1, 1024>), dim3(tiles, slots), dim3(64 * waves), lds, s,
-                               dn->tiles, dn->tile_bytes, nb, H, tb, I);
-        else
-            hipLaunchKernelGGL((moe_mfma_down<TYPE, 4, 512>), dim3(tiles, slots), dim3(64 * waves), lds, s,
-                               dn->tiles, dn->tile_bytes, nb, H, tb, I);
-    }
+    const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 1);
+    if (spw == 1)
+        hipLaunchKernelGGL((moe_mfma_down<TYPE, 1, 1024>), dim3(tiles, slots), dim3(64 * waves), lds, s, dn->tiles,
+                           dn->tile_bytes, nb, H, tb, I);
+    else
+        hipLaunchKernelGGL((moe_mfma_down<TYPE, 4, 512>), dim3(tiles, slots), dim3(64 * waves), lds, s, dn->tiles,
+                           dn->tile_bytes, nb, H, tb, I);
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
 }
@@ -1222,11 +1142,9 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
             return gu->g.type == LQ_Q6_K
                        ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s)
                        : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
-        const bool fused = false;
-        const int st = gu->g.type == LQ_Q6_K
-                           ? launch_moe_mfma_t<LQ_Q6_K>(gu, dn, tb, h, T, H, I, k, slots, topk_idx, topk_w, out, fused, s)
-                           : launch_moe_mfma_t<LQ_Q4_K>(gu, dn, tb, h, T, H, I, k, slots, topk_idx, topk_w, out, fused, s);
-        if (st || fused) return st;
+        const int st = gu->g.type == LQ_Q6_K ? launch_moe_mfma_t<LQ_Q6_K>(gu, dn, tb, h, H, I, k, slots, s)
+                                             : launch_moe_mfma_t<LQ_Q4_K>(gu, dn, tb, h, H, I, k, slots, s);
+        if (st) return st;
     } else {
         if (int st = launch_grouped<true>(gu, tb, h, H, k, slots, T, s)) return st;
         if (int st = launch_grouped<false>(dn, tb, tb.act, I, k, slots, T, s)) return st;
