@@ -62,6 +62,15 @@ int localai_hip_block_layout(int ggml_type, int *values_per_block, int *bytes_pe
 int localai_hip_dequant(int ggml_type, const void *raw_dev, int64_t n_values,
                         float *out_dev, void *stream);
 
+/* y[t, r] = sum_c w[r, c] * x[t, c] for an fp32 matrix w [rows, cols] and
+ * x [tokens, cols] -> y [tokens, rows] (all device, row-major). The device
+ * path for GGUF matrices outside the packed types (F32, F16, Q4_1, Q5_0,
+ * Q5_1), decoded once by localai_hip_dequant; it replaces the reference's
+ * dequantize + NumPy `weights @ x` fallback (engine/gguf_parser.py:269-289,
+ * :350-358). Results do not depend on the launch (fixed summation order). */
+int localai_hip_f32_matvec(const float *w_dev, int64_t rows, int64_t cols, const float *x_dev,
+                           int64_t tokens, float *y_dev, void *stream);
+
 /* ---- device-resident weight matrices ------------------------------------ */
 
 /* Upload + repack a [batch, rows, cols] GGML tensor (batch = 1 for a plain

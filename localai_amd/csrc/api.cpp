@@ -114,6 +114,15 @@ int localai_hip_dequant(int t, const void *raw, int64_t n, float *out, void *str
     return launch_dequant_ggml(t, raw, n, out, (hipStream_t)stream);
 }
 
+int localai_hip_f32_matvec(const float *w, int64_t rows, int64_t cols, const float *x, int64_t tokens, float *y,
+                           void *stream) {
+    clear_error();
+    if (!w || !x || !y) return fail(LOCALAI_EARG, "null pointer");
+    if (rows < 1 || cols < 1 || tokens < 1) return fail(LOCALAI_EARG, "f32 matvec: rows, cols and tokens must be >= 1");
+    if (int st = ensure_device()) return st;
+    return launch_f32_matvec(w, rows, cols, x, tokens, y, (hipStream_t)stream);
+}
+
 int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, const void *src,
                             int src_is_device, void *stream, localai_qmat **out) {
     clear_error();

@@ -36,6 +36,8 @@ size_t max_lds_per_block();   // LDS bytes a workgroup may use on the current de
 int launch_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *packed, int direction,
                   hipStream_t s);
 int launch_dequant_ggml(int t, const void *raw, int64_t n, float *out, hipStream_t s);
+int launch_f32_matvec(const float *W, int64_t rows, int64_t cols, const float *x, int64_t ntok, float *y,
+                      hipStream_t s);
 struct GemvPlan {
     int waves;        // waves per workgroup (split the K units)
     int slots;        // 64-value units per lane per wave

@@ -8,8 +8,10 @@ expert_matvec   W[e] @ x for expert e of a [E, rows, cols] GGML tensor; the
                 expert e is the byte slice [e*B, (e+1)*B) of the tensor.
 ZayaExpertsMixin
                 provides `_expert_matvec(self, name, expert, x)` with the
-                reference signature for a model holding `self.gguf` (a GGUFFile
-                with `.tensors[name]` -> (shape, ggml_type, offset) and `._map`).
+                reference signature for a model holding `self.gguf`: a
+                localai_amd.gguf.GGUFFile (the expert tensor's device copy
+                lives with the file), or any reader with `.tensors[name]` ->
+                (shape, ggml_type, offset) and `._map`.
 
 Selection semantics (generalising engine/zaya.py:290-306 to top-k): router
 logits are ranked (value desc, index asc: the np.argmax tie rule of
@@ -90,15 +92,12 @@ class MoELayer:
         return o.cpu().numpy(), i.cpu().numpy(), g.cpu().numpy()
 
 
-_expert_cache: dict = {}
-
-
 def expert_matvec(tensor_raw, shape, ggml_type, expert, x):
     """W[expert] @ x for a [E, rows, cols] GGML tensor given as host bytes.
 
-    The whole 3-D tensor is uploaded once (cached while `tensor_raw` is
-    alive and immutable) and expert `expert` is addressed inside it, like the
-    byte slicing of engine/zaya.py:144-150.
+    The whole 3-D tensor is uploaded once (in native_quant's weight cache when
+    `tensor_raw` is immutable) and expert `expert` is addressed inside it,
+    like the byte slicing of engine/zaya.py:144-150.
     """
     from . import native_quant
     E, rows, cols = (int(s) for s in shape)
@@ -110,17 +109,10 @@ def expert_matvec(tensor_raw, shape, ggml_type, expert, x):
         raise ValueError(f'expert input has {x.size} values, expected {cols}')
     if not 0 <= int(expert) < E:
         raise IndexError(f'expert {expert} outside [0, {E})')
-    addr, nbytes = device.host_address(tensor_raw)
+    _, nbytes = device.host_address(tensor_raw)
     if nbytes != E * rows * (cols // block) * bpb:
         raise ValueError('tensor bytes do not match [E, rows, cols]')
-    key = (addr, nbytes, int(ggml_type), E, rows, cols)
-    hit = _expert_cache.get(key)
-    if hit is None:
-        q = device.QMat.from_ggml(tensor_raw, ggml_type, rows, cols, E)
-        if native_quant._immutable(tensor_raw):
-            _expert_cache[key] = (q, tensor_raw)
-    else:
-        q = hit[0]
+    q = native_quant.weights(tensor_raw, rows, cols, ggml_type, batch=E)
     return q.matvec(device.to_device_f32(x), expert=int(expert)).cpu().numpy()
 
 
@@ -131,6 +123,17 @@ class ZayaExpertsMixin:
         info = self.gguf.tensors[name]
         if len(info.shape) != 3 or info.shape[0] != self.n_experts:
             raise ValueError(f'{name}: expected [experts,out,in], got {info.shape}')
+        device_matrix = getattr(self.gguf, 'device_matrix', None)
+        if device_matrix is not None:
+            # localai_amd.gguf.GGUFFile: the tensor's device copy lives with the file
+            E, rows, cols = info.shape
+            if not 0 <= int(expert) < E:
+                raise IndexError(f'expert {expert} outside [0, {E})')
+            xv = np.asarray(x, dtype=np.float32).reshape(-1)
+            if xv.size != cols:
+                raise ValueError(f'expert input has {xv.size} values, expected {cols}')
+            q = device_matrix(name)
+            return q.matvec(device.to_device_f32(xv), expert=int(expert)).cpu().numpy()
         block, bpb = block_layout(info.ggml_type)
         E, rows, cols = info.shape
         nbytes = E * rows * (cols // block) * bpb

@@ -17,10 +17,14 @@ device present and the library missing it raises instead of returning None.
 
 Weights: `raw` is GGML bytes in host memory (a GGUF mmap slice in the
 reference). Immutable buffers -- `bytes`, read-only memoryviews such as mmap
-slices -- are uploaded once and kept as device handles (keyed by address,
-size, type and shape, holding a reference to `raw` so the address cannot be
-reused while cached). Writable buffers are uploaded on every call. The cache
-is bounded by LOCALAI_HIP_WEIGHT_CACHE_GB (default 64).
+slices -- are uploaded once and kept as device handles, keyed by address,
+size, type and shape. A cache entry references the object that owns the
+memory (the bytes object, or the mmap behind a slice), so the address cannot
+be reused while the entry lives, but holds no exported buffer: the owner's
+mmap.close() (GGUFFile.close, engine/gguf_parser.py:77-80) still succeeds,
+and entries whose mmap has closed are dropped. Writable buffers are uploaded
+on every call. The cache is bounded by LOCALAI_HIP_WEIGHT_CACHE_GB (default
+64).
 """
 from __future__ import annotations
 
@@ -62,22 +66,43 @@ def _cache_limit() -> int:
     return int(float(os.environ.get('LOCALAI_HIP_WEIGHT_CACHE_GB', '64')) * (1 << 30))
 
 
-def weights(raw, rows, cols, ggml_type):
-    """Device handle for GGML bytes `raw` [rows, cols] (cached when immutable)."""
+def _owner(raw):
+    """The object owning raw's memory, found without keeping a buffer export."""
+    try:
+        view = memoryview(raw)
+    except TypeError:
+        return raw
+    owner = view.obj
+    view.release()
+    return owner
+
+
+def _stale(owner) -> bool:
+    return bool(getattr(owner, 'closed', False))
+
+
+def _drop(key):
+    q, _ = _cache.pop(key)
+    _cache_bytes[0] -= q.device_bytes
+    q.close()
+
+
+def weights(raw, rows, cols, ggml_type, batch=1):
+    """Device handle for GGML bytes `raw` [batch, rows, cols] (cached when immutable)."""
+    for key in [k for k, (_, o) in _cache.items() if _stale(o)]:
+        _drop(key)
     addr, nbytes = device.host_address(raw)
-    key = (addr, nbytes, int(ggml_type), int(rows), int(cols))
+    key = (addr, nbytes, int(ggml_type), int(batch), int(rows), int(cols))
     hit = _cache.get(key)
     if hit is not None:
         _cache.move_to_end(key)
         return hit[0]
-    q = device.QMat.from_ggml(raw, ggml_type, rows, cols)
+    q = device.QMat.from_ggml(raw, ggml_type, rows, cols, batch)
     if _immutable(raw):
-        _cache[key] = (q, raw)
+        _cache[key] = (q, _owner(raw))
         _cache_bytes[0] += q.device_bytes
         while _cache_bytes[0] > _cache_limit() and len(_cache) > 1:
-            _, (old, _) = _cache.popitem(last=False)
-            _cache_bytes[0] -= old.device_bytes
-            old.close()
+            _drop(next(iter(_cache)))
     return q
 
 

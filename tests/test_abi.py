@@ -56,6 +56,9 @@ def test_argument_errors_before_device_use():
     assert lib.localai_hip_qmat_create(3, 4, 32, 1, ctypes.c_void_p(1), 0, None, ctypes.byref(h)) == 2
     assert lib.localai_hip_qmat_create(12, 4, 100, 1, ctypes.c_void_p(1), 0, None, ctypes.byref(h)) == 1
     assert lib.localai_hip_matvec(None, 0, None, None, 1, None) == 1
+    assert lib.localai_hip_f32_matvec(None, 4, 4, None, 1, None, None) == 1
+    one = ctypes.c_void_p(16)
+    assert lib.localai_hip_f32_matvec(one, 0, 4, one, 1, one, None) == 1
     with pytest.raises(_lib.HipError):
         _lib.check(lib.localai_hip_dequant(99, None, 0, None, None))
 
