@@ -83,6 +83,27 @@ def capture(torch, fn, stream):
     return g
 
 
+DIST = []   # per-step distributions recorded by the timers, in call order
+
+
+def record_distribution(torch, graph, per_replay, stream, min_steps=100):
+    """After a timed region: replay `graph` (per_replay steps each) at least
+    min_steps steps' worth, an event pair around each replay on the launch
+    stream; keeps the median and p90 of the per-step times."""
+    reps = max(10, -(-min_steps // per_replay))
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    with torch.cuda.stream(stream):
+        for a, b in evs:
+            a.record(stream)
+            graph.replay()
+            b.record(stream)
+    torch.cuda.synchronize()
+    per = np.array([a.elapsed_time(b) / per_replay for a, b in evs])
+    DIST.append({'median_ms': round(float(np.median(per)), 6), 'p90_ms': round(float(np.percentile(per, 90)), 6),
+                 'samples': reps, 'steps_per_sample': per_replay,
+                 'how': 'per-step time of each replay of the timed graph, measured after the timed region'})
+
+
 def time_steps(torch, fns, stream, steps, warmup):
     """Time exactly `steps` steps of the rotation fns[0], fns[1], ... (one
     function per weight copy). One HIP graph holds a whole rotation, as a
@@ -105,7 +126,9 @@ def time_steps(torch, fns, stream, steps, warmup):
             part.replay()
         end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps      # ms per step
+    ms = start.elapsed_time(end) / steps
+    record_distribution(torch, full, n, stream)
+    return ms      # ms per step
 
 
 def time_graphs(torch, graphs, stream, steps, warmup):
@@ -510,6 +533,8 @@ def main():
           'zaya_moe_decode': wl_zaya, 'qwen3_moe_prefill': wl_qwen3, 'hbm_copy': wl_copy}[args.workload]
     r = fn(args, torch, device, synth)
     ms = r.pop('ms_per_step')
+    if DIST and 'step_stats' not in r:
+        r['step_stats'] = DIST[0]
     line = {'metric': METRIC, 'value': r.pop('value'), 'unit': r.pop('unit'), 'n_gpus': 1, 'steps': args.steps,
             'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True, 'scaling': 'weak',
             'vs_baseline': None}
