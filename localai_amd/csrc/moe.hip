@@ -33,6 +33,7 @@
 
 #include "gemv_core.h"
 #include "internal.h"
+#include "fused_sync.h"
 #include "mfma_core.h"
 
 namespace lq {
@@ -59,20 +60,6 @@ struct MoeTables {
     int max_tiles;
     int tile_w;         // tokens per tile (0: matvec path, no tile list)
     uint32_t *sync;     // counters of the fused one-token layer (1 KiB)
-};
-
-// Counter block of the fused one-token expert kernel (moe_decode1_kernel),
-// in the workspace, zeroed by the router kernel that runs before it:
-// D1_NCNT gate_up completion counters (gate_up tile r counts on r % D1_NCNT,
-// so no counter takes more than a few dozen atomics), a counter of full
-// counters, the all-done flag the down tiles poll, and an error word, each
-// on a 128-byte line of its own.
-constexpr int D1_NCNT = 16, D1_LINE = 32;
-enum {
-    D1_FULL = D1_NCNT * D1_LINE,
-    D1_DONE = D1_FULL + D1_LINE,
-    D1_ERROR = D1_DONE + D1_LINE,
-    D1_WORDS = D1_ERROR + D1_LINE
 };
 
 // ------------------------------------------------------------------ route
@@ -767,77 +754,6 @@ __global__ void moe_combine_kernel(const float *__restrict__ ysl, const int32_t 
 
 // ------------------------------------------------- one-token decode, fused
 
-// Bound on every wait of the fused layer (seconds of polling): a wait that
-// runs out sets D1_ERROR and its workgroup skips its stores (wrong output
-// instead of a hang).
-constexpr int D1_SPIN_LIMIT = 1 << 22;
-
-// Data handed between workgroups of the fused layer moves with device-
-// coherent (relaxed, device-scope atomic) loads and stores, which bypass the
-// per-XCD caches; a store of a flag follows the data stores' completion
-// (vmcnt(0)). No acquire or release fences: on this GPU each would
-// invalidate or write back a whole XCD's L2.
-template <typename V>
-__device__ __forceinline__ V d1_get(const V *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename V>
-__device__ __forceinline__ void d1_put(V *p, V v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void d1_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// Whole workgroup: wait until the all-done flag is set. One thread polls: a
-// first sleep of about 8000 cycles (the gate_up tiles take several times
-// that), then about 1000 cycles between polls; the others wait at the
-// barrier. false: the wait ran out. flag: one int of LDS.
-__device__ __forceinline__ bool d1_wait_done(uint32_t *sync, int *flag) {
-    if (threadIdx.x == 0) {
-        int ok = 0;
-        __builtin_amdgcn_s_sleep(127);
-        for (int n = 0; n < D1_SPIN_LIMIT; ++n) {
-            if (d1_get(sync + D1_DONE) != 0u) {
-                ok = 1;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(15);
-        }
-        if (!ok) d1_put(sync + D1_ERROR, 1u);
-        *flag = ok;
-    }
-    __syncthreads();
-    return *flag != 0;
-}
-
-// gate_up tile r of n_gu: count it done. The tile that fills its counter
-// (its share: the tiles r' < n_gu with r' % D1_NCNT == r % D1_NCNT) counts a
-// full counter; the tile that fills the last counter sets the flag.
-__device__ __forceinline__ void d1_count_gu(uint32_t *sync, int r, int n_gu) {
-    const int c = r % D1_NCNT;
-    const uint32_t share = (uint32_t)((n_gu - c + D1_NCNT - 1) / D1_NCNT);
-    const int ncnt = n_gu < D1_NCNT ? n_gu : D1_NCNT;
-    const uint32_t before =
-        __hip_atomic_fetch_add(sync + c * D1_LINE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (before + 1 == share) {
-        const uint32_t full =
-            __hip_atomic_fetch_add(sync + D1_FULL, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (full + 1 == (uint32_t)ncnt) d1_put(sync + D1_DONE, 1u);
-    }
-}
-
-// x of the wave's super-blocks (as mt_load_x) with device-coherent loads
-template <int SPW>
-__device__ __forceinline__ void d1_load_x(float4 (&xv)[SPW], const float *x, int nb, int sb0, int lane) {
-#pragma unroll
-    for (int k = 0; k < SPW; ++k) {
-        const int sb = sb0 + k < nb ? sb0 + k : nb - 1;
-        const uint64_t *p = reinterpret_cast<const uint64_t *>(x + 256 * (int64_t)sb + 4 * lane);
-        const uint64_t lo = d1_get(p), hi = d1_get(p + 1);
-        xv[k] = make_float4(__builtin_bit_cast(float, (uint32_t)lo), __builtin_bit_cast(float, (uint32_t)(lo >> 32)),
-                            __builtin_bit_cast(float, (uint32_t)hi), __builtin_bit_cast(float, (uint32_t)(hi >> 32)));
-    }
-}
-
 // The expert part of the MoE layer for one token with k <= 2 in one launch,
 // after the router (moe_route_kernel, which wrote topk_idx / topk_w and
 // zeroed the counter block). Workgroup r:
@@ -883,7 +799,7 @@ __global__ __launch_bounds__(512) void moe_decode1_kernel(
         for (int c = r * per + n; c < (r + 1) * per && c < H; c += blockDim.x) d1_put(out + c, 0.0f);
         d1_drain();
         __syncthreads();
-        if (threadIdx.x == 0) d1_count_gu(sync, r, n_gu);
+        if (threadIdx.x == 0) d1_count(sync, r, n_gu);
         return;
     }
     const int j = r - n_gu, s = j / dtiles, i = j % dtiles;
