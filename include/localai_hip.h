@@ -127,6 +127,35 @@ int localai_hip_matmul(const localai_qmat *m, int64_t expert, const float *x_dev
                        float *y_dev, int y_layout, void *workspace_dev, int64_t workspace_bytes,
                        void *stream);
 
+/* ---- ZAYA router (engine/zaya.py:274-307) -------------------------------- */
+
+/* Everything of ZAYA's router after the first projection r0 = W_inp h
+ * (engine/zaya.py:280-296), one workgroup: r = r0 + b_inp, then
+ * r = r + prev * eda (skipped when prev and eda are NULL), state = r,
+ * u = rmsnorm(r, eps) * norm_w, v1 = gelu(w_gate u + b_gate),
+ * v2 = gelu(w_mlp2 v1 + b_mlp2), logits = w_mlp4 v2 + b_mlp4,
+ * probs = softmax(logits), expert = argmax(probs + route_bias), the first
+ * maximum. b_* are the projections' GGUF biases (NULL when absent,
+ * engine/model.py:72-79). Matrices are fp32 device copies [rows, cols]
+ * (w_gate [r1, r], w_mlp2 [r2, r1], w_mlp4 [routes, r2]); vectors up to
+ * 4096, routes up to 512. GELU is exact (erf); the steps the reference
+ * rounds in fp32 are separate fp32 operations. Outputs: state [r],
+ * probs [routes], expert [1] (int32), all device. */
+int localai_hip_zaya_router(const float *r0_dev, const float *b_inp_dev, const float *prev_dev,
+                            const float *eda_dev, const float *norm_w_dev, float eps, int64_t r,
+                            const float *w_gate_dev, const float *b_gate_dev, int64_t r1,
+                            const float *w_mlp2_dev, const float *b_mlp2_dev, int64_t r2,
+                            const float *w_mlp4_dev, const float *b_mlp4_dev, int64_t routes,
+                            const float *route_bias_dev, float *state_dev, float *probs_dev,
+                            int32_t *expert_dev, void *stream);
+
+/* gu_dev != NULL: y[i] = silu(gu[i]) * gu[n + i] (the expert SwiGLU on the
+ * [gate; up] gate_up output, engine/zaya.py:304-305). gu_dev == NULL:
+ * y[i] = x[i] * scale[0] with scale in device memory (the route probability,
+ * :297-301 and :306). */
+int localai_hip_zaya_scale(const float *gu_dev, const float *x_dev, int64_t n, const float *scale_dev,
+                           float *y_dev, void *stream);
+
 /* ---- MoE expert layer ---------------------------------------------------- */
 
 /* Bytes of device workspace localai_hip_moe_forward needs for these sizes.

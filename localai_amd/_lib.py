@@ -36,6 +36,9 @@ SIGNATURES = {
     'localai_hip_matvec_many': (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp]),
     'localai_hip_matmul_workspace_size': (_c_i64, [_vp, _c_i64]),
     'localai_hip_matmul': (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_int, _vp, _c_i64, _vp]),
+    'localai_hip_zaya_router': (_c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _c_i64, _vp, _vp, _c_i64, _vp,
+                                         _vp, _c_i64, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp]),
+    'localai_hip_zaya_scale': (_c_int, [_vp, _vp, _c_i64, _vp, _vp, _vp]),
     'localai_hip_moe_workspace_size': (_c_i64, [_c_i64, _c_i64, _c_int, _c_i64, _c_i64]),
     'localai_hip_moe_forward': (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp, _vp,
                                          _vp, _vp, _c_i64, _vp]),

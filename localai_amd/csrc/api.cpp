@@ -123,6 +123,29 @@ int localai_hip_f32_matvec(const float *w, int64_t rows, int64_t cols, const flo
     return launch_f32_matvec(w, rows, cols, x, tokens, y, (hipStream_t)stream);
 }
 
+int localai_hip_zaya_router(const float *r0, const float *b_inp, const float *prev, const float *eda,
+                            const float *norm_w, float eps, int64_t r, const float *w_gate, const float *b_gate,
+                            int64_t r1, const float *w_mlp2, const float *b_mlp2, int64_t r2, const float *w_mlp4,
+                            const float *b_mlp4, int64_t routes, const float *route_bias, float *state,
+                            float *probs, int32_t *expert, void *stream) {
+    clear_error();
+    if (!r0 || !norm_w || !w_gate || !w_mlp2 || !w_mlp4 || !route_bias || !state || !probs || !expert)
+        return fail(LOCALAI_EARG, "null pointer");
+    if (r > (1 << 20) || r1 > (1 << 20) || r2 > (1 << 20) || routes > (1 << 20))
+        return fail(LOCALAI_EARG, "zaya router: sizes too large");
+    if (int st = ensure_device()) return st;
+    return launch_zaya_router_tail(r0, b_inp, prev, eda, norm_w, eps, (int)r, w_gate, b_gate, (int)r1, w_mlp2, b_mlp2,
+                                   (int)r2, w_mlp4, b_mlp4, (int)routes, route_bias, state, probs, expert,
+                                   (hipStream_t)stream);
+}
+
+int localai_hip_zaya_scale(const float *gu, const float *x, int64_t n, const float *scale, float *y, void *stream) {
+    clear_error();
+    if (!y) return fail(LOCALAI_EARG, "null pointer");
+    if (int st = ensure_device()) return st;
+    return launch_zaya_scale(gu, x, n, scale, y, (hipStream_t)stream);
+}
+
 int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, const void *src,
                             int src_is_device, void *stream, localai_qmat **out) {
     clear_error();

@@ -1,0 +1,155 @@
+"""ZAYA MoE block on the GPU (localai_amd.zaya.ZayaMoEMixin) against the CPU
+restatement of engine/zaya.py:274-307 (oracle/zaya_moe.py) on a synthetic
+GGUF layer: router MLP (Q8_0 first projection with a bias, F16 / F32 small
+matrices, EDA), Q6_K experts, the skip route and forced experts, through our
+GGUFFile and through a plain reader with only `.tensors` and `._map`.
+
+Tolerances: router state normwise <= 1e-6 (exact products, fp32 sums);
+probabilities within 2e-6 absolute; the expert index equal wherever the
+oracle's best two routes are more than 1e-4 apart (np.exp's own rounding is
+not restated); block output normwise <= 1e-5 (i8 MFMA expert matvecs).
+"""
+import numpy as np
+import pytest
+
+from oracle import quant
+from oracle import zaya_moe as zm
+from tests.conftest import normwise_rel
+from tests.gguf_writer import build
+from tests.gpu_util import random_ggml
+
+pytestmark = pytest.mark.gpu
+
+E, H, I, R = 16, 1024, 512, 256
+EPS = 1e-5
+
+
+def layer_tensors(rng, route_bias):
+    f32 = lambda a: np.asarray(a, np.float32)   # noqa: E731
+    raw = {
+        'ffn_gate_inp.weight': ((R, H), 8, random_ggml(rng, 8, R * H, 2e-4, 6e-4)),
+        'ffn_gate_inp.bias': ((R,), 0, f32(rng.standard_normal(R) * 0.1).tobytes()),
+        'zaya_router_eda.weight': ((R,), 0, f32(rng.uniform(-0.5, 0.5, R)).tobytes()),
+        'ffn_norm.weight': ((R,), 0, f32(rng.uniform(0.5, 1.5, R)).tobytes()),
+        'ffn_gate.weight': ((R, R), 1, (rng.standard_normal((R, R)) / 16).astype(np.float16).tobytes()),
+        'ffn_gate.bias': ((R,), 0, f32(rng.standard_normal(R) * 0.1).tobytes()),
+        'zaya_router_mlp2.weight': ((R, R), 0, f32(rng.standard_normal((R, R)) / 16).tobytes()),
+        'zaya_router_mlp4.weight': ((E + 1, R), 0, f32(rng.standard_normal((E + 1, R)) / 4).tobytes()),
+        'zaya_router_biases.weight': ((E + 1,), 0, f32(route_bias).tobytes()),
+        'ffn_gate_up_exps.weight': ((E, 2 * I, H), 14, random_ggml(rng, 14, E * 2 * I * H, 1e-4, 2e-3)),
+        'ffn_down_exps.weight': ((E, H, I), 14, random_ggml(rng, 14, E * H * I, 1e-4, 2e-3)),
+    }
+    return raw
+
+
+def write_layer(path, raw):
+    tensors = [(f'blk.1.{n}', shape, t, b) for n, (shape, t, b) in raw.items()]
+    path.write_bytes(build(tensors, metadata=[('general.architecture', 8, 'zaya')], alignment=32))
+
+
+def oracle_tensors(raw):
+    d = {n: quant.dequantize(b, t, shape) for n, (shape, t, b) in raw.items()}
+    return {'inp': d['ffn_gate_inp.weight'], 'inp_b': d['ffn_gate_inp.bias'], 'eda': d['zaya_router_eda.weight'],
+            'norm': d['ffn_norm.weight'], 'gate': d['ffn_gate.weight'], 'gate_b': d['ffn_gate.bias'],
+            'mlp2': d['zaya_router_mlp2.weight'], 'mlp2_b': None, 'mlp4': d['zaya_router_mlp4.weight'],
+            'mlp4_b': None, 'route_bias': d['zaya_router_biases.weight'], 'gate_up': d['ffn_gate_up_exps.weight'],
+            'down': d['ffn_down_exps.weight']}
+
+
+class Model:
+    n_experts = E
+    eps = EPS
+
+    def __init__(self, gguf):
+        self.gguf = gguf
+
+
+def model_class():
+    from localai_amd.zaya import ZayaMoEMixin
+    return type('ZayaGPU', (ZayaMoEMixin, Model), {})
+
+
+class PlainReader:
+    """Only what the reference's GGUFFile offers the model: tensors and _map."""
+
+    def __init__(self, g):
+        self.tensors, self._map = g.tensors, g._map
+
+
+@pytest.fixture(scope='module')
+def base(tmp_path_factory):
+    rng = np.random.default_rng(21)
+    raw = layer_tensors(rng, rng.uniform(0.0, 0.05, E + 1) * np.r_[np.ones(E), 0.0])
+    path = tmp_path_factory.mktemp('zaya') / 'layer.gguf'
+    write_layer(path, raw)
+    return path, oracle_tensors(raw)
+
+
+@pytest.mark.parametrize('reader', ['gguf', 'plain'])
+def test_block_matches_oracle(base, reader):
+    from localai_amd.gguf import GGUFFile
+    path, t = base
+    rng = np.random.default_rng(5)
+    matched = 0
+    with GGUFFile(path) as g:
+        m = model_class()(g if reader == 'gguf' else PlainReader(g))
+        prev = None
+        for step in range(6):
+            h = rng.standard_normal(H).astype(np.float32)
+            moe, state = m._moe(1, h, prev)
+            w_moe, w_state, w_probs, w_e, margin = zm.moe_block(t, E, EPS, h, prev)
+            assert normwise_rel(state, w_state) < 1e-6
+            if margin > 1e-4:
+                assert normwise_rel(moe, w_moe) < 1e-5, step
+                matched += 1
+            prev = state
+    assert matched >= 3
+
+
+def test_router_probabilities_and_expert(base):
+    """Read the router's outputs directly (probs and the index) through the C ABI."""
+    import ctypes
+    from localai_amd import _lib, device
+    from localai_amd.gguf import GGUFFile
+    path, t = base
+    rng = np.random.default_rng(8)
+    tt = device.torch()
+    with GGUFFile(path) as g:
+        m = model_class()(g)
+        L = m._zaya_layer(1)
+        for _ in range(4):
+            h = rng.standard_normal(H).astype(np.float32)
+            prev = rng.standard_normal(R).astype(np.float32)
+            _, w_state, w_probs, w_e, margin = zm.moe_block(t, E, EPS, h, prev)
+            r0 = m._zaya_matrix(L.inp).matvec(device.to_device_f32(h)).reshape(-1)
+            pd = device.to_device_f32(prev)
+            state = tt.empty(R, dtype=tt.float32, device=r0.device)
+            probs = tt.empty(E + 1, dtype=tt.float32, device=r0.device)
+            ex = tt.empty(1, dtype=tt.int32, device=r0.device)
+            p = device.ptr
+            _lib.check(_lib.load().localai_hip_zaya_router(
+                p(r0), p(L.b_inp), p(pd), p(L.eda), p(L.norm), ctypes.c_float(EPS), R, p(L.w1), p(L.b1), R,
+                p(L.w2), None, R, p(L.w3), None, E + 1, p(L.route_bias), p(state), p(probs), p(ex), None))
+            np.testing.assert_allclose(probs.cpu().numpy(), w_probs, rtol=0, atol=2e-6)
+            assert normwise_rel(state.cpu().numpy(), w_state) < 1e-6
+            if margin > 1e-4:
+                assert int(ex.cpu().item()) == w_e
+
+
+@pytest.mark.parametrize('forced', [E, 5])
+def test_skip_route_and_forced_expert(tmp_path, forced):
+    from localai_amd.gguf import GGUFFile
+    rng = np.random.default_rng(30 + forced)
+    bias = np.zeros(E + 1)
+    bias[forced] = 10.0
+    raw = layer_tensors(rng, bias)
+    path = tmp_path / 'forced.gguf'
+    write_layer(path, raw)
+    t = oracle_tensors(raw)
+    h = rng.standard_normal(H).astype(np.float32)
+    with GGUFFile(path) as g:
+        moe, state = model_class()(g)._moe(1, h, None)
+    w_moe, w_state, w_probs, w_e, _ = zm.moe_block(t, E, EPS, h, None)
+    assert w_e == forced
+    assert normwise_rel(state, w_state) < 1e-6
+    assert normwise_rel(moe, w_moe) < (1e-6 if forced == E else 1e-5)
