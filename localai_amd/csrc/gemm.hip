@@ -460,29 +460,39 @@ __device__ __forceinline__ GtRaw<T> gt_load(const uint8_t *blk, int half, int la
     return r;
 }
 
-// B operand (8 f16) of slice kk (0..3) of half HALF of the block, lane group q
+// Q4_K sub-block scale pair {d * sc, dmin * mn} (packed f16, each rounded
+// once) of row lane % 16, sub-block 4 HALF + lane / 16: the four lane groups
+// of a wave cover the four sub-blocks of a half at once; gt_b fetches the
+// pair of its own sub-block from the lane that computed it
+template <int HALF>
+__device__ __forceinline__ uint32_t gt_q4k_pair(const uint4 &hd, int q) {
+    const uint32_t s0 = hd.y, s4 = hd.z, s8 = hd.w;   // scale bytes 0..3, 4..7, 8..11
+    uint32_t sc, mn;
+    if constexpr (HALF == 0) {
+        sc = __builtin_amdgcn_ubfe(s0, 8 * q, 6);
+        mn = __builtin_amdgcn_ubfe(s4, 8 * q, 6);
+    } else {
+        sc = __builtin_amdgcn_ubfe(s8, 8 * q, 4) | (__builtin_amdgcn_ubfe(s0, 8 * q + 6, 2) << 4);
+        mn = __builtin_amdgcn_ubfe(s8, 8 * q + 4, 4) | (__builtin_amdgcn_ubfe(s4, 8 * q + 6, 2) << 4);
+    }
+    // packed f16: {sc, mn} exactly (0x6400 | n reads as 1024 + n), times
+    // {d, dmin} rounds d * sc and dmin * mn once each
+    const lq_h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const lq_h2 scmn = __builtin_bit_cast(lq_h2, sc | (mn << 16) | 0x64006400u) - k1024;
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(lq_h2, hd.x) * scmn);
+}
+
+// B operand (8 f16) of slice kk (0..3) of half HALF of the block, lane group
+// q; Q4_K: pair = the slice's scale pair for the lane's row (gt_q4k_pair)
 template <int T, int HALF, int KK>
-__device__ __forceinline__ lq_h8 gt_b(const GtRaw<T> &r, int q) {
+__device__ __forceinline__ lq_h8 gt_b(const GtRaw<T> &r, int q, uint32_t pair_ab = 0) {
     uint4 o;
     if constexpr (T == LQ_Q4_K) {
-        // group g = 4 HALF + KK: qs chunk g / 2 (bytes 8 ((g / 2) % 2) ..), nibble g % 2
+        // group g = 4 HALF + KK: qs chunk g / 2 (bytes 8 ((g / 2) % 2) ..), nibble g % 2;
+        // a value is round(a * q - b) from the exact q (one fused multiply-add)
         constexpr int g = 4 * HALF + KK, hb = (g >> 1) & 1, nib = g & 1;
-        const uint32_t s0 = r.hd.y, s4 = r.hd.z, s8 = r.hd.w;   // scale bytes 0..3, 4..7, 8..11
-        uint32_t sc, mn;
-        if constexpr (g < 4) {
-            sc = (s0 >> (8 * g)) & 63u;
-            mn = (s4 >> (8 * g)) & 63u;
-        } else {
-            constexpr int j = g - 4;
-            sc = ((s8 >> (8 * j)) & 15u) | (((s0 >> (8 * j + 6)) & 3u) << 4);
-            mn = ((s8 >> (8 * j + 4)) & 15u) | (((s4 >> (8 * j + 6)) & 3u) << 4);
-        }
-        // packed f16: {sc, mn} exactly (0x6400 | n reads as 1024 + n), times
-        // {d, dmin} rounds d * sc and dmin * mn once each; a value is then
-        // round(a * q - b) from the exact q (one fused multiply-add)
         const lq_h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-        const lq_h2 scmn = __builtin_bit_cast(lq_h2, sc | (mn << 16) | 0x64006400u) - k1024;
-        const lq_h2 ab = __builtin_bit_cast(lq_h2, r.hd.x) * scmn;
+        const lq_h2 ab = __builtin_bit_cast(lq_h2, pair_ab);
         const lq_h2 a2 = {ab.x, ab.x}, nb2 = {-ab.y, -ab.y};
         const uint32_t w0 = ((hb ? r.qs.z : r.qs.x) >> (4 * nib)) & 0x0F0F0F0Fu;
         const uint32_t w1 = ((hb ? r.qs.w : r.qs.y) >> (4 * nib)) & 0x0F0F0F0Fu;
@@ -540,6 +550,11 @@ template <int T, int HALF, int NI>
 __device__ __forceinline__ void gt_half(const GtRaw<T> &w0, const GtRaw<T> &w1, const _Float16 *xs, int lane,
                                         lq_f4 (&acc)[NI][2]) {
     const int fr = lane & 15, q = lane >> 4;
+    uint32_t pr0 = 0, pr1 = 0;
+    if constexpr (T == LQ_Q4_K) {
+        pr0 = gt_q4k_pair<HALF>(w0.hd, q);
+        pr1 = gt_q4k_pair<HALF>(w1.hd, q);
+    }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
         // all A reads of the slice in flight while the B operands are decoded
@@ -547,11 +562,18 @@ __device__ __forceinline__ void gt_half(const GtRaw<T> &w0, const GtRaw<T> &w1, 
 #pragma unroll
         for (int i = 0; i < NI; ++i)
             av[i] = *reinterpret_cast<const lq_h8 *>(xs + (16 * i + fr) * GM_BK + 8 * ((4 * kk + q) ^ fr));
+        uint32_t p0 = 0, p1 = 0;
+        if constexpr (T == LQ_Q4_K) {
+            // the pair of sub-block 4 HALF + kk of the lane's row: lane fr + 16 kk
+            const int src = 4 * (fr + 16 * kk);
+            p0 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)pr0);
+            p1 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)pr1);
+        }
         lq_h8 b0, b1;
-        if (kk == 0) { b0 = gt_b<T, HALF, 0>(w0, q); b1 = gt_b<T, HALF, 0>(w1, q); }
-        else if (kk == 1) { b0 = gt_b<T, HALF, 1>(w0, q); b1 = gt_b<T, HALF, 1>(w1, q); }
-        else if (kk == 2) { b0 = gt_b<T, HALF, 2>(w0, q); b1 = gt_b<T, HALF, 2>(w1, q); }
-        else { b0 = gt_b<T, HALF, 3>(w0, q); b1 = gt_b<T, HALF, 3>(w1, q); }
+        if (kk == 0) { b0 = gt_b<T, HALF, 0>(w0, q, p0); b1 = gt_b<T, HALF, 0>(w1, q, p1); }
+        else if (kk == 1) { b0 = gt_b<T, HALF, 1>(w0, q, p0); b1 = gt_b<T, HALF, 1>(w1, q, p1); }
+        else if (kk == 2) { b0 = gt_b<T, HALF, 2>(w0, q, p0); b1 = gt_b<T, HALF, 2>(w1, q, p1); }
+        else { b0 = gt_b<T, HALF, 3>(w0, q, p0); b1 = gt_b<T, HALF, 3>(w1, q, p1); }
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], b0, acc[i][0], 0, 0, 0);
