@@ -666,13 +666,20 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(const uint8_t *__restr
 
 // gate_up: workgroup (i, slot) = gate tile i (rows 16i ..) and up tile
 // inter / 16 + i of the slot's expert; act[p, 16i + n] = silu(g) * u
-// (engine/zaya.py:303-306) for every perm position p of the expert.
+// (engine/zaya.py:303-306) for every perm position p of the expert. With
+// zero != null the slot-0 workgroups also clear zero[0 .. nzero) (the output
+// that the down kernel then adds onto).
 template <int TYPE, int SPW, int MAXT>
 __global__ __launch_bounds__(MAXT) void moe_mfma_gate_up(const uint8_t *__restrict__ Wt, int64_t mat_bytes, int nb,
                                                          int64_t inter, MoeTables tb, const float *__restrict__ h,
-                                                         int64_t H, int k) {
+                                                         int64_t H, int k, float *__restrict__ zero,
+                                                         int64_t nzero) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int slot = blockIdx.y;
+    if (zero && slot == 0) {
+        const int64_t per = (nzero + gridDim.x - 1) / gridDim.x, c0 = blockIdx.x * per;
+        for (int64_t c = c0 + threadIdx.x; c < c0 + per && c < nzero; c += blockDim.x) zero[c] = 0.0f;
+    }
     if (slot >= tb.n_active[0]) return;
     const int e = tb.active[slot];
     const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
@@ -705,10 +712,15 @@ __global__ __launch_bounds__(MAXT) void moe_mfma_gate_up(const uint8_t *__restri
 }
 
 // down: workgroup (i, slot) = hidden tile i of the slot's expert;
-// ysl[p, 16i + n] for every perm position p of the expert
+// ysl[p, 16i + n] for every perm position p of the expert, or with out !=
+// null (k <= 2, out cleared by gate_up) out[t, 16i + n] += gate * y for the
+// token t of position p: two additions onto zero give the same sum in either
+// order, so the combine is folded in without changing the result's bits
 template <int TYPE, int SPW, int MAXT>
 __global__ __launch_bounds__(MAXT) void moe_mfma_down(const uint8_t *__restrict__ Wt, int64_t mat_bytes, int nb,
-                                                      int64_t hidden, MoeTables tb, int64_t inter) {
+                                                      int64_t hidden, MoeTables tb, int64_t inter,
+                                                      float *__restrict__ out, const float *__restrict__ topk_w,
+                                                      int k) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int slot = blockIdx.y;
     if (slot >= tb.n_active[0]) return;
@@ -728,7 +740,14 @@ __global__ __launch_bounds__(MAXT) void moe_mfma_down(const uint8_t *__restrict_
         float *fin;
         mt_pass<TYPE, SPW, 1, 1>(w, xv, nsb, smem, fin);
         const int r = threadIdx.x;
-        if (r < MT_ROWS && i * MT_ROWS + r < hidden) tb.ysl[(int64_t)p * hidden + i * MT_ROWS + r] = fin[r];
+        if (r < MT_ROWS && i * MT_ROWS + r < hidden) {
+            if (out) {
+                const int a = tb.perm[p];
+                atomicAdd(out + (int64_t)(a / k) * hidden + i * MT_ROWS + r, topk_w[a] * fin[r]);
+            } else {
+                tb.ysl[(int64_t)p * hidden + i * MT_ROWS + r] = fin[r];
+            }
+        }
         if (j + 1 < n) {
 #pragma unroll
             for (int kk = 0; kk < SPW; ++kk) xv[0][kk] = xn[0][kk];
@@ -939,17 +958,18 @@ static bool moe_mfma_ok(const localai_qmat *gu, const localai_qmat *dn, const fl
 
 template <int TYPE>
 static int launch_moe_mfma_t(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
-                             int64_t H, int64_t I, int k, int slots, hipStream_t s) {
+                             int64_t H, int64_t I, int k, int slots, float *out, const float *topk_w, int64_t T,
+                             hipStream_t s) {
     {
         const int nb = (int)gu->g.nb, spw = nb <= 16 ? 1 : 4, waves = (nb + spw - 1) / spw;
         dim3 grid((unsigned)(I / MT_ROWS), slots), block(64 * waves);
         const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 2);
         if (spw == 1)
             hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, 1, 1024>), grid, block, lds, s, gu->tiles, gu->tile_bytes, nb,
-                               I, tb, h, H, k);
+                               I, tb, h, H, k, out, T * H);
         else
             hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, 4, 512>), grid, block, lds, s, gu->tiles, gu->tile_bytes, nb,
-                               I, tb, h, H, k);
+                               I, tb, h, H, k, out, T * H);
         LQ_HIP(hipGetLastError());
     }
     const int nb = (int)dn->g.nb, spw = nb <= 16 ? 1 : 4, waves = (nb + spw - 1) / spw;
@@ -957,10 +977,10 @@ static int launch_moe_mfma_t(const localai_qmat *gu, const localai_qmat *dn, con
     const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 1);
     if (spw == 1)
         hipLaunchKernelGGL((moe_mfma_down<TYPE, 1, 1024>), dim3(tiles, slots), dim3(64 * waves), lds, s, dn->tiles,
-                           dn->tile_bytes, nb, H, tb, I);
+                           dn->tile_bytes, nb, H, tb, I, out, topk_w, k);
     else
         hipLaunchKernelGGL((moe_mfma_down<TYPE, 4, 512>), dim3(tiles, slots), dim3(64 * waves), lds, s, dn->tiles,
-                           dn->tile_bytes, nb, H, tb, I);
+                           dn->tile_bytes, nb, H, tb, I, out, topk_w, k);
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
 }
@@ -1058,9 +1078,14 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
             return gu->g.type == LQ_Q6_K
                        ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s)
                        : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
-        const int st = gu->g.type == LQ_Q6_K ? launch_moe_mfma_t<LQ_Q6_K>(gu, dn, tb, h, H, I, k, slots, s)
-                                             : launch_moe_mfma_t<LQ_Q4_K>(gu, dn, tb, h, H, I, k, slots, s);
+        // k <= 2: down adds gate * y onto out (cleared by gate_up) itself,
+        // unless out overlaps h (gate_up still reads h)
+        float *fold = k <= 2 && (out + T * H <= h || h + T * H <= out) ? out : nullptr;
+        const int st = gu->g.type == LQ_Q6_K
+                           ? launch_moe_mfma_t<LQ_Q6_K>(gu, dn, tb, h, H, I, k, slots, fold, topk_w, T, s)
+                           : launch_moe_mfma_t<LQ_Q4_K>(gu, dn, tb, h, H, I, k, slots, fold, topk_w, T, s);
         if (st) return st;
+        if (fold) return LOCALAI_OK;
     } else {
         if (int st = launch_grouped<true>(gu, tb, h, H, k, slots, T, s)) return st;
         if (int st = launch_grouped<false>(dn, tb, tb.act, I, k, slots, T, s)) return st;
