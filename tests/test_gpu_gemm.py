@@ -6,7 +6,7 @@ scaled by a power of two and rounded to f16, so each product carries at most
 2^-11 relative error and each output at most about 2^-11 * sum|w*x| (fp32
 accumulation adds K * 2^-24 of the same sum). Gates: every output within
 1e-3 * sum_k |w_k x_k| (the dot-product error bound, which holds however much
-the sum cancels), and the north-star max-rel 1e-3 (normwise:
+the sum cancels), and the path's max-rel 1e-3 target (normwise:
 max|y - y_ref| / max|y_ref|) for tiles of at least 64 outputs, where the
 typical figure is near 2e-4."""
 import numpy as np

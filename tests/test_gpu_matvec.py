@@ -2,7 +2,7 @@
 the reference's golden outputs and the reference's own test tolerances.
 
 Tolerance: fp32 accumulation of exact products gives errors of order 1e-6 of
-the output scale; the gate is the north-star max-rel 1e-3 (normwise:
+the output scale; the gate is the path's max-rel 1e-3 target (normwise:
 max|y - y_ref| / max|y_ref|) plus an elementwise check at the reference
 test suite's tolerances."""
 import ctypes
