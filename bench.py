@@ -22,10 +22,12 @@ input, weights already resident in HBM, seeded data from localai_amd/synth.py):
 Weight copies beyond 2 x the 256 MB Infinity Cache are rotated so every step
 streams its weights from HBM; one HIP graph holds a whole rotation of steps
 (as a decode step's graph holds every layer), is replayed on the launch
-stream and timed with HIP events on that stream. `roofline` is the
-dominant kernel of the workload timed alone the same way; `cpu_baseline` is
-the reference's own engine/native_quant.cpp kernels (built from source into
-oracle/_ref) on a bounded sample, on the host cores.
+stream and timed with HIP events on that stream, exactly K steps.
+`step_stats` gives the median and p90 per-step time over at least 100 more
+steps replayed after the timed region. `roofline` is the dominant kernel of
+the workload timed alone the same way; `cpu_baseline` is the reference's own
+engine/native_quant.cpp kernels (built from source into oracle/_ref) on a
+bounded sample, on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--cpu-baseline auto|off]
 """
@@ -276,9 +278,9 @@ def gate_roofline(args, torch, device, gate_host, x, stream):
     nrot = rotations(14336 * 16 * 144)
     gmats = [device.QMat.from_ggml(gate_host, 12, 14336, 4096) for _ in range(nrot)]
     gout = torch.empty(14336, dtype=torch.float32, device=device.device())
-    ggraph = capture(torch, lambda: [m.matvec(x, out=gout, stream=stream) for m in gmats], stream)
     log('timing dominant kernel')
-    kms = time_graphs(torch, [ggraph], stream, max(20, args.steps // 4), 5) / nrot
+    kms = time_steps(torch, [lambda m=m: m.matvec(x, out=gout, stream=stream) for m in gmats], stream, args.steps,
+                     args.warmup)
     achieved = gate_bytes / (kms * 1e-3) / 1e9
     for m in gmats:
         m.close()
