@@ -446,7 +446,10 @@ __device__ __forceinline__ GtRaw<T> gt_load(const uint8_t *blk, int half, int la
     const int n = lane & 15;
     if constexpr (T == LQ_Q4_K) {
         r.qs = ld16(blk + half * 1024 + 16 * lane);
-        r.hd = ld16(blk + 2048 + 16 * n);
+        // half 1 takes half 0's scales (the loop copies them): a second load
+        // of the same bytes made the register allocator split the loaded
+        // registers and wait for the load right after issuing it
+        if (half == 0) r.hd = ld16(blk + 2048 + 16 * n);
     } else if constexpr (T == LQ_Q6_K) {
         r.ql = ld16(blk + half * 1024 + 16 * lane);
         r.qh = ld16(blk + 2048 + 16 * lane);
@@ -666,7 +669,11 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
     // step loop over blocks: half 0 from Xs[0] / (a0, a1), half 1 from Xs[1] / (b0, b1);
     // the next half's weights and x are requested before the current half's MFMAs
     for (int64_t sb = 0; sb < nsb; ++sb) {
-        const GtRaw<T> b0 = gt_load<T>(w0p + sb * BB, 1, lane), b1 = gt_load<T>(w1p + sb * BB, 1, lane);
+        GtRaw<T> b0 = gt_load<T>(w0p + sb * BB, 1, lane), b1 = gt_load<T>(w1p + sb * BB, 1, lane);
+        if constexpr (T == LQ_Q4_K) {
+            b0.hd = a0.hd;
+            b1.hd = a1.hd;
+        }
         load_x(1, 2 * sb + 1);
         // nothing crosses: the loads stay ahead of the MFMAs, and the next
         // half's decode stays behind them (it would wait on these loads)
