@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 Ws[GM_BM * GM_LD];
     __shared__ __attribute__((aligned(16))) _Float16 Xs[BN * GM_LD];
     const lq_geom &g = a.g;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     // token tile
     const uint8_t *W = a.W;
     int64_t p0;
@@ -549,11 +549,11 @@ __device__ __forceinline__ lq_h8 gt_b(const GtRaw<T> &r, int q, uint32_t pair_ab
 // decoded from the wave's two row tiles, A operands from the LDS x tile
 // x tile in LDS: [token][16 chunks of 8 halves], chunk c of token t stored at
 // position c ^ (t % 16), so the 16 tokens of an A read hit 16 bank groups.
-// PRIO: the wave raises its priority while it issues a slice's MFMAs, so the
-// wave that holds ready MFMAs keeps the matrix core of its SIMD (the two
-// waves of a SIMD come from different workgroups). Dense 14336 x 4096 x 512
-// Q8_0: 88 us against 97 us; the expert GEMMs (64-token tiles) do not gain.
-template <int T, int HALF, int NI, bool PRIO>
+// The wave raises its priority while it issues a slice's MFMAs, so the wave
+// that holds ready MFMAs keeps the matrix core of its SIMD (the waves of a
+// SIMD come from different workgroups). Dense 14336 x 4096 x 512 Q8_0: 88 us
+// against 97 us; the expert GEMMs gain about 1 %.
+template <int T, int HALF, int NI>
 __device__ __forceinline__ void gt_half(const GtRaw<T> &w0, const GtRaw<T> &w1, const _Float16 *xs, int lane,
                                         lq_f4 (&acc)[NI][2]) {
     const int fr = lane & 15, q = lane >> 4;
@@ -581,13 +581,13 @@ __device__ __forceinline__ void gt_half(const GtRaw<T> &w0, const GtRaw<T> &w1, 
         else if (kk == 1) { b0 = gt_b<T, HALF, 1>(w0, q, p0); b1 = gt_b<T, HALF, 1>(w1, q, p1); }
         else if (kk == 2) { b0 = gt_b<T, HALF, 2>(w0, q, p0); b1 = gt_b<T, HALF, 2>(w1, q, p1); }
         else { b0 = gt_b<T, HALF, 3>(w0, q, p0); b1 = gt_b<T, HALF, 3>(w1, q, p1); }
-        if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], b0, acc[i][0], 0, 0, 0);
             acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], b1, acc[i][1], 0, 0, 0);
         }
-        if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_s_setprio(0);
     }
 }
 
@@ -600,7 +600,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
     const lq_geom &g = a.g;
     // wave index made wave-uniform: row-tile addresses go to scalar registers
     // (MoE Q4_K GEMMs 162 -> 128 VGPRs; gate_up 85 -> 81 us, down 55 -> 48 us)
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint8_t *Wt = a.Wt;
     int64_t p0;
     int tn;
@@ -680,7 +680,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
         // nothing crosses: the loads stay ahead of the MFMAs, and the next
         // half's decode stays behind them (it would wait on these loads)
         __builtin_amdgcn_sched_barrier(0);
-        gt_half<T, 0, NI, MODE == GM_DENSE>(a0, a1, Xs[0], lane, acc);
+        gt_half<T, 0, NI>(a0, a1, Xs[0], lane, acc);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         // next block (the last block re-reads itself: Xs[0] is not read again)
@@ -689,7 +689,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
         a1 = gt_load<T>(w1p + nx * BB, 0, lane);
         load_x(0, 2 * nx);
         __builtin_amdgcn_sched_barrier(0);
-        gt_half<T, 1, NI, MODE == GM_DENSE>(b0, b1, Xs[1], lane, acc);
+        gt_half<T, 1, NI>(b0, b1, Xs[1], lane, acc);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
