@@ -140,14 +140,15 @@ int localai_hip_matmul(const localai_qmat *m, int64_t expert, const float *x_dev
  * (w_gate [r1, r], w_mlp2 [r2, r1], w_mlp4 [routes, r2]); vectors up to
  * 4096, routes up to 512. GELU is exact (erf); the steps the reference
  * rounds in fp32 are separate fp32 operations. Outputs: state [r],
- * probs [routes], expert [1] (int32), all device. */
+ * probs [routes], expert [1] (int32), and expert_w [1] = probs[expert] when
+ * not NULL (the weight localai_hip_moe_experts1 takes), all device. */
 int localai_hip_zaya_router(const float *r0_dev, const float *b_inp_dev, const float *prev_dev,
                             const float *eda_dev, const float *norm_w_dev, float eps, int64_t r,
                             const float *w_gate_dev, const float *b_gate_dev, int64_t r1,
                             const float *w_mlp2_dev, const float *b_mlp2_dev, int64_t r2,
                             const float *w_mlp4_dev, const float *b_mlp4_dev, int64_t routes,
                             const float *route_bias_dev, float *state_dev, float *probs_dev,
-                            int32_t *expert_dev, void *stream);
+                            int32_t *expert_dev, float *expert_w_dev, void *stream);
 
 /* gu_dev != NULL: y[i] = silu(gu[i]) * gu[n + i] (the expert SwiGLU on the
  * [gate; up] gate_up output, engine/zaya.py:304-305). gu_dev == NULL:
@@ -184,6 +185,23 @@ int localai_hip_moe_forward(const float *h_dev, int64_t tokens, int64_t hidden,
                             const localai_qmat *down, float *out_dev, int32_t *topk_idx_dev,
                             float *topk_w_dev, void *workspace_dev, int64_t workspace_bytes,
                             void *stream);
+
+/* The expert part of the MoE layer for one token, with the chosen experts
+ * already in device memory (written by a router kernel, so the host need not
+ * read them): engine/zaya.py:297-306 for ZAYA's top-1 with its skip route.
+ *   out_dev[hidden] = sum_s weight[s] * y_s, s < top_k (1 or 2), where
+ *   y_s = h                                      if expert[s] == skip
+ *       = down[e] (silu(gate) * up)(gate_up[e] h) otherwise (e = expert[s])
+ * skip = -1 when every slot is an expert. One launch for gate_up and down
+ * (plus a counter clear); the sum is the same whatever order the slots land.
+ * Experts must be Q4_K or Q6_K handles with the tile form (ETYPE otherwise:
+ * the caller then runs the matvec path). Workspace: as
+ * localai_hip_moe_workspace_size(1, experts, top_k, hidden, inter); h_dev
+ * 16-byte and the workspace 256-byte aligned; out must not overlap h. */
+int localai_hip_moe_experts1(const float *h_dev, int64_t hidden, const localai_qmat *gate_up,
+                             const localai_qmat *down, int top_k, const int32_t *expert_dev,
+                             const float *weight_dev, int32_t skip, float *out_dev, void *workspace_dev,
+                             int64_t workspace_bytes, void *stream);
 
 /* ---- host weight registration for the legacy exports -------------------- */
 

@@ -127,7 +127,7 @@ int localai_hip_zaya_router(const float *r0, const float *b_inp, const float *pr
                             const float *norm_w, float eps, int64_t r, const float *w_gate, const float *b_gate,
                             int64_t r1, const float *w_mlp2, const float *b_mlp2, int64_t r2, const float *w_mlp4,
                             const float *b_mlp4, int64_t routes, const float *route_bias, float *state,
-                            float *probs, int32_t *expert, void *stream) {
+                            float *probs, int32_t *expert, float *expert_w, void *stream) {
     clear_error();
     if (!r0 || !norm_w || !w_gate || !w_mlp2 || !w_mlp4 || !route_bias || !state || !probs || !expert)
         return fail(LOCALAI_EARG, "null pointer");
@@ -136,7 +136,7 @@ int localai_hip_zaya_router(const float *r0, const float *b_inp, const float *pr
     if (int st = ensure_device()) return st;
     return launch_zaya_router_tail(r0, b_inp, prev, eda, norm_w, eps, (int)r, w_gate, b_gate, (int)r1, w_mlp2, b_mlp2,
                                    (int)r2, w_mlp4, b_mlp4, (int)routes, route_bias, state, probs, expert,
-                                   (hipStream_t)stream);
+                                   expert_w, (hipStream_t)stream);
 }
 
 int localai_hip_zaya_scale(const float *gu, const float *x, int64_t n, const float *scale, float *y, void *stream) {
@@ -318,6 +318,23 @@ int localai_hip_matmul(const localai_qmat *m, int64_t expert, const float *x, in
     return launch_gemm(one, m->data + expert * m->g.matrix_bytes, m->tiles ? m->tiles + expert * m->tile_bytes : nullptr,
                        x, tokens, y, ts, rs, ws, ws_bytes,
                        (hipStream_t)stream);
+}
+
+int localai_hip_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, const localai_qmat *dn, int k,
+                             const int32_t *expert, const float *weight, int32_t skip, float *out, void *ws,
+                             int64_t ws_bytes, void *stream) {
+    clear_error();
+    if (!h || !gu || !dn || !expert || !weight || !out || !ws) return fail(LOCALAI_EARG, "moe experts: null pointer");
+    if (H < 1 || k < 1 || k > 2) return fail(LOCALAI_EARG, "moe experts: hidden >= 1 and top_k 1 or 2");
+    const int64_t E = gu->g.batch, I = gu->g.rows / 2;
+    if (dn->g.batch != E) return fail(LOCALAI_EARG, "moe experts: gate_up and down hold different expert counts");
+    if (gu->g.cols != H || gu->g.rows % 2 || I % 64) return fail(LOCALAI_EARG, "moe experts: gate_up must be [E, 2*inter, hidden] with inter % 64 == 0");
+    if (dn->g.rows != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe experts: down must be [E, hidden, inter]");
+    if (ws_bytes < (int64_t)moe_workspace_bytes(1, E, k, H, I)) return fail(LOCALAI_EARG, "moe experts: workspace too small");
+    if ((reinterpret_cast<uintptr_t>(h) & 15) || (reinterpret_cast<uintptr_t>(ws) & 255))
+        return fail(LOCALAI_EARG, "moe experts: h must be 16-byte and workspace 256-byte aligned");
+    if (int st = ensure_device()) return st;
+    return launch_moe_experts1(h, H, gu, dn, k, expert, weight, skip, out, ws, (hipStream_t)stream);
 }
 
 int64_t localai_hip_moe_workspace_size(int64_t T, int64_t E, int k, int64_t H, int64_t I) {

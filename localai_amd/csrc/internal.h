@@ -73,12 +73,16 @@ int moe_gemm_tile();   // tokens per expert GEMM tile
 int launch_zaya_router_tail(const float *r0, const float *b0, const float *prev, const float *eda,
                             const float *norm_w, float eps, int R, const float *W1, const float *b1, int R1,
                             const float *W2, const float *b2, int R2, const float *W3, const float *b3, int NE,
-                            const float *bias, float *state, float *probs, int32_t *expert, hipStream_t s);
+                            const float *bias, float *state, float *probs, int32_t *expert, float *expert_w,
+                            hipStream_t s);
 int launch_zaya_scale(const float *gu, const float *x, int64_t n, const float *scale, float *y, hipStream_t s);
 
 size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I);
 int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const float *rb, int64_t E, int k,
                const localai_qmat *gu, const localai_qmat *dn, float *out, int32_t *topk_idx, float *topk_w,
                void *ws, hipStream_t s);
+int launch_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, const localai_qmat *dn, int k,
+                        const int32_t *topk_idx, const float *topk_w, int skip, float *out, void *ws,
+                        hipStream_t s);
 
 }  // namespace lq

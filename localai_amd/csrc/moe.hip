@@ -787,12 +787,15 @@ __global__ void moe_combine_kernel(const float *__restrict__ ysl, const int32_t 
 // the same sum in either order, so out does not depend on which down tile
 // lands first. 8 waves; SPWG / SPWD super-blocks per wave for gate_up / down.
 // LDS: the mt_pass regions.
+// skip: the route index that stands for "no expert" (ZAYA's skip route,
+// engine/zaya.py:297-301): its slot adds gate * h instead of an expert
+// output; its gate_up tiles read no weights but still clear and count.
 template <int TYPE, int SPWG, int SPWD>
 __global__ __launch_bounds__(512) void moe_decode1_kernel(
     const float *__restrict__ h, int H, int E, int k, const uint8_t *__restrict__ gu_t, int64_t gu_bytes, int nbg,
     int64_t inter, const uint8_t *__restrict__ dn_t, int64_t dn_bytes, int nbd,
     const int32_t *__restrict__ topk_idx, const float *__restrict__ topk_w, float *__restrict__ out, MoeTables tb,
-    uint32_t *__restrict__ sync) {
+    uint32_t *__restrict__ sync, int skip) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int flag;
     const int r = blockIdx.x;
@@ -801,19 +804,21 @@ __global__ __launch_bounds__(512) void moe_decode1_kernel(
     const int n_gu = k * gtiles;
     if (r < n_gu) {
         const int s = r / gtiles, i = r % gtiles;
-        const int sb0 = w * SPWG, nsb = mt_nsb(nbg, sb0, SPWG);
-        const int e = min(max(topk_idx[s], 0), E - 1);
-        const uint8_t *We = gu_t + (int64_t)e * gu_bytes;
-        const int64_t tb_bytes = (int64_t)nbg * mt_block_bytes(TYPE);
-        MtW<TYPE> wt[2][SPWG];
-        mt_load_tile<TYPE, SPWG>(wt[0], We + i * tb_bytes, nbg, sb0, nsb, lane);
-        mt_load_tile<TYPE, SPWG>(wt[1], We + (gtiles + i) * tb_bytes, nbg, sb0, nsb, lane);
-        float4 xv[1][SPWG];
-        mt_load_x<SPWG>(xv[0], h, nbg, sb0, lane);
-        float *fin;
-        mt_pass<TYPE, SPWG, 2, 1>(wt, xv, nsb, smem, fin);
         const int n = threadIdx.x;
-        if (n < MT_ROWS) d1_put(tb.act + (int64_t)s * inter + i * MT_ROWS + n, silu(fin[n]) * fin[MT_ROWS + n]);
+        if (topk_idx[s] != skip) {   // the same for the whole workgroup
+            const int sb0 = w * SPWG, nsb = mt_nsb(nbg, sb0, SPWG);
+            const int e = min(max(topk_idx[s], 0), E - 1);
+            const uint8_t *We = gu_t + (int64_t)e * gu_bytes;
+            const int64_t tb_bytes = (int64_t)nbg * mt_block_bytes(TYPE);
+            MtW<TYPE> wt[2][SPWG];
+            mt_load_tile<TYPE, SPWG>(wt[0], We + i * tb_bytes, nbg, sb0, nsb, lane);
+            mt_load_tile<TYPE, SPWG>(wt[1], We + (gtiles + i) * tb_bytes, nbg, sb0, nsb, lane);
+            float4 xv[1][SPWG];
+            mt_load_x<SPWG>(xv[0], h, nbg, sb0, lane);
+            float *fin;
+            mt_pass<TYPE, SPWG, 2, 1>(wt, xv, nsb, smem, fin);
+            if (n < MT_ROWS) d1_put(tb.act + (int64_t)s * inter + i * MT_ROWS + n, silu(fin[n]) * fin[MT_ROWS + n]);
+        }
         const int per = (H + n_gu - 1) / n_gu;   // this tile's share of out
         for (int c = r * per + n; c < (r + 1) * per && c < H; c += blockDim.x) d1_put(out + c, 0.0f);
         d1_drain();
@@ -822,9 +827,15 @@ __global__ __launch_bounds__(512) void moe_decode1_kernel(
         return;
     }
     const int j = r - n_gu, s = j / dtiles, i = j % dtiles;
+    const float gate = topk_w[s];
+    if (topk_idx[s] == skip) {   // out += gate * h on this tile's rows
+        const bool ok = d1_wait_done(sync, &flag);
+        const int row = i * MT_ROWS + (int)threadIdx.x;
+        if (threadIdx.x < MT_ROWS && row < H && ok) atomicAdd(out + row, gate * h[row]);
+        return;
+    }
     const int sb0 = w * SPWD, nsb = mt_nsb(nbd, sb0, SPWD);
     const int e = min(max(topk_idx[s], 0), E - 1);
-    const float gate = topk_w[s];
     MtW<TYPE> wt[1][SPWD];
     mt_load_tile<TYPE, SPWD>(wt[0], dn_t + (int64_t)e * dn_bytes + i * (int64_t)nbd * mt_block_bytes(TYPE), nbd, sb0,
                              nsb, lane);
@@ -994,22 +1005,22 @@ static int d1_spw(int64_t nb) {
 template <int TYPE, int SG, int SD>
 static void launch_decode1_k(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
                              int64_t H, int64_t E, int k, int64_t I, const int32_t *topk_idx, const float *topk_w,
-                             float *out, hipStream_t s) {
+                             float *out, int skip, hipStream_t s) {
     const size_t a = mt_lds_bytes(TYPE, 8, SG, 1, 2), b = mt_lds_bytes(TYPE, 8, SD, 1, 1);
     const unsigned grid = (unsigned)(k * (I / MT_ROWS) + k * ((H + MT_ROWS - 1) / MT_ROWS));
     hipLaunchKernelGGL((moe_decode1_kernel<TYPE, SG, SD>), dim3(grid), dim3(512), a > b ? a : b, s, h, (int)H,
                        (int)E, k, gu->tiles, gu->tile_bytes, (int)gu->g.nb, I, dn->tiles, dn->tile_bytes,
-                       (int)dn->g.nb, topk_idx, topk_w, out, tb, tb.sync);
+                       (int)dn->g.nb, topk_idx, topk_w, out, tb, tb.sync, skip);
 }
 
 template <int TYPE>
 static int launch_decode1_t(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
                             int64_t H, int64_t E, int k, int64_t I, const int32_t *topk_idx, const float *topk_w,
-                            float *out, hipStream_t s) {
+                            float *out, hipStream_t s, int skip = -1) {
     const int sg = d1_spw(gu->g.nb), sd = d1_spw(dn->g.nb);
 #define LQ_D1(SG, SD)                                                                                       \
     if (sg == SG && sd == SD)                                                                               \
-        launch_decode1_k<TYPE, SG, SD>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
+        launch_decode1_k<TYPE, SG, SD>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, skip, s);
     LQ_D1(1, 1) else LQ_D1(1, 2) else LQ_D1(1, 4) else LQ_D1(2, 1) else LQ_D1(2, 2) else LQ_D1(2, 4)
     else LQ_D1(4, 1) else LQ_D1(4, 2) else LQ_D1(4, 4)
 #undef LQ_D1
@@ -1094,6 +1105,30 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
     hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, s, tb.ysl, tb.pos, topk_w, k, (int)H, out);
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
+}
+
+// Zeroes the counter block of moe_decode1_kernel (a kernel, not a memset, so
+// that the call can be captured in a graph)
+__global__ void d1_clear_kernel(uint32_t *__restrict__ sync) {
+    for (int i = threadIdx.x; i < D1_WORDS; i += blockDim.x) sync[i] = 0u;
+}
+
+// The expert part of the one-token MoE layer from expert indices and weights
+// already in device memory (written by a router kernel, e.g. ZAYA's router
+// MLP): out = sum_s topk_w[s] * (topk_idx[s] == skip ? h : expert(h)).
+int launch_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, const localai_qmat *dn, int k,
+                        const int32_t *topk_idx, const float *topk_w, int skip, float *out, void *ws,
+                        hipStream_t s) {
+    const int64_t I = gu->g.rows / 2, E = gu->g.batch;
+    if (!moe_mfma_ok(gu, dn, h, H, I) || (gu->g.type != LQ_Q4_K && gu->g.type != LQ_Q6_K))
+        return fail(LOCALAI_ETYPE, "moe experts: Q4_K or Q6_K experts in the tile form, at most 32 blocks a row");
+    if (out < h + H && h < out + H) return fail(LOCALAI_EARG, "moe experts: out overlaps h");
+    MoeTables tb = carve(ws, 1, E, k, H, I);
+    hipLaunchKernelGGL(d1_clear_kernel, dim3(1), dim3(256), 0, s, tb.sync);
+    LQ_HIP(hipGetLastError());
+    return gu->g.type == LQ_Q6_K
+               ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, skip)
+               : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, skip);
 }
 
 }  // namespace lq

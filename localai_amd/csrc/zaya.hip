@@ -75,7 +75,8 @@ __global__ __launch_bounds__(ZR_THREADS) void zaya_router_tail_kernel(
     const float *__restrict__ eda, const float *__restrict__ norm_w, float eps, int R, const float *__restrict__ W1,
     const float *__restrict__ b1, int R1, const float *__restrict__ W2, const float *__restrict__ b2, int R2,
     const float *__restrict__ W3, const float *__restrict__ b3, int NE, const float *__restrict__ bias,
-    float *__restrict__ state, float *__restrict__ probs, int32_t *__restrict__ expert) {
+    float *__restrict__ state, float *__restrict__ probs, int32_t *__restrict__ expert,
+    float *__restrict__ expert_w) {
     __shared__ float va[ZR_MAXV], vb[ZR_MAXV];
     __shared__ double red[ZR_THREADS / 64];
     const int t = threadIdx.x;
@@ -132,19 +133,26 @@ __global__ __launch_bounds__(ZR_THREADS) void zaya_router_tail_kernel(
                 bi = oi;
             }
         }
-        if (t == 0) expert[0] = bi < NE ? bi : 0;
+        if (t == 0) {
+            const int e = bi < NE ? bi : 0;
+            expert[0] = e;
+            // the chosen route's probability, the same division as probs[e]
+            // (vb was written by this wave)
+            if (expert_w) expert_w[0] = __fdiv_rn(vb[e], zf);
+        }
     }
 }
 
 int launch_zaya_router_tail(const float *r0, const float *b0, const float *prev, const float *eda,
                             const float *norm_w, float eps, int R, const float *W1, const float *b1, int R1,
                             const float *W2, const float *b2, int R2, const float *W3, const float *b3, int NE,
-                            const float *bias, float *state, float *probs, int32_t *expert, hipStream_t s) {
+                            const float *bias, float *state, float *probs, int32_t *expert, float *expert_w,
+                            hipStream_t s) {
     if (R < 1 || R1 < 1 || R2 < 1 || NE < 1 || R > ZR_MAXV || R1 > ZR_MAXV || R2 > ZR_MAXV || NE > 512)
         return fail(LOCALAI_EARG, "zaya router: vector sizes 1..4096, at most 512 routes");
     if ((prev == nullptr) != (eda == nullptr)) return fail(LOCALAI_EARG, "zaya router: prev and eda go together");
     hipLaunchKernelGGL(zaya_router_tail_kernel, dim3(1), dim3(ZR_THREADS), 0, s, r0, b0, prev, eda, norm_w, eps, R,
-                       W1, b1, R1, W2, b2, R2, W3, b3, NE, bias, state, probs, expert);
+                       W1, b1, R1, W2, b2, R2, W3, b3, NE, bias, state, probs, expert, expert_w);
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
 }

@@ -13,9 +13,12 @@ Per MoE layer:
   expert e < E                        gate_up[e] h, SiLU * up, down[e] act,
                                       times probs[e] (engine/zaya.py:303-306)
   e == E (skip)                       h * probs[E] (:297-301)
-The host reads the chosen index (four bytes) to pick the expert tensors, as
-the reference's Python does. Returns (moe [dim] float32, router_state [R]
-float32) like the reference.
+Q4_K / Q6_K experts run as one launch that reads the chosen index and its
+probability on the device (localai_hip_moe_experts1, the skip route
+included), so the host waits only for the outputs. Other expert types take
+the matvec path: the host reads the index (four bytes) to pick the expert
+tensors, as the reference's Python does. Returns (moe [dim] float32,
+router_state [R] float32) like the reference.
 
 Tensors come from `self.gguf`: a localai_amd.gguf.GGUFFile keeps the device
 copies with the file; any other reader with `.tensors` and `._map` (the
@@ -136,6 +139,36 @@ class ZayaMoEMixin(ZayaExpertsMixin):
 
     # ---- the block ----------------------------------------------------------
 
+    def _zaya_experts1(self, p, h_d, expert, expert_w, out, s):
+        """The expert FFN (or the skip route) in one launch from the device-side
+        choice; False when the experts' type has no such kernel."""
+        cache = self._zaya_cache()
+        if cache.get(('experts1', p)) is False:
+            return False
+        gu = self._zaya_matrix(p + 'ffn_gate_up_exps.weight')
+        dn = self._zaya_matrix(p + 'ffn_down_exps.weight')
+        if not (isinstance(gu, device.QMat) and isinstance(dn, device.QMat)):
+            cache[('experts1', p)] = False
+            return False
+        t = device.torch()
+        lib = _lib.load()
+        H, I = h_d.numel(), gu.rows // 2
+        key = ('experts1_ws', gu.batch, H, I)
+        if key not in cache:
+            n = int(lib.localai_hip_moe_workspace_size(1, gu.batch, 1, H, I))
+            if n < 0:
+                raise ValueError(f'{p}: no MoE workspace for experts={gu.batch} hidden={H} inter={I}')
+            cache[key] = t.empty(n, dtype=t.uint8, device=h_d.device)
+        ws = cache[key]
+        ptr = device.ptr
+        st = lib.localai_hip_moe_experts1(ptr(h_d), H, gu.handle, dn.handle, 1, ptr(expert), ptr(expert_w),
+                                          self.n_experts, ptr(out), ptr(ws), ws.numel(), s)
+        if st == 2:   # ETYPE: not Q4_K / Q6_K on the tile form
+            cache[('experts1', p)] = False
+            return False
+        _lib.check(st)
+        return True
+
     def _moe(self, layer, h, prev_router):
         t = device.torch()
         lib = _lib.load()
@@ -153,15 +186,18 @@ class ZayaMoEMixin(ZayaExpertsMixin):
         state = t.empty(L.R, dtype=t.float32, device=dev)
         probs = t.empty(L.routes, dtype=t.float32, device=dev)
         expert = t.empty(1, dtype=t.int32, device=dev)
+        expert_w = t.empty(1, dtype=t.float32, device=dev)
         ptr = device.ptr
         opt = lambda v: ptr(v) if v is not None else None   # noqa: E731
         s = ctypes.c_void_p(device.stream_ptr())
         _lib.check(lib.localai_hip_zaya_router(
             ptr(r0), opt(L.b_inp), opt(prev_d), opt(L.eda if prev_d is not None else None), ptr(L.norm),
             ctypes.c_float(self.eps), L.R, ptr(L.w1), opt(L.b1), L.R1, ptr(L.w2), opt(L.b2), L.R2, ptr(L.w3),
-            opt(L.b3), L.routes, ptr(L.route_bias), ptr(state), ptr(probs), ptr(expert), s))
-        e = int(expert.cpu().item())
+            opt(L.b3), L.routes, ptr(L.route_bias), ptr(state), ptr(probs), ptr(expert), ptr(expert_w), s))
         out = t.empty(hv.size, dtype=t.float32, device=dev)
+        if self._zaya_experts1(p, h_d, expert, expert_w, out, s):
+            return out.cpu().numpy(), state.cpu().numpy()
+        e = int(expert.cpu().item())
         scale = probs[e:e + 1]
         if e == self.n_experts:
             _lib.check(lib.localai_hip_zaya_scale(None, ptr(h_d), hv.size, ptr(scale), ptr(out), s))

@@ -60,8 +60,9 @@ def test_argument_errors_before_device_use():
     one = ctypes.c_void_p(16)
     assert lib.localai_hip_f32_matvec(one, 0, 4, one, 1, one, None) == 1
     assert lib.localai_hip_zaya_router(*([None] * 5), ctypes.c_float(1e-5), 256, None, None, 256, None, None, 256,
-                                       None, None, 17, None, None, None, None, None) == 1
+                                       None, None, 17, None, None, None, None, None, None) == 1
     assert lib.localai_hip_zaya_scale(None, None, 4, None, None, None) == 1
+    assert lib.localai_hip_moe_experts1(None, 64, None, None, 1, None, None, -1, None, None, 0, None) == 1
     with pytest.raises(_lib.HipError):
         _lib.check(lib.localai_hip_dequant(99, None, 0, None, None))
 

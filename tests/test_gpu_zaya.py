@@ -4,6 +4,10 @@ GGUF layer: router MLP (Q8_0 first projection with a bias, F16 / F32 small
 matrices, EDA), Q6_K experts, the skip route and forced experts, through our
 GGUFFile and through a plain reader with only `.tensors` and `._map`.
 
+Q6_K experts run as the one-launch expert kernel (device-side index and skip
+route, localai_hip_moe_experts1); Q8_0 experts take the matvec path with the
+index read on the host; both are checked.
+
 Tolerances: router state normwise <= 1e-6 (exact products, fp32 sums);
 probabilities within 2e-6 absolute; the expert index equal wherever the
 oracle's best two routes are more than 1e-4 apart (np.exp's own rounding is
@@ -24,7 +28,7 @@ E, H, I, R = 16, 1024, 512, 256
 EPS = 1e-5
 
 
-def layer_tensors(rng, route_bias):
+def layer_tensors(rng, route_bias, xt=14):
     f32 = lambda a: np.asarray(a, np.float32)   # noqa: E731
     raw = {
         'ffn_gate_inp.weight': ((R, H), 8, random_ggml(rng, 8, R * H, 2e-4, 6e-4)),
@@ -36,8 +40,8 @@ def layer_tensors(rng, route_bias):
         'zaya_router_mlp2.weight': ((R, R), 0, f32(rng.standard_normal((R, R)) / 16).tobytes()),
         'zaya_router_mlp4.weight': ((E + 1, R), 0, f32(rng.standard_normal((E + 1, R)) / 4).tobytes()),
         'zaya_router_biases.weight': ((E + 1,), 0, f32(route_bias).tobytes()),
-        'ffn_gate_up_exps.weight': ((E, 2 * I, H), 14, random_ggml(rng, 14, E * 2 * I * H, 1e-4, 2e-3)),
-        'ffn_down_exps.weight': ((E, H, I), 14, random_ggml(rng, 14, E * H * I, 1e-4, 2e-3)),
+        'ffn_gate_up_exps.weight': ((E, 2 * I, H), xt, random_ggml(rng, xt, E * 2 * I * H, 1e-4, 2e-3)),
+        'ffn_down_exps.weight': ((E, H, I), xt, random_ggml(rng, xt, E * H * I, 1e-4, 2e-3)),
     }
     return raw
 
@@ -126,11 +130,14 @@ def test_router_probabilities_and_expert(base):
             state = tt.empty(R, dtype=tt.float32, device=r0.device)
             probs = tt.empty(E + 1, dtype=tt.float32, device=r0.device)
             ex = tt.empty(1, dtype=tt.int32, device=r0.device)
+            ew = tt.empty(1, dtype=tt.float32, device=r0.device)
             p = device.ptr
             _lib.check(_lib.load().localai_hip_zaya_router(
                 p(r0), p(L.b_inp), p(pd), p(L.eda), p(L.norm), ctypes.c_float(EPS), R, p(L.w1), p(L.b1), R,
-                p(L.w2), None, R, p(L.w3), None, E + 1, p(L.route_bias), p(state), p(probs), p(ex), None))
+                p(L.w2), None, R, p(L.w3), None, E + 1, p(L.route_bias), p(state), p(probs), p(ex), p(ew), None))
             np.testing.assert_allclose(probs.cpu().numpy(), w_probs, rtol=0, atol=2e-6)
+            # the chosen route's weight: bit for bit probs[expert]
+            assert ew.cpu().numpy().view(np.uint32)[0] == probs.cpu().numpy().view(np.uint32)[int(ex.cpu().item())]
             assert normwise_rel(state.cpu().numpy(), w_state) < 1e-6
             if margin > 1e-4:
                 assert int(ex.cpu().item()) == w_e
@@ -153,3 +160,55 @@ def test_skip_route_and_forced_expert(tmp_path, forced):
     assert w_e == forced
     assert normwise_rel(state, w_state) < 1e-6
     assert normwise_rel(moe, w_moe) < (1e-6 if forced == E else 1e-5)
+
+
+@pytest.mark.parametrize('forced', [E, 3])
+def test_matvec_path_for_q8_0_experts(tmp_path, forced):
+    """Q8_0 experts have no one-launch kernel: the block reads the index on the
+    host and runs the matvecs; the skip route and an expert both checked."""
+    from localai_amd.gguf import GGUFFile
+    rng = np.random.default_rng(40 + forced)
+    bias = np.zeros(E + 1)
+    bias[forced] = 10.0
+    raw = layer_tensors(rng, bias, xt=8)
+    path = tmp_path / 'q8.gguf'
+    write_layer(path, raw)
+    t = oracle_tensors(raw)
+    h = rng.standard_normal(H).astype(np.float32)
+    with GGUFFile(path) as g:
+        m = model_class()(g)
+        moe, state = m._moe(1, h, None)
+        assert m._zaya_cache().get(('experts1', 'blk.1.')) is False
+    w_moe, w_state, _, w_e, _ = zm.moe_block(t, E, EPS, h, None)
+    assert w_e == forced
+    assert normwise_rel(state, w_state) < 1e-6
+    assert normwise_rel(moe, w_moe) < (1e-6 if forced == E else 1e-5)
+
+
+def test_experts1_two_slots_with_skip(base):
+    """localai_hip_moe_experts1 with top_k 2, one slot an expert and one the
+    skip route: out = w0 * expert(h) + w1 * h, against the oracle's products."""
+    from localai_amd import _lib, device
+    from localai_amd.gguf import GGUFFile
+    path, t = base
+    rng = np.random.default_rng(9)
+    tt = device.torch()
+    lib = _lib.load()
+    with GGUFFile(path) as g:
+        gu = g.device_matrix('blk.1.ffn_gate_up_exps.weight')
+        dn = g.device_matrix('blk.1.ffn_down_exps.weight')
+        for e0, w in ((7, (0.625, 0.375)), (0, (0.9, 0.1))):
+            h = rng.standard_normal(H).astype(np.float32)
+            hd = device.to_device_f32(h)
+            idx = tt.tensor([e0, E], dtype=tt.int32, device=hd.device)
+            wt = tt.tensor(w, dtype=tt.float32, device=hd.device)
+            out = tt.empty(H, dtype=tt.float32, device=hd.device)
+            n = int(lib.localai_hip_moe_workspace_size(1, E, 2, H, I))
+            ws = tt.empty(n, dtype=tt.uint8, device=hd.device)
+            p = device.ptr
+            _lib.check(lib.localai_hip_moe_experts1(p(hd), H, gu.handle, dn.handle, 2, p(idx), p(wt), E, p(out),
+                                                    p(ws), n, None))
+            gate, up = np.split(zm.mat(t['gate_up'][e0], h), 2)
+            y = zm.mat(t['down'][e0], gate / (1.0 + np.exp(-np.clip(gate, -80, 80))) * up)
+            want = np.float32(w[0]) * y + np.float32(w[1]) * h
+            assert normwise_rel(out.cpu().numpy(), want) < 1e-5
