@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__
                                                        _Float16 *__restrict__ Xh, int ldh,
                                                        float *__restrict__ inv, int vec) {
     const int lane = lane_id();
-    const int64_t t = (int64_t)blockIdx.x * 4 + wave_id();
+    const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id();
     if (t >= ntok) return;
     const int64_t src = rows_map ? (int64_t)(rows_map[t] / k) : t;
     const float *x = X + src * ldx;
@@ -732,9 +732,13 @@ int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *ro
     if (cols % 8 || ldh % 8 || ldh < cols) return fail(LOCALAI_EARG, "f16 rows: cols % 8 != 0");
     const int vec = (uintptr_t)X % 16 == 0 && ldx % 4 == 0;
     const int per = (int)((ldh / 8 + 63) / 64);   // 8-value groups per lane
-    const dim3 grid((unsigned)((ntok + 3) / 4));
+    // one token per wave; one-wave workgroups below 1024 tokens, so that 512
+    // tokens reach every CU (four-wave workgroups left half of them idle)
+    const int wpg = ntok < 1024 ? 1 : 4;
+    const dim3 grid((unsigned)((ntok + wpg - 1) / wpg));
     auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, X, ldx, (int)cols, rows_map, k, ntok, Xh, (int)ldh, inv, vec);
+        hipLaunchKernelGGL(kern, grid, dim3(64 * wpg), 0, s, X, ldx, (int)cols, rows_map, k, ntok, Xh, (int)ldh, inv,
+                           vec);
     };
     if (per <= 1)
         go(x_to_f16_kernel<1>);
