@@ -194,8 +194,9 @@ int localai_hip_moe_forward(const float *h_dev, int64_t tokens, int64_t hidden,
  *       = down[e] (silu(gate) * up)(gate_up[e] h) otherwise (e = expert[s])
  * skip = -1 when every slot is an expert. One launch for gate_up and down
  * (plus a counter clear); the sum is the same whatever order the slots land.
- * Experts must be Q4_K or Q6_K handles with the tile form (ETYPE otherwise:
- * the caller then runs the matvec path). Workspace: as
+ * Experts must be Q4_K or Q6_K handles with the tile form, at most 32
+ * super-blocks a row and inter % 64 == 0 (ETYPE otherwise: the caller then
+ * runs the matvec path). Workspace: as
  * localai_hip_moe_workspace_size(1, experts, top_k, hidden, inter); h_dev
  * 16-byte and the workspace 256-byte aligned; out must not overlap h. */
 int localai_hip_moe_experts1(const float *h_dev, int64_t hidden, const localai_qmat *gate_up,

@@ -328,8 +328,11 @@ int localai_hip_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, 
     if (H < 1 || k < 1 || k > 2) return fail(LOCALAI_EARG, "moe experts: hidden >= 1 and top_k 1 or 2");
     const int64_t E = gu->g.batch, I = gu->g.rows / 2;
     if (dn->g.batch != E) return fail(LOCALAI_EARG, "moe experts: gate_up and down hold different expert counts");
-    if (gu->g.cols != H || gu->g.rows % 2 || I % 64) return fail(LOCALAI_EARG, "moe experts: gate_up must be [E, 2*inter, hidden] with inter % 64 == 0");
+    if (gu->g.cols != H || gu->g.rows % 2) return fail(LOCALAI_EARG, "moe experts: gate_up must be [E, 2*inter, hidden]");
     if (dn->g.rows != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe experts: down must be [E, hidden, inter]");
+    // shapes the fused kernel does not cover are ETYPE, like unsupported
+    // types: the caller falls back to the matvec path
+    if (I % 64) return fail(LOCALAI_ETYPE, "moe experts: inter % 64 != 0");
     if (ws_bytes < (int64_t)moe_workspace_bytes(1, E, k, H, I)) return fail(LOCALAI_EARG, "moe experts: workspace too small");
     if ((reinterpret_cast<uintptr_t>(h) & 15) || (reinterpret_cast<uintptr_t>(ws) & 255))
         return fail(LOCALAI_EARG, "moe experts: h must be 16-byte and workspace 256-byte aligned");
