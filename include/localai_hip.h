@@ -192,7 +192,10 @@ int localai_hip_moe_forward(const float *h_dev, int64_t tokens, int64_t hidden,
  *   out_dev[hidden] = sum_s weight[s] * y_s, s < top_k (1 or 2), where
  *   y_s = h                                      if expert[s] == skip
  *       = down[e] (silu(gate) * up)(gate_up[e] h) otherwise (e = expert[s])
- * skip = -1 when every slot is an expert. One launch for gate_up and down
+ * skip = -1 when every slot is an expert, else an index >= the expert count
+ * (EARG for 0 <= skip < experts); an index in expert_dev outside
+ * [0, experts) that is not skip makes that slot's rows of out NaN and is
+ * reported by localai_hip_moe_error. One launch for gate_up and down
  * (plus a counter clear); the sum is the same whatever order the slots land.
  * Experts must be Q4_K or Q6_K handles with the tile form, at most 32
  * super-blocks a row and inter % 64 == 0 (ETYPE otherwise: the caller then
@@ -203,6 +206,24 @@ int localai_hip_moe_experts1(const float *h_dev, int64_t hidden, const localai_q
                              const localai_qmat *down, int top_k, const int32_t *expert_dev,
                              const float *weight_dev, int32_t skip, float *out_dev, void *workspace_dev,
                              int64_t workspace_bytes, void *stream);
+
+/* Status of the last one-token fused expert launch that used this workspace
+ * (localai_hip_moe_experts1, or localai_hip_moe_forward with one token and
+ * top_k <= 2), which hands gate_up results to its down workgroups inside one
+ * launch. Waits for `stream`, then reads the launch's error word: LOCALAI_EARG
+ * if an expert index was outside [0, experts) and not the skip route,
+ * LOCALAI_EHIP if a bounded wait ran out; either way the affected rows of out
+ * are NaN. tokens / experts: as passed to that call. No counterpart in the
+ * reference (its expert call raises synchronously, engine/native_quant.py:115-116). */
+int localai_hip_moe_error(const void *workspace_dev, int64_t tokens, int64_t experts, void *stream);
+
+/* Test control of the fused expert kernel's waits: at most spin_limit polls
+ * per wait (<= 0: the default, seconds in all), and producers_count = 0 keeps
+ * the gate_up workgroups from counting themselves done, so every wait runs
+ * out and every workgroup still exits (the error path of
+ * localai_hip_moe_error). Process-wide; (0, 1) restores the defaults. No
+ * counterpart in the reference. */
+int localai_hip_debug_fused_wait(int spin_limit, int producers_count);
 
 /* ---- host weight registration for the legacy exports -------------------- */
 

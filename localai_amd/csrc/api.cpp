@@ -327,6 +327,7 @@ int localai_hip_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, 
     if (!h || !gu || !dn || !expert || !weight || !out || !ws) return fail(LOCALAI_EARG, "moe experts: null pointer");
     if (H < 1 || k < 1 || k > 2) return fail(LOCALAI_EARG, "moe experts: hidden >= 1 and top_k 1 or 2");
     const int64_t E = gu->g.batch, I = gu->g.rows / 2;
+    if (skip >= 0 && skip < E) return fail(LOCALAI_EARG, "moe experts: skip must be -1 or an index >= experts");
     if (dn->g.batch != E) return fail(LOCALAI_EARG, "moe experts: gate_up and down hold different expert counts");
     if (gu->g.cols != H || gu->g.rows % 2) return fail(LOCALAI_EARG, "moe experts: gate_up must be [E, 2*inter, hidden]");
     if (dn->g.rows != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe experts: down must be [E, hidden, inter]");
@@ -338,6 +339,22 @@ int localai_hip_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, 
         return fail(LOCALAI_EARG, "moe experts: h must be 16-byte and workspace 256-byte aligned");
     if (int st = ensure_device()) return st;
     return launch_moe_experts1(h, H, gu, dn, k, expert, weight, skip, out, ws, (hipStream_t)stream);
+}
+
+int localai_hip_moe_error(const void *ws, int64_t T, int64_t E, void *stream) {
+    clear_error();
+    if (!ws || T < 1 || E < 1) return fail(LOCALAI_EARG, "moe error: null workspace or sizes < 1");
+    if (int st = ensure_device()) return st;
+    uint32_t word = 0;
+    if (int st = moe_error_word(ws, T, E, (hipStream_t)stream, &word)) return st;
+    if (word & 2u) return fail(LOCALAI_EARG, "moe: an expert index was outside [0, experts) and not the skip route");
+    if (word & 1u) return fail(LOCALAI_EHIP, "moe: a wait of the fused expert kernel ran out (output rows are NaN)");
+    return LOCALAI_OK;
+}
+
+int localai_hip_debug_fused_wait(int spin_limit, int producers_count) {
+    clear_error();
+    return set_fused_wait(spin_limit, producers_count);
 }
 
 int64_t localai_hip_moe_workspace_size(int64_t T, int64_t E, int k, int64_t H, int64_t I) {

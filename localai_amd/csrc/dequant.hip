@@ -30,21 +30,21 @@ __device__ __forceinline__ uint32_t kq_min(const uint8_t *s, int g) {
 template <int T>
 __device__ __forceinline__ void decode8(const uint8_t *__restrict__ blk, int e0, float v[8]) {
     if constexpr (T == LQ_Q8_0) {
-        const float d = f16_to_f32(rd16(blk, 0));
+        const float d = f16_to_f32_bits(rd16(blk, 0));
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)blk[2 + e0 + i] * d;
     } else if constexpr (T == LQ_Q4_0 || T == LQ_Q4_1) {
-        const float d = f16_to_f32(rd16(blk, 0));
+        const float d = f16_to_f32_bits(rd16(blk, 0));
         const int qo = T == LQ_Q4_0 ? 2 : 4;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             int e = e0 + i;
             uint32_t q = (blk[qo + (e & 15)] >> (4 * (e >> 4))) & 15u;
             if constexpr (T == LQ_Q4_0) v[i] = ((float)q - 8.0f) * d;
-            else v[i] = __builtin_fmaf((float)q, d, f16_to_f32(rd16(blk, 2)));
+            else v[i] = __builtin_fmaf((float)q, d, f16_to_f32_bits(rd16(blk, 2)));
         }
     } else if constexpr (T == LQ_Q5_0 || T == LQ_Q5_1) {
-        const float d = f16_to_f32(rd16(blk, 0));
+        const float d = f16_to_f32_bits(rd16(blk, 0));
         const int ho = T == LQ_Q5_0 ? 2 : 4;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -53,11 +53,11 @@ __device__ __forceinline__ void decode8(const uint8_t *__restrict__ blk, int e0,
             uint32_t hi = (blk[ho + (e >> 3)] >> (e & 7)) & 1u;
             float q = (float)(lo | (hi << 4));
             if constexpr (T == LQ_Q5_0) v[i] = (q - 16.0f) * d;
-            else v[i] = __builtin_fmaf(q, d, f16_to_f32(rd16(blk, 2)));
+            else v[i] = __builtin_fmaf(q, d, f16_to_f32_bits(rd16(blk, 2)));
         }
     } else if constexpr (T == LQ_Q4_K || T == LQ_Q5_K) {
-        const float d = f16_to_f32(rd16(blk, 0));
-        const float dmin = f16_to_f32(rd16(blk, 2));
+        const float d = f16_to_f32_bits(rd16(blk, 0));
+        const float dmin = f16_to_f32_bits(rd16(blk, 2));
         const int g = e0 >> 5, j0 = e0 & 31;
         const float scale = d * (float)kq_scale(blk + 4, g);
         const float minimum = dmin * (float)kq_min(blk + 4, g);
@@ -70,7 +70,7 @@ __device__ __forceinline__ void decode8(const uint8_t *__restrict__ blk, int e0,
             v[i] = __builtin_fmaf((float)q, scale, -minimum);
         }
     } else if constexpr (T == LQ_Q6_K) {
-        const float d = f16_to_f32(rd16(blk, 208));
+        const float d = f16_to_f32_bits(rd16(blk, 208));
         const int h = e0 >> 7, c = (e0 >> 5) & 3, j0 = e0 & 31;
         const float ds = d * (float)(int8_t)blk[192 + 8 * h + 2 * c + (j0 >> 4)];
         const uint8_t *ql = blk + 64 * h + 32 * (c & 1);
@@ -106,7 +106,7 @@ __global__ void dequant_kernel(const uint8_t *__restrict__ raw, int64_t nvals, f
 __global__ void dequant_f16_kernel(const uint16_t *__restrict__ raw, int64_t n, float *__restrict__ out) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
-        out[i] = f16_to_f32(raw[i]);
+        out[i] = f16_to_f32_bits(raw[i]);
 }
 
 int launch_dequant_ggml(int t, const void *raw, int64_t n, float *out, hipStream_t s) {

@@ -9,11 +9,25 @@ namespace lq {
 
 typedef float lq_f4 __attribute__((ext_vector_type(4)));   // one 16-byte register tuple
 
-// IEEE binary16 -> binary32, exact for every input (subnormals, inf, NaN);
-// same values as half_to_float, engine/native_quant.cpp:12-33.
+// IEEE binary16 -> binary32 by the hardware conversion (one instruction):
+// exact for every finite value and both infinities; a signalling NaN comes
+// out quiet. Used where the value only feeds arithmetic (matvec / GEMM scales).
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
     _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffffu));
     return (float)h;
+}
+
+// IEEE binary16 -> binary32 keeping NaN payloads bit for bit (a signalling
+// NaN stays signalling): sign | 0x7f800000 | mantissa << 13, as half_to_float
+// does (engine/native_quant.cpp:12-33) and as NumPy's '<f2' widening does
+// (engine/dequant.py:20-24). Every other input takes the hardware conversion,
+// which is exact for them. Used by the dequant kernels, whose outputs are
+// compared bit for bit.
+__device__ __forceinline__ float f16_to_f32_bits(uint32_t bits16) {
+    const uint32_t h = bits16 & 0xffffu;
+    const float f = f16_to_f32(h);
+    const uint32_t nan = ((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13);
+    return (h & 0x7c00u) == 0x7c00u && (h & 0x3ffu) ? __builtin_bit_cast(float, nan) : f;
 }
 
 // Byte i of a dword as float: each maps to one v_cvt_f32_ubyte{0..3}.

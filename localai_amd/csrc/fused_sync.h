@@ -20,10 +20,18 @@ enum {
     D1_WORDS = D1_ERROR + D1_LINE
 };
 
-// Bound on every wait of the fused layer (seconds of polling): a wait that
-// runs out sets D1_ERROR and its workgroup skips its stores (wrong output
-// instead of a hang).
+// Default bound on every wait of the fused layer (polls, seconds in all): a
+// wait that runs out sets D1_ERR_WAIT in the error word and its workgroup
+// adds NaN to its rows of the output, so the failure shows in the result and
+// the host can read the word afterwards (localai_hip_moe_error).
 constexpr int D1_SPIN_LIMIT = 1 << 22;
+// Bits of the error word
+constexpr uint32_t D1_ERR_WAIT = 1u;    // a wait for the gate_up tiles ran out
+constexpr uint32_t D1_ERR_INDEX = 2u;   // an expert index outside [0, E) that is not the skip route
+
+__device__ __forceinline__ void d1_error(uint32_t *sync, uint32_t bit) {
+    __hip_atomic_fetch_or(sync + D1_ERROR, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Data handed between workgroups of the fused layer moves with device-
 // coherent (relaxed, device-scope atomic) loads and stores, which bypass the
@@ -42,20 +50,21 @@ __device__ __forceinline__ void d1_drain() { asm volatile("s_waitcnt vmcnt(0)" :
 
 // Whole workgroup: wait until the all-done flag is set. One thread polls: a
 // first sleep of about 8000 cycles (the gate_up tiles take several times
-// that), then about 1000 cycles between polls; the others wait at the
-// barrier. false: the wait ran out. flag: one int of LDS.
-__device__ __forceinline__ bool d1_wait_done(uint32_t *sync, int *flag) {
+// that), then about 1000 cycles between polls, at most `spin` polls; the
+// others wait at the barrier. false: the wait ran out (D1_ERR_WAIT is set).
+// flag: one int of LDS.
+__device__ __forceinline__ bool d1_wait_done(uint32_t *sync, int *flag, int spin) {
     if (threadIdx.x == 0) {
         int ok = 0;
         __builtin_amdgcn_s_sleep(127);
-        for (int n = 0; n < D1_SPIN_LIMIT; ++n) {
+        for (int n = 0; n < spin; ++n) {
             if (d1_get(sync + D1_DONE) != 0u) {
                 ok = 1;
                 break;
             }
             __builtin_amdgcn_s_sleep(15);
         }
-        if (!ok) d1_put(sync + D1_ERROR, 1u);
+        if (!ok) d1_error(sync, D1_ERR_WAIT);
         *flag = ok;
     }
     __syncthreads();

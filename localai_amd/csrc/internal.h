@@ -81,6 +81,10 @@ size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I
 int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const float *rb, int64_t E, int k,
                const localai_qmat *gu, const localai_qmat *dn, float *out, int32_t *topk_idx, float *topk_w,
                void *ws, hipStream_t s);
+// error word of the fused one-token expert kernel in a MoE workspace (after
+// the stream has finished); test controls of its waits
+int moe_error_word(const void *ws, int64_t T, int64_t E, hipStream_t s, uint32_t *word);
+int set_fused_wait(int spin, int count);
 int launch_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, const localai_qmat *dn, int k,
                         const int32_t *topk_idx, const float *topk_w, int skip, float *out, void *ws,
                         hipStream_t s);

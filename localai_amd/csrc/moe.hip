@@ -31,6 +31,8 @@
 // pairwise tree over the 64 lanes), rounded to fp32 once.
 #include <math.h>
 
+#include <atomic>
+
 #include "gemv_core.h"
 #include "internal.h"
 #include "fused_sync.h"
@@ -486,6 +488,9 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__rest
     int *cnt = ws;
     int *off = ws + 16 * E;
     for (int i = threadIdx.x; i < 16 * E; i += blockDim.x) cnt[i] = 0;
+    // the fused one-token kernel's counter block, whose error word
+    // localai_hip_moe_error reads, is unused on the paths that permute
+    for (int i = threadIdx.x; i < D1_WORDS; i += blockDim.x) tb.sync[i] = 0u;
     __syncthreads();
     const int nbits = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 0;
     const int per = (N + nw - 1) / nw;
@@ -792,12 +797,17 @@ __global__ void moe_combine_kernel(const float *__restrict__ ysl, const int32_t 
 // expert output; its gate_up tiles read no weights but still clear and
 // count. A template flag because the test costs the plain top-k layer
 // 0.5 us (13.2 vs 12.7 us, Q6_K, hidden 2048, top-2).
+// Failures are loud: an expert index outside [0, E) that is not the skip
+// route, or a wait that runs out (spin polls), sets a bit of the error word
+// (sync + D1_ERROR) and makes the affected rows of out NaN. count = 0 keeps
+// the gate_up tiles from counting themselves done (a test of the error path:
+// every wait then runs out and every workgroup still exits).
 template <int TYPE, int SPWG, int SPWD, bool SKIP>
 __global__ __launch_bounds__(512) void moe_decode1_kernel(
     const float *__restrict__ h, int H, int E, int k, const uint8_t *__restrict__ gu_t, int64_t gu_bytes, int nbg,
     int64_t inter, const uint8_t *__restrict__ dn_t, int64_t dn_bytes, int nbd,
     const int32_t *__restrict__ topk_idx, const float *__restrict__ topk_w, float *__restrict__ out, MoeTables tb,
-    uint32_t *__restrict__ sync, int skip) {
+    uint32_t *__restrict__ sync, int skip, int spin, int count) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int flag;
     const int r = blockIdx.x;
@@ -807,9 +817,13 @@ __global__ __launch_bounds__(512) void moe_decode1_kernel(
     if (r < n_gu) {
         const int s = r / gtiles, i = r % gtiles;
         const int n = threadIdx.x;
-        if (!SKIP || topk_idx[s] != skip) {   // the same for the whole workgroup
+        const int idx = topk_idx[s];   // the same for the whole workgroup
+        const bool is_skip = SKIP && idx == skip;
+        if (!is_skip && (idx < 0 || idx >= E)) {
+            if (n == 0 && i == 0) d1_error(sync, D1_ERR_INDEX);
+        } else if (!is_skip) {
             const int sb0 = w * SPWG, nsb = mt_nsb(nbg, sb0, SPWG);
-            const int e = min(max(topk_idx[s], 0), E - 1);
+            const int e = idx;
             const uint8_t *We = gu_t + (int64_t)e * gu_bytes;
             const int64_t tb_bytes = (int64_t)nbg * mt_block_bytes(TYPE);
             MtW<TYPE> wt[2][SPWG];
@@ -825,29 +839,32 @@ __global__ __launch_bounds__(512) void moe_decode1_kernel(
         for (int c = r * per + n; c < (r + 1) * per && c < H; c += blockDim.x) d1_put(out + c, 0.0f);
         d1_drain();
         __syncthreads();
-        if (threadIdx.x == 0) d1_count(sync, r, n_gu);
+        if (threadIdx.x == 0 && count) d1_count(sync, r, n_gu);
         return;
     }
     const int j = r - n_gu, s = j / dtiles, i = j % dtiles;
     const float gate = topk_w[s];
-    if (SKIP && topk_idx[s] == skip) {   // out += gate * h on this tile's rows
-        const bool ok = d1_wait_done(sync, &flag);
+    const int idx = topk_idx[s];
+    const float nan = __builtin_nanf("");
+    if (SKIP && idx == skip) {   // out += gate * h on this tile's rows
+        const bool ok = d1_wait_done(sync, &flag, spin);
         const int row = i * MT_ROWS + (int)threadIdx.x;
-        if (threadIdx.x < MT_ROWS && row < H && ok) atomicAdd(out + row, gate * h[row]);
+        if (threadIdx.x < MT_ROWS && row < H) atomicAdd(out + row, ok ? gate * h[row] : nan);
         return;
     }
+    const bool bad = idx < 0 || idx >= E;   // flagged by the slot's gate_up tiles
     const int sb0 = w * SPWD, nsb = mt_nsb(nbd, sb0, SPWD);
-    const int e = min(max(topk_idx[s], 0), E - 1);
+    const int e = bad ? 0 : idx;
     MtW<TYPE> wt[1][SPWD];
     mt_load_tile<TYPE, SPWD>(wt[0], dn_t + (int64_t)e * dn_bytes + i * (int64_t)nbd * mt_block_bytes(TYPE), nbd, sb0,
                              nsb, lane);
-    const bool ok = d1_wait_done(sync, &flag);
+    const bool ok = d1_wait_done(sync, &flag, spin) && !bad;
     float4 xv[1][SPWD];
     d1_load_x<SPWD>(xv[0], tb.act + (int64_t)s * inter, nbd, sb0, lane);
     float *fin;
     mt_pass<TYPE, SPWD, 1, 1>(wt, xv, nsb, smem, fin);
     const int n = threadIdx.x;
-    if (n < MT_ROWS && i * MT_ROWS + n < H && ok) atomicAdd(out + i * MT_ROWS + n, gate * fin[n]);
+    if (n < MT_ROWS && i * MT_ROWS + n < H) atomicAdd(out + i * MT_ROWS + n, ok ? gate * fin[n] : nan);
 }
 
 // ---------------------------------------------------------------- host side
@@ -1004,6 +1021,23 @@ static int d1_spw(int64_t nb) {
     return v <= 1 ? 1 : v <= 2 ? 2 : 4;
 }
 
+// Test controls of the fused kernel's waits (localai_hip_debug_fused_wait):
+// the polling bound, and whether the gate_up tiles count themselves done.
+static std::atomic<int> g_d1_spin{D1_SPIN_LIMIT}, g_d1_count{1};
+
+int set_fused_wait(int spin, int count) {
+    g_d1_spin.store(spin > 0 ? spin : D1_SPIN_LIMIT);
+    g_d1_count.store(count ? 1 : 0);
+    return LOCALAI_OK;
+}
+
+int moe_error_word(const void *ws, int64_t T, int64_t E, hipStream_t s, uint32_t *word) {
+    const uint32_t *sync = (const uint32_t *)((const uint8_t *)ws + align256((size_t)(T * E * 4)));
+    LQ_HIP(hipStreamSynchronize(s));
+    LQ_HIP(hipMemcpy(word, sync + D1_ERROR, 4, hipMemcpyDeviceToHost));
+    return LOCALAI_OK;
+}
+
 template <int TYPE, int SG, int SD>
 static void launch_decode1_k(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
                              int64_t H, int64_t E, int k, int64_t I, const int32_t *topk_idx, const float *topk_w,
@@ -1013,7 +1047,7 @@ static void launch_decode1_k(const localai_qmat *gu, const localai_qmat *dn, con
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(grid), dim3(512), a > b ? a : b, s, h, (int)H, (int)E, k, gu->tiles,
                            gu->tile_bytes, (int)gu->g.nb, I, dn->tiles, dn->tile_bytes, (int)dn->g.nb, topk_idx,
-                           topk_w, out, tb, tb.sync, skip);
+                           topk_w, out, tb, tb.sync, skip, g_d1_spin.load(), g_d1_count.load());
     };
     if (skip >= 0)
         go(moe_decode1_kernel<TYPE, SG, SD, true>);

@@ -86,9 +86,21 @@ class MoELayer:
             raise ValueError(f'no forward over {tokens} tokens yet')
         return ws[:tokens * self.E * 4].view(device.torch().float32).reshape(tokens, self.E)
 
+    def check(self, tokens, stream=None):
+        """Wait for `stream` and raise if the last forward over `tokens` tokens
+        ran the fused one-token expert kernel and one of its device-side checks
+        failed (an expert index out of range, or a hand-off wait that ran out:
+        its output rows are then NaN)."""
+        ws = self._ws.get(tokens)
+        if ws is not None:
+            _lib.check(_lib.load().localai_hip_moe_error(device.ptr(ws), tokens, self.E,
+                                                          ctypes.c_void_p(device.stream_ptr(stream))))
+
     def forward(self, h):
         """numpy [T, H] -> numpy (out [T, H], topk_idx [T, k], gates [T, k])."""
-        o, i, g = self.forward_device(device.to_device_f32(np.atleast_2d(h)))
+        h = np.atleast_2d(h)
+        o, i, g = self.forward_device(device.to_device_f32(h))
+        self.check(h.shape[0])
         return o.cpu().numpy(), i.cpu().numpy(), g.cpu().numpy()
 
 

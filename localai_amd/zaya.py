@@ -196,6 +196,9 @@ class ZayaMoEMixin(ZayaExpertsMixin):
             opt(L.b3), L.routes, ptr(L.route_bias), ptr(state), ptr(probs), ptr(expert), ptr(expert_w), s))
         out = t.empty(hv.size, dtype=t.float32, device=dev)
         if self._zaya_experts1(p, h_d, expert, expert_w, out, s):
+            ws = self._zaya_cache()[('experts1_ws', self.n_experts, hv.size,
+                                     self._zaya_matrix(p + 'ffn_gate_up_exps.weight').rows // 2)]
+            _lib.check(lib.localai_hip_moe_error(ptr(ws), 1, self.n_experts, s))   # waits for the stream
             return out.cpu().numpy(), state.cpu().numpy()
         e = int(expert.cpu().item())
         scale = probs[e:e + 1]

@@ -25,8 +25,14 @@ Parity status (what pins each function; details in the test files):
   quant.matvec_exact / matmul_exact: fp64 sums of exact products; pinned by
                     the reference's own tolerances against oracle/_ref.
   quant.q8_activation_matvec: pinned against oracle/_ref's Q4_K/Q5_K matvec.
-  moe.*             parity unpinned by the reference (it has no top-k>1 MoE
-                    and no MoE test); pinned by invariants (permutation round
-                    trip, histogram totals, gates summing to one, forced ties,
-                    reduction to a dense matvec for a one-expert layer).
+  moe.*             no reference output exists (the reference has no top-k>1
+                    MoE and no MoE test); pinned by invariants and reductions
+                    to pinned pieces: permutation round trip, histogram
+                    totals, gates summing to one, forced ties, router logits
+                    against math.fsum, one-expert and identical-expert layers
+                    (any k) against quant.matvec_exact + SciPy's expit, an
+                    exact doubling of one expert moving only its gated term,
+                    SiLU against x * expit(x).
+  quant F16 widening: pinned on all 65536 patterns against an integer
+                    restatement of half_to_float (NaN payloads included).
 """

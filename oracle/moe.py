@@ -16,10 +16,14 @@ exact fp64 products h*w in a fixed order (64 lane sums over interleaved
 4-element chunks, then a pairwise tree over the lanes), rounded once to fp32. The ranking key is
 (logit descending, expert index ascending).
 
-parity unpinned by the reference (no top-k>1 MoE, no MoE test); the tests pin
-it through invariants instead: permutation round trip, histogram totals,
-gates summing to one, forced ties, and equality with the dense matvec oracle
-for a one-expert layer.
+The reference has no top-k>1 MoE and no MoE test, so no reference output pins
+this module; tests/test_oracle_moe.py pins it through checks that a dropped,
+doubled or misplaced term fails: permutation round trip, histogram totals,
+gates summing to one, forced ties, the router logit against math.fsum, the
+one-expert layer and the all-experts-identical layer (any k) against a dense
+FFN built from quant.matvec_exact and SciPy's expit, an exact doubling of
+one expert's down weights that must move the output by exactly that
+expert's gated term, and SiLU against x * expit(x) and its limits.
 """
 from __future__ import annotations
 

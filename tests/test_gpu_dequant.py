@@ -80,3 +80,52 @@ def test_repack_round_trip_and_expert_dequant(t, rows, cols, batch):
         want = quant.dequantize(raw[e * per:(e + 1) * per], t, (rows, cols))
         np.testing.assert_array_equal(bits(got), bits(want))
     q.close()
+
+
+ALL_F16 = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+
+
+def _nan_aware_equal(got, ref):
+    """Bit equality wherever the oracle value is not a NaN; NaN exactly where
+    the oracle has one. NaN payloads that went through a product or a
+    difference are not compared: x86 and gfx950 propagate NaN payloads and
+    signs through arithmetic differently, and the reference's arithmetic on a
+    NaN scale gives a NaN with no meaningful payload either way."""
+    got, ref = np.asarray(got, np.float32), np.asarray(ref, np.float32)
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(bits(got)[~nan], bits(ref)[~nan])
+
+
+def test_dequant_f16_every_bit_pattern():
+    """All 65536 fp16 patterns as the F16 type: bit for bit, NaN payloads and
+    signalling NaNs included (engine/dequant.py:20-24; half_to_float,
+    engine/native_quant.cpp:12-33)."""
+    from localai_amd import dequant
+    raw = ALL_F16.tobytes()
+    got = dequant.dequantize(raw, 1, (65536,))
+    ref = quant.dequantize(raw, 1, (65536,))
+    np.testing.assert_array_equal(bits(got), bits(ref))
+
+
+@pytest.mark.parametrize('t', (8, 2, 3, 6, 7, 12, 13, 14))
+def test_dequant_every_fp16_scale_pattern(t):
+    """Every fp16 pattern as the block scale d (and, with a different pattern
+    per block, as the second fp16 field: dmin of Q4_K / Q5_K, m of Q4_1 /
+    Q5_1), random quants: bit-exact for every non-NaN value, NaN where the
+    oracle has NaN."""
+    from localai_amd import dequant
+    block, bpb = quant.block_layout(t)
+    rng = np.random.default_rng(900 + t)
+    nb = 65536
+    buf = rng.integers(0, 256, size=(nb, bpb), dtype=np.uint8)
+    off = 208 if t == 14 else 0
+    buf[:, off:off + 2] = ALL_F16.view(np.uint8).reshape(nb, 2)
+    if t in (3, 7, 12, 13):
+        second = ALL_F16[(np.arange(nb) * 7919) % nb]
+        buf[:, 2:4] = second.view(np.uint8).reshape(nb, 2)
+    raw = buf.tobytes()
+    got = dequant.dequantize(raw, t, (nb * block,))
+    with np.errstate(invalid='ignore', over='ignore'):
+        ref = quant.dequantize(raw, t, (nb * block,))
+    _nan_aware_equal(got, ref)

@@ -217,9 +217,9 @@ def test_legacy_registered_range_uses_cached_copy():
 
 
 @pytest.mark.parametrize('t,rows,cols', [(12, 14336, 4096), (14, 4096, 14336), (14, 1024, 4096), (8, 512, 4096)])
-def test_split_k_is_deterministic_and_rearms(t, rows, cols):
-    """Split-K workgroups combine through per-tile counters that the last
-    arrival resets; 30 back-to-back launches must give identical bits."""
+def test_repeated_launches_are_bit_identical(t, rows, cols):
+    """The waves of a workgroup meet in LDS in a fixed order (no atomics), so
+    30 back-to-back launches at the Llama-3-8B shapes must give identical bits."""
     import torch
     from localai_amd import device, synth
     rng = np.random.default_rng(77)
@@ -236,10 +236,10 @@ def test_split_k_is_deterministic_and_rearms(t, rows, cols):
 
 @pytest.mark.parametrize('t,rows,cols', [(12, 5 * 64, 16384), (14, 7 * 64 - 3, 14336), (12, 9 * 64, 8192),
                                          (8, 13 * 64 + 1, 8192), (14, 3 * 64, 4096), (12, 17 * 64, 4096)])
-def test_split_k_across_xcds(t, rows, cols):
-    """Tile counts that are not multiples of the 8 XCDs, so the split-K
-    workgroups of one tile are dispatched to different XCDs (separate L2s):
-    the partials must still combine exactly, launch after launch."""
+def test_tile_counts_not_multiple_of_xcds(t, rows, cols):
+    """Row-tile counts that are not multiples of the 8 XCDs and long rows (up
+    to 64 super-blocks, the 768-thread plan): each launch matches the oracle
+    and every launch gives the same bits."""
     import torch
     from localai_amd import device, synth
     rng = np.random.default_rng(rows + cols)
@@ -311,3 +311,77 @@ def test_matvec_many_experts_and_errors():
     finally:
         m.close()
         other.close()
+
+
+@pytest.mark.parametrize('group', [
+    # ffn_gate / ffn_up of one Llama-3-8B decode step (engine/model.py:232): the
+    # two-matrix Q4_K launch of the decode-layer benchmark
+    [('ffn_gate', 12, 14336, 4096), ('ffn_up', 12, 14336, 4096)],
+    # attn_q / attn_k / attn_v (engine/model.py:185-187), Q4_K / Q4_K / Q6_K
+    [('attn_q', 12, 4096, 4096), ('attn_k', 12, 1024, 4096), ('attn_v', 14, 1024, 4096)],
+])
+def test_matvec_many_llama3_8b_groups(group):
+    """The fused launches of the decode-layer benchmark at their exact shapes
+    and input distributions: each output bit-identical to a single-matrix
+    launch and within 1e-5 normwise of the fp64 oracle."""
+    from localai_amd import device, synth
+    rng = np.random.default_rng(2024 + len(group))
+    cols = group[0][3]
+    raws = [synth.quant_tensor(rng, t, rows, cols) for _, t, rows, _ in group]
+    x = synth.activations(rng, cols)
+    mats = [device.QMat.from_ggml(r, t, rows, cols) for r, (_, t, rows, _) in zip(raws, group)]
+    xd = device.to_device_f32(x)
+    try:
+        fused = [o.cpu().numpy() for o in device.matvec_many(mats, xd)]
+        single = [m.matvec(xd).cpu().numpy() for m in mats]
+    finally:
+        for m in mats:
+            m.close()
+    for (name, t, rows, _), raw, f, s in zip(group, raws, fused, single):
+        np.testing.assert_array_equal(f.view(np.uint32), s.view(np.uint32), err_msg=name)
+        err = normwise_rel(f, quant.matvec_exact(raw, t, rows, cols, x))
+        assert err < 1e-5, f'{name}: {err}'
+
+
+@pytest.mark.parametrize('t', (12, 13))
+def test_deviation_from_avx2_is_the_int8_activation_error(golden, t):
+    """The reference's AVX2 Q4_K / Q5_K matvecs quantise x to int8 per 32
+    values (engine/native_quant.cpp:84-109, :183-278); the GPU keeps x exact.
+    Reported, not gated to the AVX2 output: on the reference test-suite case
+    (300 x 512, tests/test_dequant.py:202-216) the GPU differs from the
+    reference's own output by about 6e-3 (Q4_K) / 7e-3 (Q5_K) normwise, and
+    that difference is the activation-quantisation term: GPU - AVX2 equals
+    exact - (oracle model of the int8 activations) to within 1e-3 of its size."""
+    raw, x = golden[f'raw_{t}'].tobytes(), golden[f'x_{t}']
+    got = gpu_matvec(raw, t, 300, 512, x)
+    avx2 = golden[f'matvec_{t}']
+    exact = quant.matvec_exact(raw, t, 300, 512, x)
+    model = quant.q8_activation_matvec(raw, t, 300, 512, x)
+    dev = normwise_rel(got, avx2)
+    print(f'type {t}: GPU vs reference AVX2 normwise {dev:.3e}; GPU vs exact {normwise_rel(got, exact):.2e}')
+    assert 2e-3 < dev < 2e-2
+    assert normwise_rel(got - avx2, exact - model) < 1e-3
+
+
+def test_deviation_from_avx2_at_ffn_gate_size():
+    """Q4_K 14336 x 4096 (the single-matvec workload): the GPU against the
+    reference's own AVX2 kernel built from source (oracle/_ref), reported as
+    above. Skipped where the reference library or AVX2 is absent."""
+    from oracle import ref
+    from localai_amd import synth
+    if not ref.available():
+        pytest.skip('reference library not built')
+    if ' avx2 ' not in open('/proc/cpuinfo').read():
+        pytest.skip('host without AVX2')
+    rng = np.random.default_rng(11)
+    raw = synth.quant_tensor(rng, 12, 14336, 4096)
+    x = synth.activations(rng, 4096)
+    got = gpu_matvec(raw, 12, 14336, 4096, x)
+    avx2 = ref.matvec(raw, x, 14336, 4096, 12, threads=8)
+    exact = quant.matvec_exact(raw, 12, 14336, 4096, x)
+    model = quant.q8_activation_matvec(raw, 12, 14336, 4096, x)
+    dev = normwise_rel(got, avx2)
+    print(f'Q4_K 14336x4096: GPU vs reference AVX2 normwise {dev:.3e}; GPU vs exact {normwise_rel(got, exact):.2e}; '
+          f'AVX2 vs exact {normwise_rel(avx2, exact):.3e}')
+    assert dev < 2e-2
+    assert normwise_rel(got - avx2, exact - model) < 1e-3

@@ -248,3 +248,31 @@ def test_one_token_layer_repeated_and_graph_replayed():
         graph.replay()
         torch.cuda.synchronize()
         check(h, out.cpu().numpy(), idx.cpu().numpy(), gates.cpu().numpy())
+
+
+def test_fused_wait_that_runs_out_is_reported():
+    """The one-token fused expert kernel with its gate_up workgroups kept from
+    counting themselves done and a bound of four polls: every wait runs out,
+    every workgroup still exits, the output is NaN and the layer's check
+    raises (EHIP). With the defaults restored the same layer matches the
+    oracle again."""
+    from localai_amd import _lib, synth
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(61)
+    E, H, I, k = 8, 512, 256, 2
+    rw, gu, dn = make_layer(rng, E, H, I, 14)
+    h = synth.activations(rng, 1, H)
+    layer = MoELayer(rw, gu, dn, 14, E, H, I, k)
+    lib = _lib.load()
+    try:
+        assert lib.localai_hip_debug_fused_wait(4, 0) == 0
+        out, _, _ = layer.forward_device(layer.router_w.new_tensor(h))
+        with pytest.raises(_lib.HipError) as err:
+            layer.check(1)
+        assert err.value.status == 3
+        assert out.isnan().all()
+    finally:
+        lib.localai_hip_debug_fused_wait(0, 1)
+    (o, i, g), (ro, ri, rg) = run_both(rw, gu, dn, 14, E, H, I, k, h)
+    np.testing.assert_array_equal(i, ri)
+    assert normwise_rel(o, ro) < 1e-5

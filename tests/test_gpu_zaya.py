@@ -143,19 +143,24 @@ def test_router_probabilities_and_expert(base):
                 assert int(ex.cpu().item()) == w_e
 
 
+@pytest.mark.parametrize('xt', [14, 12])
 @pytest.mark.parametrize('forced', [E, 5])
-def test_skip_route_and_forced_expert(tmp_path, forced):
+def test_skip_route_and_forced_expert(tmp_path, forced, xt):
+    """Q6_K and Q4_K experts: the block must take the one-launch expert kernel
+    (the skip route instantiation included) and match the oracle."""
     from localai_amd.gguf import GGUFFile
-    rng = np.random.default_rng(30 + forced)
+    rng = np.random.default_rng(30 + forced + xt)
     bias = np.zeros(E + 1)
     bias[forced] = 10.0
-    raw = layer_tensors(rng, bias)
+    raw = layer_tensors(rng, bias, xt=xt)
     path = tmp_path / 'forced.gguf'
     write_layer(path, raw)
     t = oracle_tensors(raw)
     h = rng.standard_normal(H).astype(np.float32)
     with GGUFFile(path) as g:
-        moe, state = model_class()(g)._moe(1, h, None)
+        m = model_class()(g)
+        moe, state = m._moe(1, h, None)
+        assert m._zaya_cache().get(('experts1', 'blk.1.')) is not False
     w_moe, w_state, w_probs, w_e, _ = zm.moe_block(t, E, EPS, h, None)
     assert w_e == forced
     assert normwise_rel(state, w_state) < 1e-6
@@ -185,12 +190,23 @@ def test_matvec_path_for_q8_0_experts(tmp_path, forced):
     assert normwise_rel(moe, w_moe) < (1e-6 if forced == E else 1e-5)
 
 
-def test_experts1_two_slots_with_skip(base):
+@pytest.fixture(scope='module')
+def base_q4k(tmp_path_factory):
+    rng = np.random.default_rng(22)
+    raw = layer_tensors(rng, rng.uniform(0.0, 0.05, E + 1) * np.r_[np.ones(E), 0.0], xt=12)
+    path = tmp_path_factory.mktemp('zaya_q4k') / 'layer.gguf'
+    write_layer(path, raw)
+    return path, oracle_tensors(raw)
+
+
+@pytest.mark.parametrize('which', ['q6k', 'q4k'])
+def test_experts1_two_slots_with_skip(base, base_q4k, which):
     """localai_hip_moe_experts1 with top_k 2, one slot an expert and one the
-    skip route: out = w0 * expert(h) + w1 * h, against the oracle's products."""
+    skip route: out = w0 * expert(h) + w1 * h, against the oracle's products;
+    Q6_K and Q4_K experts."""
     from localai_amd import _lib, device
     from localai_amd.gguf import GGUFFile
-    path, t = base
+    path, t = base if which == 'q6k' else base_q4k
     rng = np.random.default_rng(9)
     tt = device.torch()
     lib = _lib.load()
@@ -212,3 +228,37 @@ def test_experts1_two_slots_with_skip(base):
             y = zm.mat(t['down'][e0], gate / (1.0 + np.exp(-np.clip(gate, -80, 80))) * up)
             want = np.float32(w[0]) * y + np.float32(w[1]) * h
             assert normwise_rel(out.cpu().numpy(), want) < 1e-5
+            _lib.check(lib.localai_hip_moe_error(p(ws), 1, E, None))
+
+
+def test_experts1_checks_indices_and_skip(base):
+    """A skip value inside [0, E) is an argument error at the call; an expert
+    index outside [0, E) that is not the skip route makes its rows NaN and is
+    reported by localai_hip_moe_error (EARG), while a valid call after it on
+    the same workspace reports nothing."""
+    from localai_amd import _lib, device
+    from localai_amd.gguf import GGUFFile
+    path, t = base
+    tt = device.torch()
+    lib = _lib.load()
+    p = device.ptr
+    with GGUFFile(path) as g:
+        gu = g.device_matrix('blk.1.ffn_gate_up_exps.weight')
+        dn = g.device_matrix('blk.1.ffn_down_exps.weight')
+        hd = device.to_device_f32(np.random.default_rng(3).standard_normal(H).astype(np.float32))
+        out = tt.empty(H, dtype=tt.float32, device=hd.device)
+        n = int(lib.localai_hip_moe_workspace_size(1, E, 2, H, I))
+        ws = tt.empty(n, dtype=tt.uint8, device=hd.device)
+        wt = tt.tensor([0.5, 0.5], dtype=tt.float32, device=hd.device)
+        idx = tt.tensor([2, E], dtype=tt.int32, device=hd.device)
+        assert lib.localai_hip_moe_experts1(p(hd), H, gu.handle, dn.handle, 2, p(idx), p(wt), 3, p(out),
+                                            p(ws), n, None) == 1
+        bad = tt.tensor([2, E + 3], dtype=tt.int32, device=hd.device)
+        _lib.check(lib.localai_hip_moe_experts1(p(hd), H, gu.handle, dn.handle, 2, p(bad), p(wt), -1, p(out),
+                                                p(ws), n, None))
+        assert lib.localai_hip_moe_error(p(ws), 1, E, None) == 1
+        assert tt.isnan(out).all()
+        _lib.check(lib.localai_hip_moe_experts1(p(hd), H, gu.handle, dn.handle, 2, p(idx), p(wt), E, p(out),
+                                                p(ws), n, None))
+        _lib.check(lib.localai_hip_moe_error(p(ws), 1, E, None))
+        assert tt.isfinite(out).all()

@@ -217,3 +217,29 @@ def test_matvec_exact_matches_bruteforce_scalar():
     w = quant.dequantize(raw, 14, (2, 256))
     brute = [sum(float(w[r, c]) * float(x[c]) for c in range(256)) for r in range(2)]
     np.testing.assert_allclose(quant.matvec_exact(raw, 14, 2, 256, x), brute, rtol=1e-12)
+
+
+def test_f16_widening_is_half_to_float_for_every_pattern():
+    """The oracle's '<f2' widening (engine/dequant.py:20-24) against an
+    integer restatement of half_to_float (engine/native_quant.cpp:12-33) on
+    all 65536 patterns: zeros, subnormals (renormalised), normals, infinities
+    and NaNs with their payloads (a signalling NaN stays signalling)."""
+    h = np.arange(65536, dtype=np.uint32)
+    sign = (h & 0x8000) << 16
+    exp = (h >> 10) & 0x1F
+    mant = h & 0x3FF
+    want = np.empty(65536, dtype=np.uint32)
+    normal = (exp > 0) & (exp < 31)
+    want[normal] = sign[normal] | ((exp[normal] + 112) << 23) | (mant[normal] << 13)
+    special = exp == 31
+    want[special] = sign[special] | 0x7F800000 | (mant[special] << 13)
+    zero = (exp == 0) & (mant == 0)
+    want[zero] = sign[zero]
+    for i in np.nonzero((exp == 0) & (mant != 0))[0]:     # subnormal: shift until the hidden bit appears
+        m, e = int(mant[i]), -14
+        while not m & 0x400:
+            m <<= 1
+            e -= 1
+        want[i] = int(sign[i]) | ((e + 127) << 23) | ((m & 0x3FF) << 13)
+    got = quant.dequantize(h.astype(np.uint16).tobytes(), 1, (65536,)).view(np.uint32)
+    np.testing.assert_array_equal(got, want)

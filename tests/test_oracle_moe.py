@@ -85,3 +85,82 @@ def test_expert_slices_follow_zaya_byte_offsets():
     for e in range(3):
         np.testing.assert_array_equal(moe.expert_matrix(raw, 12, e, 64, 256),
                                       quant.dequantize(raw[e * per:(e + 1) * per], 12, (64, 256)))
+
+
+def _dense_swiglu(gu_raw, dn_raw, t, H, I, x):
+    """One expert's FFN from pieces pinned elsewhere: quant.matvec_exact (pinned
+    against the reference library) and SiLU as x * expit(x) (SciPy's logistic
+    function, engine/zaya.py:305 without the clip, which changes nothing
+    below |x| = 80)."""
+    from scipy.special import expit
+    v = quant.matvec_exact(gu_raw, t, 2 * I, H, x)
+    a = v[:I] * expit(v[:I]) * v[I:]
+    return quant.matvec_exact(dn_raw, t, H, I, a)
+
+
+def test_identical_experts_give_the_dense_ffn_for_any_k():
+    """All experts byte-identical: the gates sum to one, so for every k the
+    layer is the dense SwiGLU FFN whatever the gates are. A dropped gate
+    factor (k x dense) or one applied twice (sum g^2 x dense) fails."""
+    from localai_amd import synth
+    rng = np.random.default_rng(6)
+    H, I, E = 256, 512, 6
+    gu1 = synth.quant_tensor(rng, 12, 2 * I, H)
+    dn1 = synth.quant_tensor(rng, 12, H, I)
+    h = rng.standard_normal((4, H)).astype(np.float32)
+    rw = rng.standard_normal((E, H)).astype(np.float32) * 0.1
+    dense = np.stack([_dense_swiglu(gu1, dn1, 12, H, I, h[t]) for t in range(4)])
+    for k in (1, 2, 3, 6):
+        out, idx, g, _ = moe.moe_forward(h, rw, gu1 * E, dn1 * E, 12, E, k, I)
+        if k > 1:
+            assert g.min() < 0.9 / k < 1.1 / k < g.max()      # gates far from uniform
+        np.testing.assert_allclose(out, dense, rtol=1e-10, atol=1e-12 * np.abs(dense).max())
+
+
+def test_doubling_one_experts_down_weights_doubles_only_its_gated_term():
+    """Q6_K weights are linear in d (w = d * sc * q), so adding one to the
+    exponent of every d of expert e's down slice doubles that expert's
+    output exactly. The layer output must then grow by gate[t, slot(e)] * y_e
+    for the tokens routed to e (y_e from a one-expert layer on e's bytes,
+    whose gate is 1), and stay the same for every other token."""
+    from localai_amd import synth
+    rng = np.random.default_rng(7)
+    H, I, E, k, T = 256, 256, 5, 2, 12
+    gu = synth.quant_tensor(rng, 14, 2 * I, H, batch=E)
+    dn = synth.quant_tensor(rng, 14, H, I, batch=E)
+    h = rng.standard_normal((T, H)).astype(np.float32)
+    rw = rng.standard_normal((E, H)).astype(np.float32) * 0.2
+    out, idx, g, _ = moe.moe_forward(h, rw, gu, dn, 14, E, k, I)
+    e = int(np.bincount(idx.reshape(-1), minlength=E).argmax())
+    per_gu, per_dn = moe.expert_bytes(14, 2 * I, H), moe.expert_bytes(14, H, I)
+    blocks = np.frombuffer(dn, np.uint8).reshape(-1, 210).copy()
+    nb = per_dn // 210
+    d = blocks[e * nb:(e + 1) * nb, 208:210].copy().view(np.uint16)
+    assert np.all(((d >> 10) & 31) > 0) and np.all(((d >> 10) & 31) < 30)   # normal, room to double
+    blocks[e * nb:(e + 1) * nb, 208:210] = (d + np.uint16(0x400)).view(np.uint8)
+    out2, idx2, g2, _ = moe.moe_forward(h, rw, gu, blocks.tobytes(), 14, E, k, I)
+    np.testing.assert_array_equal(idx2, idx)
+    y_e, _, g1, _ = moe.moe_forward(h, np.zeros((1, H), np.float32), gu[e * per_gu:(e + 1) * per_gu],
+                                    dn[e * per_dn:(e + 1) * per_dn], 14, 1, 1, I)
+    assert np.all(g1 == 1.0)
+    routed = 0
+    for t in range(T):
+        slots = np.nonzero(idx[t] == e)[0]
+        want = g[t, slots[0]] * y_e[t] if slots.size else np.zeros(H)
+        routed += slots.size
+        np.testing.assert_allclose(out2[t] - out[t], want, rtol=1e-9, atol=1e-12 * np.abs(out).max())
+    assert 0 < routed < T
+
+
+def test_silu_matches_the_logistic_function_and_its_limits():
+    """engine/zaya.py:305: g / (1 + exp(-clip(g, -80, 80))) against g * expit(g)
+    and its limits: silu(0) = 0, silu(g) -> g for large g, -> 0 for very
+    negative g, silu(-g) = silu(g) - g."""
+    from scipy.special import expit
+    g = np.concatenate([np.linspace(-90, 90, 3601), [-1e4, -80.5, 80.5, 1e4, 0.0]])
+    s = moe.silu(g)
+    np.testing.assert_allclose(s, g * expit(g), rtol=1e-13, atol=1e-30)
+    assert moe.silu(np.array([0.0]))[0] == 0.0
+    np.testing.assert_allclose(moe.silu(np.array([40.0, 1e4])), [40.0, 1e4], rtol=1e-15)
+    assert abs(moe.silu(np.array([-1e4]))[0]) < 1e-30
+    np.testing.assert_allclose(moe.silu(-g[:3601]), moe.silu(g[:3601]) - g[:3601], rtol=1e-12, atol=1e-12)
