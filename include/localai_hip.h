@@ -207,6 +207,26 @@ int localai_hip_moe_experts1(const float *h_dev, int64_t hidden, const localai_q
                              const float *weight_dev, int32_t skip, float *out_dev, void *workspace_dev,
                              int64_t workspace_bytes, void *stream);
 
+/* Bytes of the library's static device workspace (one per device, held
+ * until the process ends) used by localai_hip_moe_forward_static. */
+int64_t localai_hip_static_workspace_bytes(void);
+
+/* localai_hip_moe_forward with the workspace taken from a static device array
+ * inside the library (localai_hip_static_workspace_bytes() = 64 MiB per
+ * device) instead of a caller buffer: it allocates nothing (no hipMalloc, no
+ * hipFree), so callers that cannot allocate -- code under HIP graph capture,
+ * serving loops that forbid allocation -- can run the MoE layer. Same
+ * arguments, limits and results as localai_hip_moe_forward; sizes whose
+ * workspace (localai_hip_moe_workspace_size) exceeds the static one are
+ * LOCALAI_EARG. All calls on one device share its array: calls that overlap
+ * in time on one device race, and the router logits the workspace holds
+ * after a call are overwritten by the next. No counterpart in the reference. */
+int localai_hip_moe_forward_static(const float *h_dev, int64_t tokens, int64_t hidden,
+                                   const float *router_w_dev, const float *router_b_dev,
+                                   int64_t experts, int top_k, const localai_qmat *gate_up,
+                                   const localai_qmat *down, float *out_dev, int32_t *topk_idx_dev,
+                                   float *topk_w_dev, void *stream);
+
 /* Status of the last one-token fused expert launch that used this workspace
  * (localai_hip_moe_experts1, or localai_hip_moe_forward with one token and
  * top_k <= 2), which hands gate_up results to its down workgroups inside one

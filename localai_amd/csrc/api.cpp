@@ -93,7 +93,8 @@ int localai_hip_init(int device) {
         g_device = device;
     }
     LQ_HIP(hipSetDevice(device));
-    return LOCALAI_OK;
+    // device address of the static workspace (localai_hip_moe_forward_static)
+    return static_ws_setup();
 }
 
 int localai_hip_block_layout(int t, int *vpb, int *bpb) {

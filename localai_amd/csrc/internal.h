@@ -30,6 +30,7 @@ void set_legacy_status(int status);
     } while (0)
 
 int ensure_device();   // make the library's device current for this thread
+int static_ws_setup(); // look up the current device's static workspace (static_ws.hip)
 size_t max_lds_per_block();   // LDS bytes a workgroup may use on the current device
 
 // launchers (return LOCALAI_* status)

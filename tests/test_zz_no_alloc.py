@@ -1,0 +1,84 @@
+"""localai_hip_moe_forward_static -- the MoE layer with the library's static
+device workspace (allocates nothing) -- against localai_hip_moe_forward with
+a caller workspace, through the C ABI: the same kernels on the same inputs,
+so routing, gates and outputs must be identical bit for bit, on two calls in
+a row of which the second has fewer tokens (the static array keeps the first
+call's contents). Sizes whose workspace exceeds the static one are EARG."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import moe as omoe
+from tests.conftest import normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(seed, E, H, I, k, t):
+    from localai_amd import synth
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(seed)
+    rw = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    gu = synth.quant_tensor(rng, t, 2 * I, H, batch=E)
+    dn = synth.quant_tensor(rng, t, H, I, batch=E)
+    return MoELayer(rw, gu, dn, t, E, H, I, k), (rw, gu, dn), rng
+
+
+def _static(layer, hd):
+    from localai_amd import _lib, device
+    tt = device.torch()
+    T = hd.shape[0]
+    out = tt.empty((T, layer.H), dtype=tt.float32, device=hd.device)
+    idx = tt.empty((T, layer.k), dtype=tt.int32, device=hd.device)
+    gates = tt.empty((T, layer.k), dtype=tt.float32, device=hd.device)
+    p = device.ptr
+    st = _lib.load().localai_hip_moe_forward_static(
+        p(hd), T, layer.H, p(layer.router_w), None, layer.E, layer.k, layer.gate_up.handle, layer.down.handle,
+        p(out), p(idx), p(gates), ctypes.c_void_p(device.stream_ptr()))
+    _lib.check(st)
+    return out, idx, gates
+
+
+@pytest.mark.parametrize('case', ['zaya_decode', 'qwen3_prefill'])
+def test_static_workspace_matches_caller_workspace(case):
+    from localai_amd import device, synth
+    if case == 'zaya_decode':   # hidden 2048, 16 Q6_K experts, top-2, intermediate 4096: 8 tokens, then 1
+        layer, (rw, gu, dn), rng = _layer(71, 16, 2048, 4096, 2, 14)
+        sizes = (8, 1)
+    else:                       # 64 Q4_K experts, top-8, intermediate 768: 96 tokens (GEMM path), then 8
+        layer, (rw, gu, dn), rng = _layer(72, 64, 2048, 768, 8, 12)
+        sizes = (96, 8)
+    for T in sizes:
+        h = synth.activations(rng, T, layer.H)
+        hd = device.to_device_f32(h)
+        so, si, sg = (a.cpu().numpy() for a in _static(layer, hd))
+        wo, wi, wg = (a.cpu().numpy() for a in layer.forward_device(hd))
+        np.testing.assert_array_equal(si, wi)
+        np.testing.assert_array_equal(sg.view(np.uint32), wg.view(np.uint32))
+        np.testing.assert_array_equal(so.view(np.uint32), wo.view(np.uint32))
+        if T <= 8:
+            ref, ridx, _, _ = omoe.moe_forward(h, rw, gu, dn, 14 if case == 'zaya_decode' else 12, layer.E,
+                                               layer.k, layer.I)
+            np.testing.assert_array_equal(si, ridx)
+            assert normwise_rel(so, ref) < 1e-5
+
+
+def test_static_workspace_size_limit():
+    from localai_amd import _lib, device
+    lib = _lib.load()
+    cap = int(lib.localai_hip_static_workspace_bytes())
+    assert cap == 64 << 20
+    layer, _, _ = _layer(73, 128, 2048, 768, 8, 12)
+    T = 4096
+    assert int(lib.localai_hip_moe_workspace_size(T, 128, 8, 2048, 768)) > cap
+    tt = device.torch()
+    hd = tt.zeros((T, 2048), dtype=tt.float32, device=device.device())
+    out = tt.empty((T, 2048), dtype=tt.float32, device=hd.device)
+    idx = tt.empty((T, 8), dtype=tt.int32, device=hd.device)
+    gates = tt.empty((T, 8), dtype=tt.float32, device=hd.device)
+    p = device.ptr
+    st = lib.localai_hip_moe_forward_static(p(hd), T, 2048, p(layer.router_w), None, 128, 8, layer.gate_up.handle,
+                                            layer.down.handle, p(out), p(idx), p(gates), None)
+    assert st == 1
+    assert b'static' in lib.localai_hip_last_error()
