@@ -127,6 +127,44 @@ int localai_hip_matmul(const localai_qmat *m, int64_t expert, const float *x_dev
                        float *y_dev, int y_layout, void *workspace_dev, int64_t workspace_bytes,
                        void *stream);
 
+/* ---- decode layer: the matvec chain in one launch ----------------------- */
+
+/* Bytes of workspace localai_hip_layer_chain needs. The workspace must be
+ * zero-filled before its first use; every launch leaves it so. */
+int64_t localai_hip_layer_workspace_size(int64_t dim, int64_t ffn);
+
+/* The matvecs of one decode layer with the glue between them, from the
+ * attention output of layer L to the attention inputs of layer L+1
+ * (engine/model.py:229-233 of layer L, then :182-185 and :203-213 of L+1):
+ *   x1 = pre + W_o att
+ *   act = silu(W_gate u) * (W_up u),   u = norm(x1) * w_ffn
+ *   x_out = x1 + W_down act
+ *   q, k, v = W_q v', W_k v', W_v v',   v' = norm(x_out) * w_attn
+ * norm(x) = x / sqrt(mean(x^2) + eps) (engine/model.py:82, the mean in fp64);
+ * silu as engine/model.py:232. With rope_cos / rope_sin ([rope_half] each,
+ * cos / sin of position * inv_freq as the caller computes them,
+ * engine/model.py:190-203) q and k get Llama's adjacent-pair RoPE in every
+ * head of head_dim values (:205-210); NULL for none.
+ * mats: the seven handles in the order attn_output, ffn_gate, ffn_up,
+ * ffn_down, attn_q, attn_k, attn_v of layer L+1 (w_attn is its attn_norm),
+ * each a Q4_K or Q6_K matrix with the tile form; dim and ffn multiples of
+ * 256. One launch: the stages' workgroups run in stage order and each waits
+ * on device for the stage before it, after requesting its own weights.
+ * Matvec results are those of localai_hip_matvec on the same inputs.
+ * ETYPE for shapes or types without a kernel (the caller then runs the
+ * separate matvecs). Calls on one workspace must not overlap. */
+int localai_hip_layer_chain(const localai_qmat *const *mats, const float *pre_dev, const float *att_dev,
+                            const float *w_ffn_dev, const float *w_attn_dev, float eps,
+                            const float *rope_cos_dev, const float *rope_sin_dev, int head_dim,
+                            int rope_half, float *x_out_dev, float *q_dev, float *k_dev, float *v_dev,
+                            void *workspace_dev, int64_t workspace_bytes, void *stream);
+
+/* Waits for `stream`, then reports whether a wait between the stages of the
+ * last localai_hip_layer_chain launches on this workspace ran out
+ * (LOCALAI_EHIP; the affected outputs are NaN) and clears the report. No
+ * counterpart in the reference. */
+int localai_hip_layer_error(void *workspace_dev, void *stream);
+
 /* ---- ZAYA router (engine/zaya.py:274-307) -------------------------------- */
 
 /* Everything of ZAYA's router after the first projection r0 = W_inp h

@@ -355,7 +355,58 @@ int localai_hip_moe_error(const void *ws, int64_t T, int64_t E, void *stream) {
 
 int localai_hip_debug_fused_wait(int spin_limit, int producers_count) {
     clear_error();
+    set_layer_wait(spin_limit, producers_count);
     return set_fused_wait(spin_limit, producers_count);
+}
+
+int64_t localai_hip_layer_workspace_size(int64_t dim, int64_t ffn) {
+    if (dim < 1 || ffn < 1) return -1;
+    return (int64_t)layer_workspace_bytes(dim, ffn);
+}
+
+int localai_hip_layer_chain(const localai_qmat *const *mats, const float *pre, const float *att,
+                            const float *w_ffn, const float *w_attn, float eps, const float *rope_cos,
+                            const float *rope_sin, int head_dim, int rope_half, float *x_out, float *q_out,
+                            float *k_out, float *v_out, void *ws, int64_t ws_bytes, void *stream) {
+    clear_error();
+    if (!mats || !pre || !att || !w_ffn || !w_attn || !x_out || !q_out || !k_out || !v_out || !ws)
+        return fail(LOCALAI_EARG, "layer chain: null pointer");
+    for (int i = 0; i < 7; ++i) {
+        const localai_qmat *m = mats[i];
+        if (!m) return fail(LOCALAI_EARG, "layer chain: null matrix handle");
+        if (m->g.batch != 1) return fail(LOCALAI_EARG, "layer chain: matrices must be plain 2-D tensors");
+        if ((m->g.type != LQ_Q4_K && m->g.type != LQ_Q6_K) || !m->tiles)
+            return fail(LOCALAI_ETYPE, "layer chain: Q4_K / Q6_K matrices with the tile form only");
+    }
+    const int64_t dim = mats[0]->g.rows, ffn = mats[1]->g.rows;
+    if (mats[0]->g.cols != dim) return fail(LOCALAI_EARG, "layer chain: attn_output must be [dim, dim]");
+    if (dim % 256 || ffn % 256) return fail(LOCALAI_ETYPE, "layer chain: dim and ffn must be multiples of 256");
+    if (mats[1]->g.cols != dim || mats[2]->g.rows != ffn || mats[2]->g.cols != dim ||
+        mats[2]->g.type != mats[1]->g.type)
+        return fail(LOCALAI_EARG, "layer chain: ffn_gate and ffn_up must be [ffn, dim] of one type");
+    if (mats[3]->g.rows != dim || mats[3]->g.cols != ffn) return fail(LOCALAI_EARG, "layer chain: ffn_down must be [dim, ffn]");
+    for (int i = 4; i < 7; ++i)
+        if (mats[i]->g.cols != dim) return fail(LOCALAI_EARG, "layer chain: attn_q / attn_k / attn_v must have dim columns");
+    if ((rope_cos == nullptr) != (rope_sin == nullptr)) return fail(LOCALAI_EARG, "layer chain: rope_cos and rope_sin go together");
+    if (rope_cos && (head_dim < 2 || head_dim % 2 || rope_half < 0 || 2 * rope_half > head_dim))
+        return fail(LOCALAI_EARG, "layer chain: RoPE needs an even head_dim and rope_half <= head_dim / 2");
+    if (ws_bytes < (int64_t)layer_workspace_bytes(dim, ffn)) return fail(LOCALAI_EARG, "layer chain: workspace too small");
+    auto mis = [](const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & m) != 0; };
+    if (mis(pre, 15) || mis(att, 15) || mis(x_out, 15) || mis(ws, 255))
+        return fail(LOCALAI_EARG, "layer chain: pre, att and x_out 16-byte, workspace 256-byte aligned");
+    if (int st = ensure_device()) return st;
+    return launch_layer_chain(mats, pre, att, w_ffn, w_attn, eps, rope_cos, rope_sin, head_dim, rope_half, x_out,
+                              q_out, k_out, v_out, ws, (hipStream_t)stream);
+}
+
+int localai_hip_layer_error(void *ws, void *stream) {
+    clear_error();
+    if (!ws) return fail(LOCALAI_EARG, "layer error: null workspace");
+    if (int st = ensure_device()) return st;
+    uint32_t word = 0;
+    if (int st = layer_error_word(ws, (hipStream_t)stream, &word)) return st;
+    if (word) return fail(LOCALAI_EHIP, "layer chain: a wait between stages ran out (outputs are NaN)");
+    return LOCALAI_OK;
 }
 
 int64_t localai_hip_moe_workspace_size(int64_t T, int64_t E, int k, int64_t H, int64_t I) {

@@ -121,8 +121,12 @@ int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_
     return LOCALAI_OK;
 }
 
-// RT row tiles of one matrix, workgroup index blk within the matrix
-template <int TYPE, int SPW, int RT>
+// RT row tiles of one matrix, workgroup index blk within the matrix.
+// PIPE: the wave's super-blocks stream through two register sets
+// (mt_pass_pipe) instead of being requested all at once (long rows, where a
+// wave holds several blocks and their dot products would otherwise all wait
+// for the last load).
+template <int TYPE, int SPW, int RT, bool PIPE = false>
 __device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
                                                 int64_t tiles, const float *__restrict__ x,
                                                 float *__restrict__ y, int64_t blk) {
@@ -130,15 +134,25 @@ __device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, 
     const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
     float4 xv[1][SPW];
     mt_load_x<SPW>(xv[0], x, nb, sb0, lane);   // x first: it is consumed first
-    MtW<TYPE> w[RT][SPW];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        const int64_t tile = blk * RT + t < tiles ? blk * RT + t : tiles - 1;
-        mt_load_tile<TYPE, SPW>(w[t], Wt + tile * nb * mt_block_bytes(TYPE), nb, sb0, nsb, lane);
-    }
-    __builtin_amdgcn_sched_barrier(0);
     float *fin;
-    mt_pass<TYPE, SPW, RT, 1>(w, xv, nsb, smem, fin);
+    if constexpr (PIPE) {
+        const uint8_t *tile[RT];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const int64_t tl = blk * RT + t < tiles ? blk * RT + t : tiles - 1;
+            tile[t] = Wt + tl * nb * mt_block_bytes(TYPE);
+        }
+        mt_pass_pipe<TYPE, SPW, RT>(tile, nb, sb0, nsb, xv[0], smem, fin);
+    } else {
+        MtW<TYPE> w[RT][SPW];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const int64_t tile = blk * RT + t < tiles ? blk * RT + t : tiles - 1;
+            mt_load_tile<TYPE, SPW>(w[t], Wt + tile * nb * mt_block_bytes(TYPE), nb, sb0, nsb, lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mt_pass<TYPE, SPW, RT, 1>(w, xv, nsb, smem, fin);
+    }
     const int i = threadIdx.x;
     if (i < RT * 16) {
         const int64_t tile = blk * RT + (i >> 4), row = tile * MT_ROWS + (i & 15);
@@ -148,12 +162,12 @@ __device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, 
 
 // Q4_K workgroups of 1024 threads are held to 64 VGPRs (8 waves per SIMD) so
 // that two fit on a CU; the Q6_K body needs more registers than that
-template <int TYPE, int SPW, int RT, int MAXT>
+template <int TYPE, int SPW, int RT, int MAXT, bool PIPE = false>
 __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(MAXT == 1024 && TYPE == LQ_Q4_K ? 8 : 1)))
 void gemv_mfma(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
                                                   int64_t tiles, const float *__restrict__ x,
                                                   float *__restrict__ y) {
-    mt_matvec_block<TYPE, SPW, RT>(Wt, rows, nb, tiles, x, y, blockIdx.x);
+    mt_matvec_block<TYPE, SPW, RT, PIPE>(Wt, rows, nb, tiles, x, y, blockIdx.x);
 }
 
 // Several matrices with the same K and the same x in one launch: job j owns
@@ -167,7 +181,7 @@ struct MtJobs {
     int n;
 };
 // Q6 = false: Q4_K jobs only (no Q6_K body compiled in, 64 VGPRs at 1024 threads)
-template <int SPW, int RT, int MAXT, bool Q6>
+template <int SPW, int RT, int MAXT, bool Q6, bool PIPE = false>
 __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(MAXT == 1024 && !Q6 ? 8 : 1)))
 void gemv_mfma_many(MtJobs jobs, int nb, const float *__restrict__ x) {
     const int64_t b = blockIdx.x;
@@ -177,9 +191,9 @@ void gemv_mfma_many(MtJobs jobs, int nb, const float *__restrict__ x) {
         if (i < jobs.n && b >= jobs.blk0[i]) j = i;
     const int64_t tiles = (jobs.rows[j] + MT_ROWS - 1) / MT_ROWS;
     if (Q6 && jobs.type[j] == LQ_Q6_K)
-        mt_matvec_block<LQ_Q6_K, SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
+        mt_matvec_block<LQ_Q6_K, SPW, RT, PIPE>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
     else
-        mt_matvec_block<LQ_Q4_K, SPW, RT>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
+        mt_matvec_block<LQ_Q4_K, SPW, RT, PIPE>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
 }
 
 // Launch plan: the waves of a workgroup split the super-blocks of one row
@@ -188,28 +202,40 @@ void gemv_mfma_many(MtJobs jobs, int nb, const float *__restrict__ x) {
 //             per workgroup when SPW = 1 (x staged once for both)
 //   nb <= 32, fewer tiles:  SPW = ceil(nb / 8), up to 8 waves, one tile per
 //             workgroup, so that small matrices still spread over the CUs
-//   nb > 32:  SPW = ceil(nb / 12), up to 12 waves (768 threads, so each wave
-//             may hold all of its SPW blocks in registers)
+//   nb > 32:  SPW = ceil(nb / 8) (5..9), 8 waves, the wave's blocks
+//             streamed through two register sets (mt_pass_pipe): Q6_K
+//             4096 x 14336 took 12.1 us with all of a wave's blocks requested
+//             at once (12 waves x 5) and 11.5 us this way
 struct MtPlan {
     int spw, waves, rt;
+    bool pipe;
 };
 static MtPlan mt_plan(int nb, int64_t tiles, bool q6) {
     MtPlan p;
     const bool big = tiles >= 768;
-    p.spw = nb > 32 ? (nb + 11) / 12 : big ? (nb + 15) / 16 : (nb + 7) / 8;
+    p.pipe = nb > 32;
+    p.spw = nb > 32 ? (nb + 7) / 8 : big ? (nb + 15) / 16 : (nb + 7) / 8;
     p.waves = (nb + p.spw - 1) / p.spw;
     p.rt = (big && p.spw == 1 && !q6) ? 2 : 1;   // two Q6_K tiles need more registers
     return p;
 }
 
 #define MT_DISPATCH(L)                                         \
-    switch (p.spw) {                                           \
-        case 1: if (p.rt == 2) L(1, 2, 1024); else L(1, 1, 1024); break; \
-        case 2: L(2, 1, 1024); break;                          \
-        case 3: L(3, 1, 768); break;                           \
-        case 4: L(4, 1, 768); break;                           \
-        case 5: L(5, 1, 768); break;                           \
-        default: L(6, 1, 768); break;                          \
+    if (p.pipe) {                                              \
+        switch (p.spw) {                                       \
+            case 5: L(5, 1, 512, true); break;                 \
+            case 6: L(6, 1, 512, true); break;                 \
+            case 7: L(7, 1, 512, true); break;                 \
+            case 8: L(8, 1, 512, true); break;                 \
+            default: L(9, 1, 512, true); break;                \
+        }                                                      \
+    } else {                                                   \
+        switch (p.spw) {                                       \
+            case 1: if (p.rt == 2) L(1, 2, 1024, false); else L(1, 1, 1024, false); break; \
+            case 2: L(2, 1, 1024, false); break;               \
+            case 3: L(3, 1, 768, false); break;                \
+            default: L(4, 1, 768, false); break;               \
+        }                                                      \
     }
 
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s) {
@@ -222,10 +248,10 @@ int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, floa
     const MtPlan p = mt_plan(nb, tiles, q6);
     dim3 grid((unsigned)((tiles + p.rt - 1) / p.rt)), block(64 * p.waves);
     const size_t lds = mt_lds_bytes(g.type, p.waves, p.spw, 1, p.rt);
-#define MT_L(S, R, M)                                                                                           \
+#define MT_L(S, R, M, P)                                                                                        \
     do {                                                                                                        \
-        if (q6) hipLaunchKernelGGL((gemv_mfma<LQ_Q6_K, S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y); \
-        else hipLaunchKernelGGL((gemv_mfma<LQ_Q4_K, S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y);    \
+        if (q6) hipLaunchKernelGGL((gemv_mfma<LQ_Q6_K, S, R, M, P>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y); \
+        else hipLaunchKernelGGL((gemv_mfma<LQ_Q4_K, S, R, M, P>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y);    \
     } while (0)
     MT_DISPATCH(MT_L)
 #undef MT_L
@@ -262,10 +288,10 @@ int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const
     for (int j = n; j <= MT_MAX_JOBS; ++j) jobs.blk0[j] = b;
     dim3 grid((unsigned)b), block(64 * p.waves);
     const size_t lds = mt_lds_bytes(any_q6 ? LQ_Q6_K : LQ_Q4_K, p.waves, p.spw, 1, p.rt);
-#define MT_L(S, R, M)                                                                           \
+#define MT_L(S, R, M, P)                                                                        \
     do {                                                                                        \
-        if (any_q6) hipLaunchKernelGGL((gemv_mfma_many<S, R, M, true>), grid, block, lds, s, jobs, nb, x);  \
-        else hipLaunchKernelGGL((gemv_mfma_many<S, R, M, false>), grid, block, lds, s, jobs, nb, x);        \
+        if (any_q6) hipLaunchKernelGGL((gemv_mfma_many<S, R, M, true, P>), grid, block, lds, s, jobs, nb, x);  \
+        else hipLaunchKernelGGL((gemv_mfma_many<S, R, M, false, P>), grid, block, lds, s, jobs, nb, x);        \
     } while (0)
     MT_DISPATCH(MT_L)
 #undef MT_L

@@ -86,6 +86,14 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
 // the stream has finished); test controls of its waits
 int moe_error_word(const void *ws, int64_t T, int64_t E, hipStream_t s, uint32_t *word);
 int set_fused_wait(int spin, int count);
+// decode-layer matvec chain (layer.hip); m: o, gate, up, down, q, k, v
+size_t layer_workspace_bytes(int64_t dim, int64_t ffn);
+int launch_layer_chain(const localai_qmat *const *m, const float *pre, const float *att, const float *w_ffn,
+                       const float *w_attn, float eps, const float *rope_cos, const float *rope_sin, int head_dim,
+                       int rope_half, float *x_out, float *q_out, float *k_out, float *v_out, void *ws,
+                       hipStream_t s);
+int layer_error_word(void *ws, hipStream_t s, uint32_t *word);
+int set_layer_wait(int spin, int count);
 int launch_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, const localai_qmat *dn, int k,
                         const int32_t *topk_idx, const float *topk_w, int skip, float *out, void *ws,
                         hipStream_t s);

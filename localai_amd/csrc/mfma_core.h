@@ -413,4 +413,64 @@ __device__ __forceinline__ void mt_pass(const MtW<TYPE> (&w)[RT][SPW], const flo
     __syncthreads();
 }
 
+// Software-pipelined form of the per-wave work of mt_pass for one x: the
+// wave's super-blocks of RT tiles stream through two register sets, so the
+// dot products of block k run while blocks k + 1 and k + 2 are in flight and
+// a wave never holds more than two blocks of weights. tile[t]: block 0 of
+// tile t; the caller has loaded xv (its x loads go out before the weights).
+// Same arithmetic and summation order as mt_pass (identical results).
+template <int TYPE, int SPW, int RT>
+__device__ __forceinline__ void mt_pass_pipe(const uint8_t *const (&tile)[RT], int nb, int sb0, int nsb,
+                                             const float4 (&xv)[SPW], uint8_t *smem, float *&fin) {
+    constexpr int XB = mt_xbytes(TYPE);
+    const int lane = lane_id(), wv = wave_id(), nw = blockDim.x >> 6;
+    uint8_t *wl = smem + wv * SPW * XB;
+    float *red = reinterpret_cast<float *>(smem + nw * SPW * XB);   // [nw][RT][64]
+    fin = red + nw * RT * 64;
+    MtW<TYPE> w[2][RT];
+    auto load = [&](MtW<TYPE>(&dst)[RT], int k) {
+        const int kk = k < nsb ? k : 0;
+        const int sb = sb0 + kk < nb ? sb0 + kk : nb - 1;
+#pragma unroll
+        for (int t = 0; t < RT; ++t) dst[t] = mt_load_w<TYPE>(tile[t] + (int64_t)sb * mt_block_bytes(TYPE), lane);
+    };
+    load(w[0], 0);
+    if (SPW > 1) load(w[1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) mt_stage<TYPE>(xv[k], wl + k * XB, lane);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const MtLane<TYPE> L = mt_lane<TYPE>(lane);
+    float acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+        if (k < nsb) {
+            const MtA<TYPE> a = mt_load_a<TYPE>(wl + k * XB, L);
+#pragma unroll
+            for (int t = 0; t < RT; ++t) acc[t] = mt_dot<TYPE>(w[k & 1][t], a, L, acc[t]);
+        }
+        if (k + 2 < SPW) {
+            __builtin_amdgcn_sched_barrier(0);
+            load(w[k & 1], k + 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) red[(wv * RT + t) * 64 + lane] = acc[t];
+    __syncthreads();
+    const int i = threadIdx.x;
+    if (i < RT * 16) {
+        const int t = i >> 4, n = i & 15;
+        float s = 0.0f;
+        for (int kk = 0; kk < nw; ++kk) {
+            const float *r = red + (kk * RT + t) * 64 + n;
+            s += (r[0] + r[16]) + (r[32] + r[48]);
+        }
+        fin[i] = s;
+    }
+    __syncthreads();
+}
+
 }  // namespace lq
