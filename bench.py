@@ -1,10 +1,14 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized-matmul / MoE path on one MI355X.
 
+With no --workload the run prints ONE JSON line: the headline workload
+(llama3_8b_decode_layer) at top level, and every other workload below under
+"workloads". With --workload NAME only that workload is measured.
+
 Workloads (one "step" = one pass of the path over one batch of synthetic
 input, weights already resident in HBM, seeded data from localai_amd/synth.py):
 
-  llama3_8b_decode_layer (default)  the seven decode matvecs of one
+  llama3_8b_decode_layer (headline)  the seven decode matvecs of one
       Llama-3-8B layer at batch 1, Q4_K_M mix (q/k/o/gate/up Q4_K, v/down
       Q6_K). value = algorithmic bytes / time (GB/s). q/k/v and gate/up,
       which read the same vector, are each one fused launch
@@ -16,6 +20,13 @@ input, weights already resident in HBM, seeded data from localai_amd/synth.py):
       intermediate 4096, Q6_K experts, T = 1 (T = 8 reported alongside).
   qwen3_moe_prefill Qwen3-MoE-style prefill: hidden 2048, 128 experts, top-8,
       intermediate 768, Q4_K experts, 512 tokens, Zipf(1.1) logit bias.
+  llama3_8b_layer_chain  the same seven matvecs as one launch with the glue
+      of the decode step between them (residual adds, both RMSNorms, SiLU*up,
+      localai_hip_layer_chain).
+  hbm_read_floor    the streaming-read kernel (localai_hip_stream_read) over
+      the same byte counts: one 33 MB launch, the layer's four dependent
+      launches, and the whole layer's 139 MB as one launch -- what a launch
+      of that size can stream at best on this GPU.
   hbm_copy          a plain 256 MiB device-to-device copy: the calibration
       kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE (known bytes per launch).
 
@@ -25,9 +36,13 @@ streams its weights from HBM; one HIP graph holds a whole rotation of steps
 stream and timed with HIP events on that stream, exactly K steps.
 `step_stats` gives the median and p90 per-step time over at least 100 more
 steps replayed after the timed region. `roofline` is the dominant kernel of
-the workload timed alone the same way; `cpu_baseline` is the reference's own
+the workload timed alone the same way (or the whole layer where it is a
+composition of kernels); `cpu_baseline` is the reference's own
 engine/native_quant.cpp kernels (built from source into oracle/_ref) on a
-bounded sample, on the host cores.
+bounded sample, on the host cores, pinned (sched_setaffinity) to one logical
+CPU per physical core, at the reference's thread policy and on all cores
+(the reference's pool caps at 8 threads), with the NumPy dequantize + matmul
+path timed beside it for the dense configs.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--cpu-baseline auto|off]
 """
@@ -49,7 +64,10 @@ MFMA_F16_PEAK_TFS = 2500.0      # dense f16/bf16 MFMA
 MALL_BYTES = 256 << 20
 METRIC = 'µs/layer + achieved HBM GB/s (% of peak) for Q4_K/Q6_K matvec & MoE layer'
 WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill',
-             'hbm_copy']
+             'llama3_8b_layer_chain', 'hbm_read_floor', 'hbm_copy']
+# the default run: the headline, then these under "workloads"
+DEFAULT_SUITE = ['q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill', 'llama3_8b_layer_chain',
+                 'hbm_read_floor']
 
 
 def log(msg):
@@ -61,7 +79,8 @@ def parse():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=200)
     ap.add_argument('--warmup', type=int, default=20)
-    ap.add_argument('--workload', default='llama3_8b_decode_layer', choices=WORKLOADS)
+    ap.add_argument('--workload', default=None, choices=WORKLOADS,
+                    help='one workload only (default: the headline plus every workload of the suite)')
     ap.add_argument('--cpu-baseline', default='auto', choices=['auto', 'off'])
     ap.add_argument('--seed', type=int, default=0)
     return ap.parse_args()
@@ -202,8 +221,97 @@ def time_cpu(fn, min_samples=5, budget_s=10.0, warm=2):
     return float(np.median(samples)), len(samples)
 
 
+def host_info():
+    """lscpu model name and the physical cores this process may run on, with
+    one logical CPU per physical core (the CPUs the baselines are pinned to)."""
+    import subprocess
+    info = {'model': cpu_model(), 'logical_cpus': os.cpu_count()}
+    allowed = sorted(os.sched_getaffinity(0)) if hasattr(os, 'sched_getaffinity') else list(range(os.cpu_count()))
+    primary = {}
+    try:
+        out = subprocess.run(['lscpu'], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(':')
+            if k.strip() == 'Model name':
+                info['model'] = v.strip()
+        out = subprocess.run(['lscpu', '-p=CPU,CORE,SOCKET'], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith('#'):
+                continue
+            cpu, core, sock = (int(x) for x in line.split(','))
+            if cpu in allowed:
+                primary.setdefault((sock, core), cpu)
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    cores = sorted(primary.values()) if primary else allowed
+    info['physical_cores'] = len(cores)
+    info['allowed_cpus'] = len(allowed)
+    info['_cores'] = cores
+    return info
+
+
+HOST = {}
+
+
+def host():
+    if not HOST:
+        HOST.update(host_info())
+    return HOST
+
+
 def host_note():
-    return f'host {cpu_model()}, {os.cpu_count()} logical CPUs visible'
+    h = host()
+    return (f"host {h['model']}, {h['physical_cores']} physical cores / {h['allowed_cpus']} logical CPUs "
+            f"available, pinned to one logical CPU per physical core")
+
+
+class pinned:
+    """Pin this process (and the threads the reference's pool starts) to the
+    first n physical cores, one logical CPU each, as `taskset` would."""
+
+    def __init__(self, n):
+        self.cpus = host()['_cores'][:max(1, n)]
+
+    def __enter__(self):
+        self.old = os.sched_getaffinity(0) if hasattr(os, 'sched_setaffinity') else None
+        if self.old is not None:
+            os.sched_setaffinity(0, self.cpus)
+        return self.cpus
+
+    def __exit__(self, *exc):
+        if self.old is not None:
+            os.sched_setaffinity(0, self.old)
+
+
+def cpu_runs(call, policy_threads, work, unit, sample, scale_us=1.0, min_samples=20, budget_s=8.0, numpy_call=None,
+             numpy_work=None):
+    """The reference kernels at the reference's thread policy (pinned to that
+    many physical cores) and on all physical cores (threads capped at 8 like
+    the reference's pool), plus the NumPy dequantize + matmul path when
+    numpy_call is given. call(None) runs one sample at the policy's thread
+    counts, call(n) with n threads everywhere; work is the bytes or flops it
+    represents (GB/s or TFLOP/s from the median)."""
+    div = 1e9 if unit == 'GB/s' else 1e12
+    allc = host()['physical_cores']
+    with pinned(policy_threads) as cpus:
+        us, n = time_cpu(lambda: call(None), min_samples=min_samples, budget_s=budget_s)
+    ta = min(8, allc)
+    with pinned(allc):
+        us_all, n_all = time_cpu(lambda: call(ta), min_samples=min_samples, budget_s=budget_s)
+    out = {'value': round(work / (us * 1e-6) / div, 5), 'unit': unit, 'cores': policy_threads, 'kind': 'reference',
+           'us_per_layer': round(us * scale_us, 1), 'samples': n,
+           'sample': f'{sample}; median of {n}; {host_note()} ({len(cpus)} for this run)',
+           'host': {k: v for k, v in host().items() if not k.startswith('_')},
+           'all_cores': {'value': round(work / (us_all * 1e-6) / div, 5), 'threads': ta, 'cores': allc,
+                         'us_per_layer': round(us_all * scale_us, 1), 'samples': n_all}}
+    if numpy_call is not None:
+        with pinned(allc):
+            us_np, n_np = time_cpu(numpy_call, min_samples=2, budget_s=budget_s, warm=1)
+        out['numpy'] = {'value': round((numpy_work or work) / (us_np * 1e-6) / div, 5), 'unit': unit,
+                        'us': round(us_np, 1), 'samples': n_np,
+                        'what': 'oracle restatement of engine/dequant.py dequantize + NumPy matmul '
+                                '(engine/gguf_parser.py:273-288 fallback), all physical cores'}
+    return out
 
 
 # ---------------------------------------------------------------- workloads
@@ -253,12 +361,11 @@ def wl_layer(args, torch, device, synth):
         from oracle import ref
         calls = [(host[name], vecs[src], rows, cols, t, reference_threads(rows, t))
                  for name, t, rows, cols, src in layer]
-        us, n = time_cpu(lambda: [ref.matvec(*c[:5], threads=c[5]) for c in calls], min_samples=20)
-        cpu = {'value': round(layer_bytes / (us * 1e-6) / 1e9, 3), 'unit': 'GB/s', 'us_per_layer': round(us, 1),
-               'cores': max(c[5] for c in calls), 'kind': 'reference',
-               'sample': f'{n} full layers (7 matvecs), median; engine/native_quant.cpp built with g++ -O2 '
-                         f'-mavx2 -mfma, reference thread policy '
-                         f'{dict((nm, c[5]) for (nm, *_), c in zip(layer, calls))}; {host_note()}'}
+        policy = dict((nm, c[5]) for (nm, *_), c in zip(layer, calls))
+        cpu = cpu_runs(lambda th: [ref.matvec(*c[:5], threads=c[5] if th is None else th) for c in calls],
+                       max(c[5] for c in calls), layer_bytes, 'GB/s',
+                       f'full layers (7 matvecs) of engine/native_quant.cpp built with g++ -O2 -mavx2 -mfma, '
+                       f'reference thread policy {policy}')
     gbs = layer_bytes / (ms * 1e-3) / 1e9
     return {
         'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
@@ -311,12 +418,13 @@ def wl_q4k(args, torch, device, synth):
     ms = roof['us_per_launch'] / 1e3
     cpu = None
     if args.cpu_baseline != 'off' and ref_ok():
-        from oracle import ref
+        from oracle import ref, quant
         th = reference_threads(14336, 12)
-        us, n = time_cpu(lambda: ref.matvec(raw, xv, 14336, 4096, 12, threads=th), min_samples=20)
-        cpu = {'value': round(nbytes / (us * 1e-6) / 1e9, 3), 'unit': 'GB/s', 'us_per_layer': round(us, 1),
-               'cores': th, 'kind': 'reference',
-               'sample': f'{n} calls of localai_q4k_matvec 14336x4096, median; {host_note()}'}
+
+        def numpy_path():
+            return quant.dequantize(raw, 12, (14336, 4096)) @ xv
+        cpu = cpu_runs(lambda t: ref.matvec(raw, xv, 14336, 4096, 12, threads=th if t is None else t), th, nbytes,
+                       'GB/s', 'calls of localai_q4k_matvec 14336x4096', numpy_call=numpy_path)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
@@ -345,16 +453,19 @@ def wl_q8_prefill(args, torch, device, synth):
     tfs = flops / (ms * 1e-3) / 1e12
     cpu = None
     if args.cpu_baseline != 'off' and ref_ok():
-        from oracle import ref
+        from oracle import ref, quant
         srows = 224                      # 1/64 of the rows, all 512 tokens
         sub = raw[:srows * (cols // 32) * 34]
         th = reference_threads(rows, 8)
-        us, n = time_cpu(lambda: ref.matmul(sub, xh, srows, cols, 8, threads=th), min_samples=3, budget_s=15)
         sflops = 2 * srows * cols * tokens
-        cpu = {'value': round(sflops / (us * 1e-6) / 1e12, 5), 'unit': 'TFLOP/s', 'cores': th, 'kind': 'reference',
-               'us_per_layer': round(us * rows / srows, 1),
-               'sample': f'{n} calls of localai_q8_0_matmul on {srows} of {rows} rows x {tokens} tokens '
-                         f'(median; us_per_layer scaled to all rows); {host_note()}'}
+        nrows = 1792                     # NumPy path: 1/8 of the rows
+
+        def numpy_path():
+            return xh @ quant.dequantize(raw[:nrows * (cols // 32) * 34], 8, (nrows, cols)).T
+        cpu = cpu_runs(lambda t: ref.matmul(sub, xh, srows, cols, 8, threads=th if t is None else t), th, sflops,
+                       'TFLOP/s', f'calls of localai_q8_0_matmul on {srows} of {rows} rows x {tokens} tokens '
+                       f'(us_per_layer scaled to all rows)', scale_us=rows / srows, min_samples=3, budget_s=12,
+                       numpy_call=numpy_path, numpy_work=2 * nrows * cols * tokens)
     return {'value': round(tfs, 2), 'unit': 'TFLOP/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'mfma_frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'dtype': 'f16 MFMA, fp32 accumulate',
             'data': 'synthetic (seeded GGML Q8_0 bytes, fp32 N(0,1) activations)',
@@ -450,12 +561,10 @@ def wl_zaya(args, torch, device, synth):
     cpu = None
     if args.cpu_baseline != 'off' and ref_ok():
         gu, dn, rw, h, idx = data
-        fn = _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, 1, None, threads=min(4, os.cpu_count() or 1))
-        us, n = time_cpu(fn, min_samples=5, budget_s=10)
-        cpu = {'value': round(nbytes / (us * 1e-6) / 1e9, 3), 'unit': 'GB/s', 'us_per_layer': round(us, 1),
-               'cores': min(4, os.cpu_count() or 1), 'kind': 'reference',
-               'sample': f'{n} MoE layers at T=1 (numpy router + localai_q6k_matvec per selected expert, '
-                         f'threads=4 as engine/zaya.py), median; {host_note()}'}
+        cpu = cpu_runs(lambda th: _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, 1, None,
+                                           threads=4 if th is None else th)(), 4, nbytes, 'GB/s',
+                       'MoE layers at T=1 (numpy router + localai_q6k_matvec per selected expert, threads=4 as '
+                       'engine/zaya.py:161)', min_samples=5, budget_s=8)
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
             'data': 'synthetic (seeded Q6_K experts, router N(0,0.02), h N(0,1))',
@@ -484,13 +593,11 @@ def wl_qwen3(args, torch, device, synth):
     cpu = None
     if args.cpu_baseline != 'off' and ref_ok():
         gu, dn, rw, h, idx = data
-        th = min(6, os.cpu_count() or 1)
-        fn = _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, T, bias, threads=th)
-        us, n = time_cpu(fn, min_samples=2, budget_s=20, warm=1)
-        cpu = {'value': round(flops / (us * 1e-6) / 1e12, 5), 'unit': 'TFLOP/s', 'us_per_layer': round(us, 1),
-               'cores': th, 'kind': 'reference',
-               'sample': f'{n} MoE prefill layers (numpy router + localai_q4k_matmul per expert on its gathered '
-                         f'tokens), median; {host_note()}'}
+        th = reference_threads(2 * I, 12)
+        cpu = cpu_runs(lambda t_: _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, T, bias,
+                                           threads=th if t_ is None else t_)(), th, flops, 'TFLOP/s',
+                       'MoE prefill layers (numpy router + localai_q4k_matmul per expert on its gathered tokens)',
+                       min_samples=2, budget_s=12)
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'tflops': round(tfs, 2),
             'mfma_frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'dtype': 'fp32 / f16 MFMA',
@@ -502,6 +609,89 @@ def wl_qwen3(args, torch, device, synth):
                          'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4),
                          'traffic': None, 'us_per_launch': round(ms * 1e3, 3), 'bytes_per_launch': nbytes},
             'cpu_baseline': cpu}
+
+
+def wl_chain(args, torch, device, synth):
+    """The decode layer's seven matvecs as one launch with the glue between
+    them (localai_hip_layer_chain): o, residual + RMSNorm, gate/up with
+    SiLU*up, down, residual + RMSNorm, next layer's q/k/v."""
+    from localai_amd.layer import DecodeLayerChain
+    layer = synth.LLAMA3_8B_LAYER
+    layer_bytes = synth.layer_algorithmic_bytes()
+    copies = rotations(synth.layer_weight_bytes())
+    rng = np.random.default_rng(args.seed)
+    host = {name: synth.quant_tensor(rng, t, rows, cols) for name, t, rows, cols, _ in layer}
+    pre = device.to_device_f32(synth.activations(rng, 4096))
+    att = device.to_device_f32(synth.activations(rng, 4096))
+    w1 = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
+    w2 = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
+    log(f'chain: building {copies} layer copies')
+    chains = [DecodeLayerChain({n: device.QMat.from_ggml(host[n], t, r, c) for n, t, r, c, _ in layer}, w1, w2,
+                               1e-5, head_dim=128) for _ in range(copies)]
+    stream = torch.cuda.Stream()
+    outs = tuple(torch.empty_like(o) for o in chains[0].forward_device(pre, att))
+    torch.cuda.synchronize()
+    ms = time_steps(torch, [lambda c=c: c.forward_device(pre, att, out=outs, stream=stream) for c in chains], stream,
+                    args.steps, args.warmup)
+    chains[0].check(stream)
+    gbs = layer_bytes / (ms * 1e-3) / 1e9
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+            'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
+            'data': 'synthetic (seeded GGML Q4_K/Q6_K bytes, fp32 N(0,1) activations, norm weights U(0.5,1.5))',
+            'config': {'workload': 'llama3_8b_decode_layer_chain_one_launch', 'algorithmic_bytes_per_layer': layer_bytes,
+                       'weight_copies_rotated': copies},
+            'roofline': {'bound': 'hbm', 'kernel': 'layer_chain_kernel (the whole chain)', 'achieved': round(gbs, 1),
+                         'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None,
+                         'us_per_launch': round(ms * 1e3, 3), 'bytes_per_launch': layer_bytes},
+            'cpu_baseline': None}
+
+
+def wl_floor(args, torch, device, synth):
+    """Streaming-read floors (localai_hip_stream_read): what one launch of a
+    given size can read at best, rotated beyond the Infinity Cache like the
+    matvec workloads."""
+    from localai_amd import _lib
+    lib = _lib.load()
+    segs = {'qkv': 9469952 + 2379776 + 3461120, 'o': 9469952, 'gate_up': 2 * 33030144, 'down': 48168960}
+    segs = {k: v - v % 16 for k, v in segs.items()}
+    layer = sum(segs.values())
+    copies = rotations(layer)
+    bufs = [torch.empty(layer, dtype=torch.uint8, device=device.device()).fill_(i + 1) for i in range(copies)]
+    out = torch.zeros(4, dtype=torch.int32, device=device.device())
+    stream = torch.cuda.Stream()
+    sp = lambda: ctypes_stream(stream)   # noqa: E731
+
+    def read(buf, off, n):
+        _lib.check(lib.localai_hip_stream_read(device.ptr(buf) + off, n, device.ptr(out), sp()))
+
+    def per_layer_chain(buf):
+        off = 0
+        for name in ('qkv', 'o', 'gate_up', 'down'):
+            read(buf, off, segs[name])
+            off += segs[name]
+    res = {}
+    ms = time_steps(torch, [lambda b=b: read(b, 0, 33030144) for b in bufs], stream, args.steps, args.warmup)
+    res['one_launch_33MB'] = {'us': round(ms * 1e3, 3), 'GB/s': round(33030144 / (ms * 1e-3) / 1e9, 1),
+                              'frac': round(33030144 / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    ms = time_steps(torch, [lambda b=b: per_layer_chain(b) for b in bufs], stream, args.steps, args.warmup)
+    res['layer_as_four_launches'] = {'us': round(ms * 1e3, 3), 'GB/s': round(layer / (ms * 1e-3) / 1e9, 1),
+                                     'frac': round(layer / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                     'bytes': segs}
+    ms1 = time_steps(torch, [lambda b=b: read(b, 0, layer) for b in bufs], stream, args.steps, args.warmup)
+    gbs = layer / (ms1 * 1e-3) / 1e9
+    res['layer_as_one_launch'] = {'us': round(ms1 * 1e3, 3), 'GB/s': round(gbs, 1),
+                                  'frac': round(gbs / HBM_PEAK_GBS, 4)}
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms1, 'hbm_frac': round(gbs / HBM_PEAK_GBS, 4),
+            'dtype': 'u8', 'data': 'constant bytes', 'floors': res,
+            'config': {'workload': 'hbm_stream_read', 'bytes_per_layer': layer, 'copies_rotated': copies},
+            'roofline': {'bound': 'hbm', 'kernel': 'stream_read_kernel', 'achieved': round(gbs, 1),
+                         'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
+            'cpu_baseline': None}
+
+
+def ctypes_stream(stream):
+    import ctypes
+    return ctypes.c_void_p(int(stream.cuda_stream))
 
 
 def wl_copy(args, torch, device, synth):
@@ -520,6 +710,19 @@ def wl_copy(args, torch, device, synth):
             'cpu_baseline': None}
 
 
+FUNCS = {'llama3_8b_decode_layer': 'wl_layer', 'q4k_matvec': 'wl_q4k', 'q8_0_prefill': 'wl_q8_prefill',
+         'zaya_moe_decode': 'wl_zaya', 'qwen3_moe_prefill': 'wl_qwen3', 'llama3_8b_layer_chain': 'wl_chain',
+         'hbm_read_floor': 'wl_floor', 'hbm_copy': 'wl_copy'}
+
+
+def run_workload(name, args, torch, device, synth):
+    DIST.clear()
+    r = globals()[FUNCS[name]](args, torch, device, synth)
+    if DIST and 'step_stats' not in r:
+        r['step_stats'] = DIST[0]
+    return r
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -531,16 +734,24 @@ def main():
 
     if native_quant.get_native() is None:
         raise SystemExit('no HIP device / library: the benchmark needs the GPU path')
-    fn = {'llama3_8b_decode_layer': wl_layer, 'q4k_matvec': wl_q4k, 'q8_0_prefill': wl_q8_prefill,
-          'zaya_moe_decode': wl_zaya, 'qwen3_moe_prefill': wl_qwen3, 'hbm_copy': wl_copy}[args.workload]
-    r = fn(args, torch, device, synth)
+    name = args.workload or 'llama3_8b_decode_layer'
+    log(f'workload {name}')
+    r = run_workload(name, args, torch, device, synth)
+    suite = {}
+    if args.workload is None:
+        for other in DEFAULT_SUITE:
+            log(f'workload {other}')
+            w = run_workload(other, args, torch, device, synth)
+            w['ms_per_step'] = round(w['ms_per_step'], 6)
+            suite[other] = w
+            torch.cuda.empty_cache()
     ms = r.pop('ms_per_step')
-    if DIST and 'step_stats' not in r:
-        r['step_stats'] = DIST[0]
     line = {'metric': METRIC, 'value': r.pop('value'), 'unit': r.pop('unit'), 'n_gpus': 1, 'steps': args.steps,
             'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True, 'scaling': 'weak',
             'vs_baseline': None}
     line.update(r)
+    if suite:
+        line['workloads'] = suite
     print(json.dumps(line), flush=True)
 
 

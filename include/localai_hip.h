@@ -283,6 +283,15 @@ int localai_hip_moe_error(const void *workspace_dev, int64_t tokens, int64_t exp
  * counterpart in the reference. */
 int localai_hip_debug_fused_wait(int spin_limit, int producers_count);
 
+/* ---- measurement -------------------------------------------------------- */
+
+/* Read `bytes` (a multiple of 16) at src_dev once, as fast as the kernel can
+ * stream them, and leave a fold of the data in out_dev[0] only in the
+ * practically impossible case that it equals a fixed constant: the HBM read
+ * floor the decode kernels are compared with (bench.py, hbm_read_floor). No
+ * counterpart in the reference. */
+int localai_hip_stream_read(const void *src_dev, int64_t bytes, uint32_t *out_dev, void *stream);
+
 /* ---- host weight registration for the legacy exports -------------------- */
 
 /* Declare [host, host+nbytes) immutable (e.g. a GGUF mmap). Legacy calls whose

@@ -359,6 +359,15 @@ int localai_hip_debug_fused_wait(int spin_limit, int producers_count) {
     return set_fused_wait(spin_limit, producers_count);
 }
 
+int localai_hip_stream_read(const void *src, int64_t bytes, uint32_t *out, void *stream) {
+    clear_error();
+    if (!src || !out) return fail(LOCALAI_EARG, "stream read: null pointer");
+    if (bytes < 0 || bytes % 16 || (reinterpret_cast<uintptr_t>(src) & 15))
+        return fail(LOCALAI_EARG, "stream read: bytes a multiple of 16 and a 16-byte aligned source");
+    if (int st = ensure_device()) return st;
+    return launch_stream_read(src, bytes, out, (hipStream_t)stream);
+}
+
 int64_t localai_hip_layer_workspace_size(int64_t dim, int64_t ffn) {
     if (dim < 1 || ffn < 1) return -1;
     return (int64_t)layer_workspace_bytes(dim, ffn);

@@ -86,6 +86,8 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
 // the stream has finished); test controls of its waits
 int moe_error_word(const void *ws, int64_t T, int64_t E, hipStream_t s, uint32_t *word);
 int set_fused_wait(int spin, int count);
+int launch_stream_read(const void *src, int64_t bytes, uint32_t *out, hipStream_t s);
+
 // decode-layer matvec chain (layer.hip); m: o, gate, up, down, q, k, v
 size_t layer_workspace_bytes(int64_t dim, int64_t ffn);
 int launch_layer_chain(const localai_qmat *const *m, const float *pre, const float *att, const float *w_ffn,

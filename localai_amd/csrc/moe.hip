@@ -184,6 +184,12 @@ constexpr int ROUTE_CH = 8;
 // logits, then the row of h as fp64. PART: H is not a
 // multiple of 256 * ROUTE_CH, so the last pass over a row has chunks past
 // its end.
+// Phase marks of the router (entry, h staged, logits summed, selection
+// done); empty unless a profiling build defines it.
+#ifndef ROUTE_MARK
+#define ROUTE_MARK(phase)
+#endif
+
 template <bool LDS_H, bool PART, bool LEAN = false>
 __device__ __forceinline__ void route_token(const float *__restrict__ h, int H, const float *__restrict__ rw,
                                             const float *__restrict__ rb, int E, int k, float *__restrict__ logits,
@@ -204,6 +210,7 @@ __device__ __forceinline__ void route_token(const float *__restrict__ h, int H, 
             v[j] = *reinterpret_cast<const float4 *>(row + (i < H ? i : H - 4));   // unconditional
         }
     };
+    ROUTE_MARK(0);
     float4 wv[CH];
     if (onepass && w < E) load(wv, rw + (int64_t)w * H, 0);   // in flight while h is staged
     if (LDS_H) {
@@ -214,6 +221,7 @@ __device__ __forceinline__ void route_token(const float *__restrict__ h, int H, 
         }
         __syncthreads();
     }
+    ROUTE_MARK(1);
     // lane l sums elements 256j + 4l + c (j = 0, 1, ..., c = 0..3) in that
     // order (exact fp64 products); H is a multiple of 4, so a chunk is either
     // wholly inside the row or wholly past its end
@@ -251,14 +259,19 @@ __device__ __forceinline__ void route_token(const float *__restrict__ h, int H, 
     if (onepass) {
         if (!LDS_H) load(hv, ht, 0);
         for (int e = w; e < E; e += nw) {
-            const int en = e + nw < E ? e + nw : e;
-            float4 wn[CH];
-            load(wn, rw + (int64_t)en * H, 0);
-            double s = 0.0;
-            dot(wv, hv, 0, s);
-            finish(e, s);
+            if (e + nw < E) {   // the next expert's row goes out before this one is summed
+                float4 wn[CH];
+                load(wn, rw + (int64_t)(e + nw) * H, 0);
+                double s = 0.0;
+                dot(wv, hv, 0, s);
+                finish(e, s);
 #pragma unroll
-            for (int j = 0; j < CH; ++j) wv[j] = wn[j];
+                for (int j = 0; j < CH; ++j) wv[j] = wn[j];
+            } else {
+                double s = 0.0;
+                dot(wv, hv, 0, s);
+                finish(e, s);
+            }
         }
     } else {
         for (int e = w; e < E; e += nw) {
@@ -272,8 +285,11 @@ __device__ __forceinline__ void route_token(const float *__restrict__ h, int H, 
             finish(e, s);
         }
     }
+    ROUTE_MARK(2);
     __syncthreads();
+    ROUTE_MARK(3);
     if (w == 0) route_select_any(lds_f, E, k, t, topk_idx, topk_w, tb, tables);
+    ROUTE_MARK(4);
 }
 
 template <bool LDS_H, bool PART>
