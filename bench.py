@@ -393,17 +393,18 @@ def gate_roofline(args, torch, device, gate_host, x, stream):
         m.close()
     return {'bound': 'hbm', 'kernel': 'gemv_mfma_q4k 14336x4096', 'achieved': round(achieved, 1),
             'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4),
-            'traffic': measured_traffic('gemv_q4k_14336x4096_traffic.json'),
+            'traffic': measured_traffic('q4k', 'gate'),
             'us_per_launch': round(kms * 1e3, 3), 'bytes_per_launch': gate_bytes}
 
 
-def measured_traffic(name):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    passes (profiles/), calibrated on a copy of known size; None if absent."""
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of one kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic.json, calibrated on a
+    copy of known size); None if absent."""
     try:
-        with open(os.path.join(ROOT, 'profiles', name)) as f:
-            return int(json.load(f)['traffic_bytes'])
-    except (OSError, ValueError, KeyError):
+        with open(os.path.join(ROOT, 'profiles', 'traffic.json')) as f:
+            return int(json.load(f)[workload][kernel]['traffic_bytes'])
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
@@ -471,9 +472,9 @@ def wl_q8_prefill(args, torch, device, synth):
             'data': 'synthetic (seeded GGML Q8_0 bytes, fp32 N(0,1) activations)',
             'config': {'workload': 'q8_0_prefill_gemm_14336x4096x512', 'tokens': tokens, 'flops': flops,
                        'weight_copies_rotated': copies},
-            'roofline': {'bound': 'mfma', 'kernel': 'x_to_f16 + gemm_kernel<Q8_0> (whole call)',
+            'roofline': {'bound': 'mfma', 'kernel': 'x_to_f16 + gemm_tile_kernel<Q8_0> (whole call)',
                          'achieved': round(tfs, 1), 'peak': MFMA_F16_PEAK_TFS, 'unit': 'TFLOP/s',
-                         'frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'traffic': None,
+                         'frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'traffic': measured_traffic('q8', 'gemm'),
                          'us_per_launch': round(ms * 1e3, 3), 'flops_per_launch': flops},
             'cpu_baseline': cpu}
 
@@ -509,7 +510,34 @@ def _moe_gpu(args, torch, device, synth, E, H, I, k, t, T, bias, per_expert_byte
                             for L in layers], stream, args.steps, args.warmup)
     if not torch.isfinite(out).all():
         raise SystemExit('non-finite MoE output')
+    _moe_gpu.last = (layers, hd, stream)
     return ms, nbytes, distinct, copies, (gu, dn, rw, h, idx.cpu().numpy())
+
+
+def experts1_roofline(args, torch, device, E, H, I, k, per_expert):
+    """The fused one-token expert kernel (localai_hip_moe_experts1: gate_up
+    and down of the chosen experts in one launch) timed alone over the rotated
+    layer copies of the last _moe_gpu call, with its router's choice fixed."""
+    import ctypes
+    from localai_amd import _lib
+    layers, hd, stream = _moe_gpu.last
+    lib = _lib.load()
+    _, idx, gates = layers[0].forward_device(hd)
+    out = torch.empty(H, dtype=torch.float32, device=hd.device)
+    sp = ctypes.c_void_p(int(stream.cuda_stream))
+
+    def run(L):
+        ws = L.workspace(1)
+        _lib.check(lib.localai_hip_moe_experts1(device.ptr(hd), H, L.gate_up.handle, L.down.handle, k,
+                                                device.ptr(idx), device.ptr(gates), -1, device.ptr(out),
+                                                device.ptr(ws), ws.numel(), sp))
+    ms = time_steps(torch, [lambda L=L: run(L) for L in layers], stream, args.steps, args.warmup)
+    nbytes = k * per_expert + 2 * H * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {'bound': 'hbm', 'kernel': 'moe_decode1_kernel (localai_hip_moe_experts1: both experts, gate_up and down)',
+            'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4),
+            'traffic': measured_traffic('zaya', 'decode1'), 'us_per_launch': round(ms * 1e3, 3),
+            'bytes_per_launch': nbytes}
 
 
 def _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, T, bias, threads):
@@ -551,10 +579,14 @@ def wl_zaya(args, torch, device, synth):
     E, H, I, k, t = 16, 2048, 4096, 2, 14
     per_expert = 2 * I * (H // 256) * 210 + H * (I // 256) * 210
     res = {}
+    roof = None
     for T in (1, 8):
         ms, nbytes, distinct, copies, data = _moe_gpu(args, torch, device, synth, E, H, I, k, t, T, None,
                                                       per_expert, 'zaya')
         res[T] = (ms, nbytes, distinct, copies, data)
+        if T == 1:
+            roof = experts1_roofline(args, torch, device, E, H, I, k, per_expert)
+        _moe_gpu.last = None
     ms, nbytes, distinct, copies, data = res[1]
     gbs = nbytes / (ms * 1e-3) / 1e9
     ms8, nb8, d8, _, _ = res[8]
@@ -573,12 +605,7 @@ def wl_zaya(args, torch, device, synth):
                        'tokens_8': {'us_per_layer': round(ms8 * 1e3, 3), 'distinct_experts': d8,
                                     'algorithmic_bytes': nb8,
                                     'GB/s': round(nb8 / (ms8 * 1e-3) / 1e9, 2)}},
-            'roofline': {'bound': 'hbm', 'kernel': 'whole MoE layer (route, permute, grouped gate_up, '
-                                                    'grouped down, combine)',
-                         'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                         'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None,
-                         'us_per_launch': round(ms * 1e3, 3), 'bytes_per_launch': nbytes},
-            'cpu_baseline': cpu}
+            'roofline': roof, 'cpu_baseline': cpu}
 
 
 def wl_qwen3(args, torch, device, synth):
@@ -587,6 +614,7 @@ def wl_qwen3(args, torch, device, synth):
     bias = synth.zipf_bias(E)
     ms, nbytes, distinct, copies, data = _moe_gpu(args, torch, device, synth, E, H, I, k, t, T, bias,
                                                   per_expert, 'qwen3')
+    _moe_gpu.last = None
     flops = 2 * T * k * (H * 2 * I + I * H)
     gbs = nbytes / (ms * 1e-3) / 1e9
     tfs = flops / (ms * 1e-3) / 1e12
