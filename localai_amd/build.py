@@ -4,7 +4,9 @@
 
 Every source is compiled on each call (the objects go to localai_amd/_build/,
 the library to localai_amd/liblocalai_hip.so). Packed-fp32 instruction
-selection is disabled for all device code.
+selection is disabled for all device code. Kernels whose global loads count
+their own waits are checked in their generated assembly (isa_check.py); the
+build fails if one touches a register whose load may still be in flight.
 """
 from __future__ import annotations
 
@@ -42,11 +44,24 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+# kernels whose global loads are asm with hand-counted waits (isa_check.py)
+COUNTED_LOADS = [('gemm.hip', 'gemm_cu_q80_kernel')]
+
+
+def _check(item) -> None:
+    from .isa_check import check_source
+    src, kernel = item
+    check_source(HIPCC, COMMON, CSRC / src, kernel, BUILD / (src + '.' + kernel + '.s'))
+
+
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs) + len(COUNTED_LOADS))) as ex:
+        checks = [ex.submit(_check, item) for item in COUNTED_LOADS]
         objs = list(ex.map(_compile, srcs))
+        for c in checks:
+            c.result()
     tmp = LIB.with_suffix('.so.tmp')
     cmd = [HIPCC, '-shared', f'--offload-arch={ARCH}', '-o', str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)

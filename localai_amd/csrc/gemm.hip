@@ -2,17 +2,29 @@
 //
 // Counterpart of decoded_matmul_row / localai_*_matmul
 // (engine/native_quant.cpp:444-531, :744-768): the reference decodes each row
-// exactly to fp32 and runs fp32 FMAs over the tokens. Here a workgroup owns a
-// 128-row x 128-token output tile; per 128-value K step it decodes its 128
-// weight rows exactly in fp32 (the same per-type formulas as the dequant
-// kernels), rounds them once to f16 into an LDS tile, stages the matching f16
-// activations next to it, and 4 waves (64 x 64 outputs each) run
-// v_mfma_f32_16x16x32_f16 with fp32 accumulation.
+// exactly to fp32 and runs fp32 FMAs over the tokens. Here weights are decoded
+// exactly (the per-type formulas of the dequant kernels), rounded once to f16
+// and multiplied with v_mfma_f32_16x16x32_f16 in fp32 accumulation.
 //
-// Activations are converted once per call: each token row is scaled by a
-// power of two so that its largest magnitude lies in [2^14, 2^15) (exact),
-// rounded to f16, and the output is scaled back by the inverse power. f16 (11
-// significant bits) rather than bf16 (8) keeps the normwise error near 2^-12.
+// Activations are converted once per call (x_to_f16): each token row is scaled
+// by a power of two so that its largest magnitude lies in [2^14, 2^15)
+// (exact), rounded to f16, and the output is scaled back by the inverse power.
+// f16 (11 significant bits) rather than bf16 (8) keeps the normwise error near
+// 2^-12. The rows are stored row-major, or (for the CU-tile kernel) in MFMA
+// operand order, 1 KB per 16 tokens x 32 values.
+//
+// Three kernels:
+//   gemm_kernel       any type from the GGML bytes: a workgroup decodes a
+//                     128-row weight tile into LDS per 128-value step and 4
+//                     waves multiply it with 128 tokens (also the MoE expert
+//                     tiles of moe.hip);
+//   gemm_tile_kernel  Q4_K / Q6_K / Q8_0 from the tile form (mfma_core.h):
+//                     each wave decodes its own two 16-row tiles into B
+//                     operands in registers, x is staged in LDS
+//                     (global_load_lds), dense and MoE;
+//   gemm_cu_q80_kernel dense Q8_0 with 256 tokens or more: one 224-row x
+//                     128-token tile per CU, sized to what L2 can feed a CU
+//                     (its own section below).
 #include <type_traits>
 
 #include "gemv_core.h"
@@ -40,14 +52,25 @@ constexpr int GM_LD = GM_BK + 8;       // LDS row stride in halves (272 B: 16 la
 // (two 16-byte loads, one 16-byte store); NG > 0: the lane's NG groups stay
 // in registers between the max and the conversion, NG = 0: the row is read
 // twice. cols is a multiple of 8; vec: X rows are 16-byte aligned.
+// tiled: Xh holds MFMA A operands instead of rows: token t's values
+// 32 q + 8 c .. + 7 (c < 4) go to 16-byte slot ((t / 16) * (ldh / 32) + q) * 64
+// + (t % 16) + 16 c, so that one 32-value slice of 16 tokens is 1 KB
+// contiguous in lane order; tokens ntok .. ntok_pad - 1 are written as zeros.
 template <int NG>
 __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__ X, int64_t ldx, int cols,
                                                        const int32_t *__restrict__ rows_map, int k, int64_t ntok,
                                                        _Float16 *__restrict__ Xh, int ldh,
-                                                       float *__restrict__ inv, int vec) {
+                                                       float *__restrict__ inv, int vec, int tiled, int64_t ntok_pad) {
     const int lane = lane_id();
     const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id();
-    if (t >= ntok) return;
+    if (t >= ntok_pad) return;
+    if (t >= ntok) {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int gi = lane; gi < (ldh >> 3); gi += 64)
+            *reinterpret_cast<h8 *>(Xh + 8 * ((((t >> 4) * (ldh >> 5) + (gi >> 2)) << 6) + (t & 15) + 16 * (gi & 3))) = z;
+        return;
+    }
     const int64_t src = rows_map ? (int64_t)(rows_map[t] / k) : t;
     const float *x = X + src * ldx;
     const int ngx = cols >> 3, ng = ldh >> 3;
@@ -111,7 +134,10 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__
             o[c] = (_Float16)(l[c] * sc);
             o[4 + c] = (_Float16)(h[c] * sc);
         }
-        *reinterpret_cast<h8 *>(xh + 8 * gi) = o;
+        if (tiled)
+            *reinterpret_cast<h8 *>(Xh + 8 * ((((t >> 4) * (ldh >> 5) + (gi >> 2)) << 6) + (t & 15) + 16 * (gi & 3))) = o;
+        else
+            *reinterpret_cast<h8 *>(xh + 8 * gi) = o;
     };
     if (NG > 0) {
 #pragma unroll
@@ -715,6 +741,300 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- CU-tile GEMM (Q8_0, many tokens)
+
+// One workgroup per CU owns a 224-row x 128-token output tile (14 row tiles
+// x 8 token tiles; 14336 x 512 is exactly 256 such tiles). The shape follows
+// from what a CU can be fed: L2 delivers about 32 B per clock to a CU (1 KB
+// contiguous per load instruction; half that for 64-byte pieces of rows 8 KB
+// apart). Per 64-value K step the tile needs 128 tokens x 128 B of x and 224
+// rows x 68 B of Q8_0 weights, about 31 KB, roughly what L2 delivers in the
+// time of the step's MFMAs.
+//
+// Waves 0..6 compute: wave w owns row tiles 2w, 2w + 1 for all 8 token tiles
+// (32 v_mfma_f32_16x16x32_f16 per step). It loads its own raw weights (tile
+// form, 1 KB contiguous per load) and decodes them in registers straight into
+// MFMA A operands, so weights never pass through LDS. x (the tiled form of
+// x_to_f16, 16 KB per step: 8 token tiles x 2 slices, 1 KB each in lane
+// order) goes into a 4-step LDS ring three steps ahead, wave w copying token
+// tile w with global_load_lds; the compute waves read it as B operands (one
+// conflict-free ds_read_b128 per token tile and slice). With the weights as
+// A and the tokens as B, each lane ends up holding 4 consecutive rows of one
+// token, stored as one 16-byte write. Ring slot (j + 3) % 4 is refilled at
+// step j, after the barrier that ended step j - 1, its last reader. One
+// workgroup barrier per step.
+//
+// The compute waves' weight loads are asm whose completion the kernel counts
+// itself (4 loads per step); every use goes through cu_wait_w, which
+// names the registers, and the build checks the generated code for any
+// instruction touching a register whose load may still be in flight. The
+// MFMAs are asm with the accumulators in VGPRs: as builtins, the register
+// allocator rotated the accumulators through copies at every iteration of
+// the unrolled loop, and in AGPRs the compiler capped the VGPRs at 128 and
+// spilled (copied) registers with loads in flight into AGPRs.
+constexpr int CU_RT = 14;                        // row tiles per workgroup
+constexpr int CU_TT = 8;                         // token tiles per workgroup
+constexpr int CU_WR = 2;                         // row tiles per compute wave
+constexpr int CU_NC = 7;                         // compute waves
+constexpr int CU_RING = 4;                       // x ring depth (steps)
+constexpr int CU_XSTEP = CU_TT * 2 * 1024;       // x bytes per step
+constexpr int CU_TOKENS = CU_TT * 16;
+// LDS requested per workgroup: more than half of a CU's 160 KB (the ring uses
+// 64 KB), so that no CU holds two workgroups (a second one would halve that
+// CU's MFMA rate and leave another CU idle)
+constexpr int CU_LDS_RESERVE = 96 * 1024;
+static_assert(CU_RING * CU_XSTEP <= CU_LDS_RESERVE, "CU-tile LDS");
+
+// global loads with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
+// byte offset (fewer VGPRs than 64-bit addresses per load)
+__device__ __forceinline__ void cu_load(mt_i4 &v, const void *base, uint32_t off) {
+    asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(off), "s"(base) : "memory");
+}
+__device__ __forceinline__ void cu_load(int &v, const void *base, uint32_t off) {
+    asm volatile("global_load_dword %0, %1, %2" : "=v"(v) : "v"(off), "s"(base) : "memory");
+}
+// Workgroup barrier without the fence of __syncthreads, whose wait for every
+// outstanding LDS read would stall on the next step's operand prefetch. What
+// crosses it is ordered by hand: each wave waits (vmcnt) for its own copies
+// into the ring before arriving, and every read of a ring slot has been
+// consumed by an MFMA (lgkmcnt wait) before the barrier that precedes the
+// slot's refill. The memory clobber keeps the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void cu_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// 1 KB from global memory (16 bytes per lane) into LDS at the wave-uniform
+// byte address lds (lane i's bytes at lds + 16 i), through M0, which it saves
+// and restores
+__device__ __forceinline__ void cu_dma(const void *src, uint32_t lds) {
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep)
+                 : "v"(src), "s"(lds)
+                 : "memory");
+}
+template <int N, class W>
+__device__ __forceinline__ void cu_wait_w(W &w) {
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(w[0].q), "+v"(w[0].d), "+v"(w[1].q), "+v"(w[1].d) : "n"(N) : "memory");
+}
+
+// XCD-aware tile order. Workgroups go to the 8 XCDs round robin
+// (blockIdx.x % 8); renumbered, each XCD runs a contiguous range, ordered as
+// groups of (up to) 4 token blocks of one row block. The 4 workgroups of a
+// row block then run side by side on one XCD and read each weight step from
+// its L2 (HBM reads the 62 MB of 14336 x 4096 weights once), and the XCD's
+// workgroups, all at similar K positions, share the x steps in L2 as well.
+__device__ __forceinline__ void cu_tile(int nrb, int ntb, int &rb, int &tb) {
+    const int G = gridDim.x, per = G / 8, rem = G % 8, xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
+    const int L = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int tq = L / (4 * nrb), r = L % (4 * nrb), gs = ntb - 4 * tq < 4 ? ntb - 4 * tq : 4;
+    rb = r / gs;
+    tb = 4 * tq + r % gs;
+}
+
+// y_vec: Y rows are contiguous (y_rs 1), 16-byte aligned, y_ts % 4 == 0
+__global__ __launch_bounds__(512, 1) void gemm_cu_q80_kernel(GemmArgs a, int nrb, int ntb, int y_vec) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t cu_lds[];
+    const lq_geom &g = a.g;
+    const int lane = lane_id(), w = wave_id();
+    int rb, tb;
+    cu_tile(nrb, ntb, rb, tb);
+    const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS, nsb = mt_nsb(g);
+    const int64_t p0 = (int64_t)tb * CU_TOKENS, t0 = (int64_t)rb * CU_RT;
+    const int nsteps = (int)(nsb * 4);               // 64-value steps (a multiple of 4)
+
+    // x: wave w copies token tile w (both 32-value slices, 2 KB) of each step
+    // into the ring; the compute waves read every token tile
+    const int64_t nks = a.ldh / 32, ttiles = (a.ntok + 15) / 16;
+    int64_t xtt = p0 / 16 + w;
+    xtt = xtt < ttiles ? xtt : ttiles - 1;
+    const uint8_t *const xsrc = reinterpret_cast<const uint8_t *>(a.Xh) + xtt * nks * 1024 + 16 * lane;
+    const uint32_t ring = (uint32_t)(uintptr_t)cu_lds + 2048 * w;
+    auto dma = [&](int j) {                          // 2 loads
+        const int jj = j < nsteps ? j : nsteps - 1;
+        const uint32_t dst = ring + (j % CU_RING) * CU_XSTEP;
+        cu_dma(xsrc + 2048 * jj, dst);
+        cu_dma(xsrc + 2048 * jj + 1024, dst + 1024);
+    };
+    dma(0);
+    dma(1);
+    dma(2);
+
+    if (w == CU_NC) {
+        // ---- the eighth wave only copies: x(j + 1) (requested at step j - 2)
+        // is complete once at most the 4 loads of steps j - 1 and j are in flight
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (int j = 0; j < nsteps; ++j) {
+            dma(j + 3);
+            asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            cu_barrier();
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
+
+    // ---- compute waves
+    uint32_t woff[CU_WR];
+#pragma unroll
+    for (int r = 0; r < CU_WR; ++r) {
+        int64_t t = t0 + CU_WR * w + r;
+        t = t < tiles ? t : tiles - 1;
+        woff[r] = (uint32_t)(t * nsb * MT_Q80_BLOCK);
+    }
+    const uint32_t qlane = 16 * lane, dlane = 4096 + 16 * (lane & 15);
+    struct WRaw { mt_i4 q; int d; };
+    auto load_w = [&](WRaw (&dst)[CU_WR], int j) {    // 4 loads
+        j = j < nsteps ? j : nsteps - 1;
+        const int blk = j >> 2, piece = j & 3;
+        const uint8_t *qb = a.Wt + (int64_t)blk * MT_Q80_BLOCK + piece * 1024, *db = a.Wt + (int64_t)blk * MT_Q80_BLOCK + 4 * piece;
+#pragma unroll
+        for (int r = 0; r < CU_WR; ++r) {
+            cu_load(dst[r].q, qb, woff[r] + qlane);
+            cu_load(dst[r].d, db, woff[r] + dlane);
+        }
+    };
+    typedef lq_h8 WOps[CU_WR][2];
+    auto decode = [&](WRaw (&src)[CU_WR], WOps &o) {
+#pragma unroll
+        for (int r = 0; r < CU_WR; ++r) {
+            const uint32_t d = (uint32_t)src[r].d;
+            const lq_h2 d0 = __builtin_bit_cast(lq_h2, (d & 0xFFFFu) * 0x10001u);
+            const lq_h2 d1 = __builtin_bit_cast(lq_h2, (d >> 16) * 0x10001u);
+            uint4 o0, o1;
+            q8_pairs((uint32_t)src[r].q[0], d0, o0.x, o0.y);
+            q8_pairs((uint32_t)src[r].q[1], d0, o0.z, o0.w);
+            q8_pairs((uint32_t)src[r].q[2], d1, o1.x, o1.y);
+            q8_pairs((uint32_t)src[r].q[3], d1, o1.z, o1.w);
+            o[r][0] = __builtin_bit_cast(lq_h8, o0);
+            o[r][1] = __builtin_bit_cast(lq_h8, o1);
+        }
+    };
+
+    lq_f4 acc[CU_WR][CU_TT];
+#pragma unroll
+    for (int r = 0; r < CU_WR; ++r)
+#pragma unroll
+        for (int i = 0; i < CU_TT; ++i) acc[r][i] = lq_f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // x B operands: slice sl of step j is read into xv[sl] as soon as the
+    // MFMAs of slice sl of step j - 1 are issued (x(j) has been in LDS since
+    // the barrier that ended step j - 2), so the reads overlap MFMAs
+    typedef lq_h8 XOps[2][CU_TT];
+    auto read_x = [&](int j, XOps &xv, int sl) {
+        const uint8_t *xs = cu_lds + (j % CU_RING) * CU_XSTEP + 16 * lane + sl * 1024;
+#pragma unroll
+        for (int i = 0; i < CU_TT; ++i) xv[sl][i] = *reinterpret_cast<const lq_h8 *>(xs + 2048 * i);
+    };
+    auto mfmas = [&](int j, XOps &xv, WOps &cur) {
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {
+#pragma unroll
+            for (int i = 0; i < CU_TT; ++i)
+#pragma unroll
+                for (int r = 0; r < CU_WR; ++r)
+                    asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(acc[r][i]) : "v"(cur[r][sl]), "v"(xv[sl][i]));
+            read_x(j + 1, xv, sl);
+        }
+    };
+
+    // Raw weights run 4 steps ahead in 4 register sets. Each step a compute
+    // wave requests its 2 KB of x(j + 3), then 4 weight loads: the raw set
+    // decoded at step j was requested at step j - 4 and is complete once at
+    // most the 18 loads of steps j - 3 .. j - 1 are in flight; the wave's own
+    // part of x(j + 1), requested at step j - 2, once at most 16 are (the
+    // weights of step j - 2 and steps j - 1, j), and the barrier then makes
+    // all of x(j + 1) visible. One decoded operand set: the MFMAs read their
+    // operands at issue, so the decode may overwrite them once the step's
+    // MFMAs are issued. The two compute waves of a SIMD (w and w + 4) run
+    // opposite phases, one issuing MFMAs while the other decodes:
+    //   waves 0..3, step j: MFMAs(j); decode W(j + 1); request x(j + 3), W(j + 5)
+    //   waves 4..6, step j: decode W(j); request x(j + 3), W(j + 4); MFMAs(j)
+    // Everything the prologue requested has landed before the loop: the
+    // compiler may copy loop-carried registers on entry, and a copy of a
+    // register still waiting for its load would read stale data.
+    WRaw wr[4][CU_WR];
+    WOps cur;
+    XOps xv;
+    if (w < 4) {
+        WRaw w0[CU_WR];
+        load_w(w0, 0);
+#pragma unroll
+        for (int k = 1; k <= 4; ++k) load_w(wr[k & 3], k);
+        cu_wait_w<16>(w0);
+        decode(w0, cur);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) cu_wait_w<0>(wr[k]);
+        __syncthreads();
+        read_x(0, xv, 0);
+        read_x(0, xv, 1);
+        auto step = [&](int j, WRaw (&w1)[CU_WR]) {
+            mfmas(j, xv, cur);
+            cu_wait_w<18>(w1);
+            decode(w1, cur);                    // past the end: a clamped copy nobody uses
+            dma(j + 3);
+            load_w(w1, j + 5);
+            asm volatile("s_waitcnt vmcnt(16)" ::: "memory");   // own part of x(j + 1)
+            cu_barrier();
+        };
+        for (int j = 0; j < nsteps; j += 4) {
+            step(j, wr[1]);
+            step(j + 1, wr[2]);
+            step(j + 2, wr[3]);
+            step(j + 3, wr[0]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) load_w(wr[k], k);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) cu_wait_w<0>(wr[k]);
+        __syncthreads();
+        read_x(0, xv, 0);
+        read_x(0, xv, 1);
+        auto step = [&](int j, WRaw (&w0)[CU_WR]) {
+            cu_wait_w<18>(w0);
+            decode(w0, cur);
+            dma(j + 3);
+            load_w(w0, j + 4);
+            mfmas(j, xv, cur);
+            asm volatile("s_waitcnt vmcnt(16)" ::: "memory");   // own part of x(j + 1)
+            cu_barrier();
+        };
+        for (int j = 0; j < nsteps; j += 4) {
+            step(j, wr[0]);
+            step(j + 1, wr[1]);
+            step(j + 2, wr[2]);
+            step(j + 3, wr[3]);
+        }
+    }
+    // the loads past the end land in registers the compiler counts as free;
+    // and the MFMAs are asm, so the compiler does not know to wait for their
+    // results before reading the accumulators: 24 wait states cover the
+    // longest (16-pass) MFMA write-to-read distance
+    asm volatile("s_waitcnt vmcnt(0)\n s_nop 7\n s_nop 7\n s_nop 7" ::: "memory");
+
+    // D: lane holds rows 4 (lane / 16) + v of a row tile, token lane % 16 of a token tile
+#pragma unroll
+    for (int i = 0; i < CU_TT; ++i) {
+        const int64_t p = p0 + 16 * i + (lane & 15);
+        if (p >= a.ntok) continue;
+        const float sc = a.inv[p];
+        float *yp = a.Y + p * a.y_ts;
+#pragma unroll
+        for (int r = 0; r < CU_WR; ++r) {
+            const int64_t t = t0 + CU_WR * w + r, row = t * MT_ROWS + 4 * (lane >> 4);
+            if (t >= tiles) continue;
+            const lq_f4 v = acc[r][i] * sc;
+            if (y_vec && row + 3 < g.rows) {
+                *reinterpret_cast<lq_f4 *>(yp + row) = v;
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (row + k < g.rows) yp[(row + k) * a.y_rs] = v[k];
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- host side
 
 // f16 activation rows are padded with zeros to a multiple of 256 values (the
@@ -722,23 +1042,26 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
 static int64_t gemm_ldh(const lq_geom &g) { return 256 * ((g.cols + 255) / 256); }
 
 int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok) {
-    const int64_t xh = (ntok * gemm_ldh(g) * 2 + 255) & ~(int64_t)255;
+    // room for the tiled form too: tokens padded to a multiple of 16
+    const int64_t xh = (((ntok + 15) / 16 * 16) * gemm_ldh(g) * 2 + 255) & ~(int64_t)255;
     return xh + ntok * 4;
 }
 
 int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *rows_map, int k, int64_t ntok,
-                    _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s) {
+                    _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s, int tiled) {
     if (ntok <= 0) return LOCALAI_OK;
     if (cols % 8 || ldh % 8 || ldh < cols) return fail(LOCALAI_EARG, "f16 rows: cols % 8 != 0");
+    if (tiled && ldh % 32) return fail(LOCALAI_EARG, "f16 tiles: row length % 32 != 0");
     const int vec = (uintptr_t)X % 16 == 0 && ldx % 4 == 0;
     const int per = (int)((ldh / 8 + 63) / 64);   // 8-value groups per lane
+    const int64_t npad = tiled ? (ntok + 15) / 16 * 16 : ntok;
     // one token per wave; one-wave workgroups below 1024 tokens, so that 512
     // tokens reach every CU (four-wave workgroups left half of them idle)
-    const int wpg = ntok < 1024 ? 1 : 4;
-    const dim3 grid((unsigned)((ntok + wpg - 1) / wpg));
+    const int wpg = npad < 1024 ? 1 : 4;
+    const dim3 grid((unsigned)((npad + wpg - 1) / wpg));
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, dim3(64 * wpg), 0, s, X, ldx, (int)cols, rows_map, k, ntok, Xh, (int)ldh, inv,
-                           vec);
+                           vec, tiled, npad);
     };
     if (per <= 1)
         go(x_to_f16_kernel<1>);
@@ -784,11 +1107,25 @@ int launch_gemm(const lq_geom &g, const uint8_t *W, const uint8_t *Wt, const flo
     if (ws_bytes < gemm_workspace_bytes(g, ntok)) return fail(LOCALAI_EARG, "matmul: workspace too small");
     const int64_t ldh = gemm_ldh(g);
     _Float16 *Xh = (_Float16 *)ws;
-    float *inv = (float *)((uint8_t *)ws + ((ntok * ldh * 2 + 255) & ~(int64_t)255));
-    if (int st = launch_x_to_f16(X, g.cols, g.cols, nullptr, 1, ntok, Xh, ldh, inv, s)) return st;
+    float *inv = (float *)((uint8_t *)ws + ((((ntok + 15) / 16 * 16) * ldh * 2 + 255) & ~(int64_t)255));
     GemmArgs a{};
     a.g = g; a.W = W; a.Xh = Xh; a.ldh = (int)ldh; a.inv = inv; a.ntok = ntok; a.Y = Y; a.y_ts = y_ts; a.y_rs = y_rs;
     a.Wt = Wt;
+    // the CU-tile kernel: Q8_0 tile form, enough tokens to fill the CUs, and
+    // 32-bit byte offsets into the weights and the tiled x
+    const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
+    if (Wt && g.type == LQ_Q8_0 && ntok >= 256 && (size_t)CU_LDS_RESERVE <= max_lds_per_block() &&
+        tiles * mt_nsb(g) * MT_Q80_BLOCK < ((int64_t)1 << 32) && (ntok + 15) / 16 * 16 * ldh * 2 < ((int64_t)1 << 32)) {
+        if (int st = launch_x_to_f16(X, g.cols, g.cols, nullptr, 1, ntok, Xh, ldh, inv, s, 1)) return st;
+        const int64_t nrb = (tiles + CU_RT - 1) / CU_RT, ntb = (ntok + CU_TOKENS - 1) / CU_TOKENS;
+        if (nrb * ntb > ((int64_t)1 << 30)) return fail(LOCALAI_EARG, "matmul: problem too large");
+        const int y_vec = y_rs == 1 && y_ts % 4 == 0 && (uintptr_t)Y % 16 == 0;
+        hipLaunchKernelGGL(gemm_cu_q80_kernel, dim3((unsigned)(nrb * ntb)), dim3(512), CU_LDS_RESERVE, s, a, (int)nrb,
+                           (int)ntb, y_vec);
+        LQ_HIP(hipGetLastError());
+        return LOCALAI_OK;
+    }
+    if (int st = launch_x_to_f16(X, g.cols, g.cols, nullptr, 1, ntok, Xh, ldh, inv, s)) return st;
     if (Wt) {
         const int64_t nwg = ((g.rows + GT_WROWS - 1) / GT_WROWS) * ((ntok + GM_BN - 1) / GM_BN);
         if (nwg > ((int64_t)1 << 30)) return fail(LOCALAI_EARG, "matmul: problem too large");

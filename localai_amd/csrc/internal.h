@@ -64,7 +64,7 @@ int launch_gemm(const lq_geom &g, const uint8_t *packed, const uint8_t *Wt, cons
                 int64_t y_ts, int64_t y_rs, void *ws, int64_t ws_bytes, hipStream_t s);
 
 int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *rows_map, int k, int64_t ntok,
-                    _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s);
+                    _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s, int tiled = 0);
 int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, const uint8_t *Wt_all, int64_t wt_bytes, bool gate_up,
                     const _Float16 *Xh, int64_t ldh, const float *inv, const int32_t *rows_map, int rows_k,
                     float *Y, int64_t y_ts, int64_t inter, const int32_t *tile_e, const int32_t *tile_p0,

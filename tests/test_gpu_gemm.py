@@ -75,6 +75,22 @@ def test_k_lengths(t, nblocks):
     check(got, raw, t, rows, cols, xs)
 
 
+@pytest.mark.parametrize('rows,cols,tokens', [(112, 256, 256), (113, 512, 257), (300, 160, 300), (16, 768, 600),
+                                            (1000, 1024, 512), (1800, 256, 256)])
+def test_q8_0_workgroup_tiles(rows, cols, tokens):
+    """Q8_0 with 256 tokens or more runs on 112-row x 256-token workgroup
+    tiles: ragged row and token edges, K padded up to whole 256-value blocks
+    (cols 160), one and several tiles each way, and both output layouts."""
+    rng = np.random.default_rng(rows + cols + tokens)
+    raw = random_ggml(rng, 8, rows * cols)
+    xs = rng.standard_normal((tokens, cols)).astype(np.float32)
+    got = gpu_matmul(raw, 8, rows, cols, xs)
+    assert got.shape == (tokens, rows)
+    check(got, raw, 8, rows, cols, xs)
+    if rows * tokens <= 300 * 300:
+        np.testing.assert_array_equal(gpu_matmul(raw, 8, rows, cols, xs, rows_major=True), got.T)
+
+
 def test_rows_major_layout_matches_reference_convention():
     """y_layout 1 is the [rows, tokens] buffer of localai_*_matmul (engine/native_quant.cpp:492)."""
     rng = np.random.default_rng(11)
