@@ -472,7 +472,7 @@ def wl_q8_prefill(args, torch, device, synth):
             'data': 'synthetic (seeded GGML Q8_0 bytes, fp32 N(0,1) activations)',
             'config': {'workload': 'q8_0_prefill_gemm_14336x4096x512', 'tokens': tokens, 'flops': flops,
                        'weight_copies_rotated': copies},
-            'roofline': {'bound': 'mfma', 'kernel': 'x_to_f16 + gemm_tile_kernel<Q8_0> (whole call)',
+            'roofline': {'bound': 'mfma', 'kernel': 'x_to_f16 (tiled) + gemm_cu_q80_kernel (whole call)',
                          'achieved': round(tfs, 1), 'peak': MFMA_F16_PEAK_TFS, 'unit': 'TFLOP/s',
                          'frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'traffic': measured_traffic('q8', 'gemm'),
                          'us_per_launch': round(ms * 1e3, 3), 'flops_per_launch': flops},

@@ -305,6 +305,52 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
     route_token<LDS_H, PART>(h, H, rw, rb, E, k, logits, topk_idx, topk_w, tb, tables, blockIdx.x, lds_f);
 }
 
+// Router logits of one token spread over E one-wave workgroups: workgroup e
+// computes logit e exactly as a wave of route_token does (lane l sums
+// elements 256 j + 4 l + c in (j, c) order as exact fp64 products, chunks
+// past H adding exact zero products, then the butterfly), so the logits are
+// equal bit for bit. One workgroup read the whole 16 x 2048 router matrix in
+// about 6.5 us; 16 workgroups read one row each at the same time. Workgroup
+// 0 also clears the counter block of moe_decode1_kernel, which then selects
+// the experts itself. PART: H is not a multiple of 256 * ROUTE_CH.
+template <bool PART>
+__global__ __launch_bounds__(64) void moe_route1_kernel(const float *__restrict__ h, int H,
+                                                        const float *__restrict__ rw,
+                                                        const float *__restrict__ rb, float *__restrict__ logits,
+                                                        uint32_t *__restrict__ sync) {
+    const int lane = threadIdx.x, e = blockIdx.x;
+    if (e == 0)
+        for (int i = lane; i < D1_WORDS; i += 64) sync[i] = 0u;
+    constexpr int CH = ROUTE_CH;
+    const float *row = rw + (int64_t)e * H;
+    double s = 0.0;
+    for (int i0 = 0; i0 < H; i0 += 256 * CH) {
+        float4 wv[CH], hv[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int i = i0 + 256 * j + 4 * lane;
+            const int ic = i < H ? i : H - 4;
+            wv[j] = *reinterpret_cast<const float4 *>(row + ic);
+            hv[j] = *reinterpret_cast<const float4 *>(h + ic);
+        }
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const bool in = !PART || i0 + 256 * j + 4 * lane < H;
+            s = __builtin_fma(in ? (double)hv[j].x : 0.0, (double)wv[j].x, s);
+            s = __builtin_fma(in ? (double)hv[j].y : 0.0, (double)wv[j].y, s);
+            s = __builtin_fma(in ? (double)hv[j].z : 0.0, (double)wv[j].z, s);
+            s = __builtin_fma(in ? (double)hv[j].w : 0.0, (double)wv[j].w, s);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) {
+        float f = (float)s;
+        if (rb) f = f + rb[e];
+        logits[e] = f;
+    }
+}
+
 // Tile of the many-token router: each wave covers RL_T tokens x RL_E
 // experts, a workgroup RL_WT x RL_WE such tiles, i.e. RL_TOK token rows and
 // RL_EXP expert rows.
@@ -808,6 +854,9 @@ __global__ void moe_combine_kernel(const float *__restrict__ ysl, const int32_t 
 // the same sum in either order, so out does not depend on which down tile
 // lands first. 8 waves; SPWG / SPWD super-blocks per wave for gate_up / down.
 // LDS: the mt_pass regions.
+// sel_logits (not null; E <= 64): the router wrote only the logits
+// (moe_route1_kernel) and each workgroup selects the experts itself, before
+// anything else; topk_idx / topk_w then receive the selection.
 // SKIP: skip is the route index that stands for "no expert" (ZAYA's skip
 // route, engine/zaya.py:297-301): its slot adds gate * h instead of an
 // expert output; its gate_up tiles read no weights but still clear and
@@ -821,15 +870,32 @@ __global__ void moe_combine_kernel(const float *__restrict__ ysl, const int32_t 
 template <int TYPE, int SPWG, int SPWD, bool SKIP>
 __global__ __launch_bounds__(512) void moe_decode1_kernel(
     const float *__restrict__ h, int H, int E, int k, const uint8_t *__restrict__ gu_t, int64_t gu_bytes, int nbg,
-    int64_t inter, const uint8_t *__restrict__ dn_t, int64_t dn_bytes, int nbd,
-    const int32_t *__restrict__ topk_idx, const float *__restrict__ topk_w, float *__restrict__ out, MoeTables tb,
-    uint32_t *__restrict__ sync, int skip, int spin, int count) {
+    int64_t inter, const uint8_t *__restrict__ dn_t, int64_t dn_bytes, int nbd, const int32_t *topk_idx,
+    const float *topk_w, float *__restrict__ out, MoeTables tb, uint32_t *__restrict__ sync, int skip, int spin,
+    int count, const float *__restrict__ sel_logits) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int flag;
+    __shared__ int sel_idx[2];
+    __shared__ float sel_w[2];
     const int r = blockIdx.x;
     const int lane = lane_id(), w = wave_id();
     const int gtiles = (int)(inter / MT_ROWS), dtiles = (H + MT_ROWS - 1) / MT_ROWS;
     const int n_gu = k * gtiles;
+    if (sel_logits) {
+        // the experts come from the E logits of moe_route1_kernel: every
+        // workgroup selects them itself (route_select, the router's own
+        // rule); workgroup 0 also writes them out
+        if (w == 0) {
+            route_select<1>(sel_logits, E, k, 0, sel_idx, sel_w, tb, 0);
+            if (r == 0 && lane < k) {
+                const_cast<int32_t *>(topk_idx)[lane] = sel_idx[lane];
+                const_cast<float *>(topk_w)[lane] = sel_w[lane];
+            }
+        }
+        __syncthreads();
+        topk_idx = sel_idx;
+        topk_w = sel_w;
+    }
     if (r < n_gu) {
         const int s = r / gtiles, i = r % gtiles;
         const int n = threadIdx.x;
@@ -1057,13 +1123,13 @@ int moe_error_word(const void *ws, int64_t T, int64_t E, hipStream_t s, uint32_t
 template <int TYPE, int SG, int SD>
 static void launch_decode1_k(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
                              int64_t H, int64_t E, int k, int64_t I, const int32_t *topk_idx, const float *topk_w,
-                             float *out, int skip, hipStream_t s) {
+                             float *out, int skip, hipStream_t s, const float *sel_logits) {
     const size_t a = mt_lds_bytes(TYPE, 8, SG, 1, 2), b = mt_lds_bytes(TYPE, 8, SD, 1, 1);
     const unsigned grid = (unsigned)(k * (I / MT_ROWS) + k * ((H + MT_ROWS - 1) / MT_ROWS));
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(grid), dim3(512), a > b ? a : b, s, h, (int)H, (int)E, k, gu->tiles,
                            gu->tile_bytes, (int)gu->g.nb, I, dn->tiles, dn->tile_bytes, (int)dn->g.nb, topk_idx,
-                           topk_w, out, tb, tb.sync, skip, g_d1_spin.load(), g_d1_count.load());
+                           topk_w, out, tb, tb.sync, skip, g_d1_spin.load(), g_d1_count.load(), sel_logits);
     };
     if (skip >= 0)
         go(moe_decode1_kernel<TYPE, SG, SD, true>);
@@ -1074,11 +1140,11 @@ static void launch_decode1_k(const localai_qmat *gu, const localai_qmat *dn, con
 template <int TYPE>
 static int launch_decode1_t(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
                             int64_t H, int64_t E, int k, int64_t I, const int32_t *topk_idx, const float *topk_w,
-                            float *out, hipStream_t s, int skip = -1) {
+                            float *out, hipStream_t s, int skip = -1, const float *sel_logits = nullptr) {
     const int sg = d1_spw(gu->g.nb), sd = d1_spw(dn->g.nb);
 #define LQ_D1(SG, SD)                                                                                       \
     if (sg == SG && sd == SD)                                                                               \
-        launch_decode1_k<TYPE, SG, SD>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, skip, s);
+        launch_decode1_k<TYPE, SG, SD>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, skip, s, sel_logits);
     LQ_D1(1, 1) else LQ_D1(1, 2) else LQ_D1(1, 4) else LQ_D1(2, 1) else LQ_D1(2, 2) else LQ_D1(2, 4)
     else LQ_D1(4, 1) else LQ_D1(4, 2) else LQ_D1(4, 4)
 #undef LQ_D1
@@ -1092,6 +1158,20 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
     const int64_t I = gu->g.rows / 2;
     MoeTables tb = carve(ws, T, E, k, H, I);
     const int one = T == 1 && tb.tile_w == 0;   // single token: the router writes the tables
+    if (one && k <= 2 && E <= 64 && moe_mfma_ok(gu, dn, h, H, I)) {
+        // one token through the fused expert kernel: the router writes only
+        // the logits and the expert kernel selects
+        if (H % (256 * ROUTE_CH))
+            hipLaunchKernelGGL(moe_route1_kernel<true>, dim3((unsigned)E), dim3(64), 0, s, h, (int)H, rw, rb,
+                               tb.logits, tb.sync);
+        else
+            hipLaunchKernelGGL(moe_route1_kernel<false>, dim3((unsigned)E), dim3(64), 0, s, h, (int)H, rw, rb,
+                               tb.logits, tb.sync);
+        LQ_HIP(hipGetLastError());
+        return gu->g.type == LQ_Q6_K
+                   ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, -1, tb.logits)
+                   : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, -1, tb.logits);
+    }
     if (T >= ROUTE_TILE_TOKENS) {
         const bool part = H % 256 != 0;
         const dim3 lgrid((unsigned)((T + RL_TOK - 1) / RL_TOK), (unsigned)((E + RL_EXP - 1) / RL_EXP));
