@@ -458,7 +458,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 // Workgroup: 4 waves x 2 row tiles (128 weight rows; for gate_up 64 gate rows
 // and the 64 matching up rows) x BN tokens, 128 K values per step.
 
-constexpr int GT_WROWS = 128;          // weight rows per workgroup (dense, down)
+constexpr int GT_WROWS = 128;          // weight rows per workgroup (dense, 4 waves)
+constexpr int GM_MOE_NW = 8;           // waves per workgroup of the expert tile GEMMs
 
 template <int T> struct GtRaw;
 template <> struct GtRaw<LQ_Q4_K> { uint4 qs, hd; };
@@ -617,10 +618,13 @@ __device__ __forceinline__ void gt_half(const GtRaw<T> &w0, const GtRaw<T> &w1, 
     }
 }
 
-template <int T, int BN, int MODE>
-__global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
+// NW waves per workgroup (4 or 8): 32 NW weight rows (gate_up: 16 NW gate and
+// 16 NW up rows) share one staged x tile; 8 waves halve the x bytes each
+// weight byte brings along (the MoE expert tiles)
+template <int T, int BN, int MODE, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_tile_kernel(GemmArgs a) {
     constexpr int NI = BN / 16;            // 16-token MFMA tiles per wave
-    constexpr int XN = BN * 16 / 256;      // 16-byte x chunks per thread and step
+    constexpr int XN = BN * 16 / (64 * NW);   // 16-byte x chunks per thread and step
     constexpr int BB = mt_block_bytes(T);
     __shared__ __attribute__((aligned(16))) _Float16 Xs[2][BN * GM_BK];
     const lq_geom &g = a.g;
@@ -636,7 +640,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
         // xcd * per + id / 8 walks the row blocks of one token tile per XCD
         const int id = blockIdx.x, per = gridDim.x / 8;
         const int L = (id % 8) * per + id / 8;
-        const int nrb = (int)((g.rows + GT_WROWS - 1) / GT_WROWS);
+        const int nrb = (int)((g.rows + 32 * NW - 1) / (32 * NW));
         const int64_t ntt = (a.ntok + BN - 1) / BN;
         if (L >= nrb * ntt) return;
         blk = L % nrb;
@@ -651,27 +655,27 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
         tn = a.tile_n[tile];
     }
     const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS, nsb = mt_nsb(g);
-    // the wave's two row tiles: dense / down 8 blk + 2 wave + j; gate_up
-    // gate tile 4 blk + wave (j = 0) and its up tile inter / 16 + 4 blk + wave
+    // the wave's two row tiles: dense / down 2 NW blk + 2 wave + j; gate_up
+    // gate tile NW blk + wave (j = 0) and its up tile inter / 16 + NW blk + wave
     int64_t t0, t1;
     if constexpr (MODE == GM_MOE_GATE_UP) {
-        t0 = 4 * blk + wave;
-        t1 = a.inter / MT_ROWS + 4 * blk + wave;
+        t0 = NW * blk + wave;
+        t1 = a.inter / MT_ROWS + NW * blk + wave;
     } else {
-        t0 = 8 * blk + 2 * wave;
+        t0 = 2 * NW * blk + 2 * wave;
         t1 = t0 + 1;
     }
     const uint8_t *w0p = Wt + (t0 < tiles ? t0 : tiles - 1) * nsb * BB;
     const uint8_t *w1p = Wt + (t1 < tiles ? t1 : tiles - 1) * nsb * BB;
 
-    // x loader: instruction i of wave w fills tile chunks (4i + w) * 64 + lane,
-    // i.e. token row (4i + w) * 4 + lane / 16, position lane % 16, from the
+    // x loader: instruction i of wave w fills tile chunks (NW i + w) * 64 + lane,
+    // i.e. token row (NW i + w) * 4 + lane / 16, position lane % 16, from the
     // row's chunk (lane % 16) ^ (row % 16); straight from global memory into
     // LDS (no registers), waited for with vmcnt before the step's barrier
     const _Float16 *xsrc[XN];
 #pragma unroll
     for (int i = 0; i < XN; ++i) {
-        const int row = (4 * i + wave) * 4 + (lane >> 4), c = (lane & 15) ^ (row & 15);
+        const int row = (NW * i + wave) * 4 + (lane >> 4), c = (lane & 15) ^ (row & 15);
         xsrc[i] = a.Xh + gemm_xrow(a, p0 + (row < tn ? row : 0)) * a.ldh + 8 * c;
     }
     auto load_x = [&](int buf, int64_t step) {
@@ -679,7 +683,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel(GemmArgs a) {
         for (int i = 0; i < XN; ++i)
             __builtin_amdgcn_global_load_lds(
                 (const void *)(xsrc[i] + step * GM_BK),
-                (__attribute__((address_space(3))) void *)&Xs[buf][(4 * i + wave) * 64 * 8], 16, 0, 0);
+                (__attribute__((address_space(3))) void *)&Xs[buf][(NW * i + wave) * 64 * 8], 16, 0, 0);
     };
 
     lq_f4 acc[NI][2];
@@ -1089,10 +1093,10 @@ static int launch_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t s) {
     return LOCALAI_OK;
 }
 
-template <int MODE, int BN>
+template <int MODE, int BN, int NW = 4>
 static int launch_gemm_tile_t(const GemmArgs &a, dim3 grid, hipStream_t s) {
     switch (a.g.type) {
-#define LQ_GT(TT) case TT: hipLaunchKernelGGL((gemm_tile_kernel<TT, BN, MODE>), grid, dim3(256), 0, s, a); break;
+#define LQ_GT(TT) case TT: hipLaunchKernelGGL((gemm_tile_kernel<TT, BN, MODE, NW>), grid, dim3(64 * NW), 0, s, a); break;
         LQ_GT(LQ_Q4_K) LQ_GT(LQ_Q6_K) LQ_GT(LQ_Q8_0)
 #undef LQ_GT
         default: return fail(LOCALAI_ETYPE, "matmul: no tile form for this GGML type");
@@ -1151,11 +1155,12 @@ int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, const uint8_t *Wt_all
     if (max_tiles <= 0) return LOCALAI_OK;
     if (max_tiles > 65535) return fail(LOCALAI_EARG, "moe: too many token tiles");
     if (Wt_all && (!gate_up || inter % MT_ROWS == 0)) {
+        constexpr int NW = GM_MOE_NW;
         if (gate_up)
-            return launch_gemm_tile_t<GM_MOE_GATE_UP, GM_MOE_BN>(
-                a, dim3((unsigned)((inter + 63) / 64), (unsigned)max_tiles), s);
-        return launch_gemm_tile_t<GM_MOE_DOWN, GM_MOE_BN>(
-            a, dim3((unsigned)((g.rows + GT_WROWS - 1) / GT_WROWS), (unsigned)max_tiles), s);
+            return launch_gemm_tile_t<GM_MOE_GATE_UP, GM_MOE_BN, NW>(
+                a, dim3((unsigned)((inter + 16 * NW - 1) / (16 * NW)), (unsigned)max_tiles), s);
+        return launch_gemm_tile_t<GM_MOE_DOWN, GM_MOE_BN, NW>(
+            a, dim3((unsigned)((g.rows + 32 * NW - 1) / (32 * NW)), (unsigned)max_tiles), s);
     }
     if (gate_up) {
         dim3 grid((unsigned)((inter + GM_BM / 2 - 1) / (GM_BM / 2)), (unsigned)max_tiles);
