@@ -23,6 +23,12 @@ input, weights already resident in HBM, seeded data from localai_amd/synth.py):
   llama3_8b_layer_chain  the same seven matvecs as one launch with the glue
       of the decode step between them (residual adds, both RMSNorms, SiLU*up,
       localai_hip_layer_chain).
+  llama3_8b_attention_decode  decode attention of one token over a 4096-
+      position fp32 KV cache: 32 query heads, 8 kv heads, head_dim 128
+      (localai_hip_attention_decode, the token's k / v row written by the
+      same call).
+  qwen35_delta_net_step  Qwen3.5's gated delta-net step, 32 heads x 128 x
+      128 fp32 state read and written once (localai_hip_delta_net_step).
   hbm_read_floor    the streaming-read kernel (localai_hip_stream_read) over
       the same byte counts: one 33 MB launch, the layer's four dependent
       launches, and the whole layer's 139 MB as one launch -- what a launch
@@ -64,10 +70,11 @@ MFMA_F16_PEAK_TFS = 2500.0      # dense f16/bf16 MFMA
 MALL_BYTES = 256 << 20
 METRIC = 'µs/layer + achieved HBM GB/s (% of peak) for Q4_K/Q6_K matvec & MoE layer'
 WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill',
-             'llama3_8b_layer_chain', 'hbm_read_floor', 'hbm_copy']
+             'llama3_8b_layer_chain', 'llama3_8b_attention_decode', 'qwen35_delta_net_step', 'hbm_read_floor',
+             'hbm_copy']
 # the default run: the headline, then these under "workloads"
 DEFAULT_SUITE = ['q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill', 'llama3_8b_layer_chain',
-                 'hbm_read_floor']
+                 'llama3_8b_attention_decode', 'qwen35_delta_net_step', 'hbm_read_floor']
 
 
 def log(msg):
@@ -717,6 +724,123 @@ def wl_floor(args, torch, device, synth):
             'cpu_baseline': None}
 
 
+def _cpu_port(fn, work, unit, sample):
+    """A NumPy restatement of the reference's own code for a path with no
+    compiled reference kernel here, timed on all physical cores (pinned)."""
+    div = 1e9 if unit == 'GB/s' else 1e12
+    allc = host()['physical_cores']
+    with pinned(allc) as cpus:
+        us, n = time_cpu(fn, min_samples=5, budget_s=6)
+    return {'value': round(work / (us * 1e-6) / div, 5), 'unit': unit, 'cores': allc, 'kind': 'port',
+            'us_per_layer': round(us, 1), 'samples': n,
+            'sample': f'{sample}; median of {n}; {host_note()} ({len(cpus)} for this run)',
+            'host': {k: v for k, v in host().items() if not k.startswith('_')}}
+
+
+def wl_attention(args, torch, device, synth):
+    """Llama-3-8B decode attention at context 4096 (localai_hip_attention_decode):
+    32 query heads over 8 kv heads of head_dim 128, fp32 cache, the token at
+    position 4095 (its k / v row written into the cache by the same call)."""
+    from localai_amd import attention
+    from oracle import attention as oatt
+    nh, nkv, hd, ctx = 32, 8, 128, 4096
+    pos = ctx - 1
+    rng = np.random.default_rng(args.seed)
+    row = nkv * hd * 4
+    nbytes = 2 * pos * row + 2 * row + nh * hd * 4 + 2 * row + nh * hd * 4
+    copies = rotations(2 * ctx * row)
+    kc = rng.standard_normal((ctx, nkv, hd)).astype(np.float32)
+    vc = rng.standard_normal((ctx, nkv, hd)).astype(np.float32)
+    qv = rng.standard_normal(nh * hd).astype(np.float32)
+    kn = rng.standard_normal(nkv * hd).astype(np.float32)
+    vn = rng.standard_normal(nkv * hd).astype(np.float32)
+    log(f'attention: {copies} cache copies ({copies * 2 * ctx * row / 1e6:.0f} MB)')
+    kd, vd = torch.from_numpy(kc).to(device.device()), torch.from_numpy(vc).to(device.device())
+    caches = []
+    for _ in range(copies):
+        c = attention.KVCache(1, nkv, hd, ctx, n_heads=nh)
+        c.k[0].copy_(kd)
+        c.v[0].copy_(vd)
+        caches.append(c)
+    del kd, vd
+    q, k, v = (device.to_device_f32(a) for a in (qv, kn, vn))
+    out = torch.empty(nh * hd, dtype=torch.float32, device=device.device())
+    stream = torch.cuda.Stream()
+    ms = time_steps(torch, [lambda c=c: attention.attention_decode(q, k, v, c, 0, pos, nh, out=out, stream=stream)
+                            for c in caches], stream, args.steps, args.warmup)
+    want, kc2, vc2 = oatt.gqa_decode(qv, kc, vc, pos, nh, nkv, hd, k_new=kn, v_new=vn)
+    got = out.cpu().numpy()
+    err = float(np.abs(got - want).max() / np.abs(want).max())
+    if not err <= 2e-5:
+        raise SystemExit(f'attention output off by {err:.2e} (normwise)')
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_baseline != 'off':
+        cpu = _cpu_port(lambda: oatt.gqa_decode_f32(qv, kc2, vc2, pos, nh, nkv, hd), nbytes, 'GB/s',
+                        'decode attention over 4096 positions, the reference\'s float32 np.repeat + einsum '
+                        '(engine/model.py:223-227) restated')
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+            'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
+            'data': 'synthetic (N(0,1) fp32 cache, q, k, v)',
+            'config': {'workload': 'llama3_8b_attention_decode_ctx4096', 'n_heads': nh, 'n_kv_heads': nkv,
+                       'head_dim': hd, 'positions': ctx, 'algorithmic_bytes': nbytes, 'layer_copies_rotated': copies,
+                       'normwise_vs_oracle': err},
+            'roofline': {'bound': 'hbm', 'kernel': 'attn_chunk_kernel + attn_merge_kernel (whole call)',
+                         'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                         'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': measured_traffic('attention', 'chunk'),
+                         'us_per_launch': round(ms * 1e3, 3), 'bytes_per_launch': nbytes},
+            'cpu_baseline': cpu}
+
+
+def wl_delta_net(args, torch, device, synth):
+    """Qwen3.5 gated delta-net step (localai_hip_delta_net_step) at the
+    default linear-attention shape: 32 value heads, key and value dim 128."""
+    from localai_amd import attention
+    from oracle import attention as oatt
+    heads, kd, vd = 32, 128, 128
+    rng = np.random.default_rng(args.seed)
+    sbytes = heads * kd * vd * 4
+    nbytes = 2 * sbytes + (2 * heads * kd + 2 * heads * vd + 2 * heads) * 4
+    copies = rotations(2 * sbytes)
+    st = (rng.standard_normal((heads, kd, vd)) * 0.1).astype(np.float32)
+    qv = rng.standard_normal((heads, kd)).astype(np.float32)
+    kv = rng.standard_normal((heads, kd)).astype(np.float32)
+    qv /= np.linalg.norm(qv, axis=1, keepdims=True) * np.sqrt(kd)
+    kv /= np.linalg.norm(kv, axis=1, keepdims=True)
+    vv = rng.standard_normal((heads, vd)).astype(np.float32)
+    decay = -rng.uniform(0.001, 0.1, heads).astype(np.float32)
+    beta = rng.uniform(0.1, 0.9, heads).astype(np.float32)
+    states = [device.to_device_f32(st) for _ in range(copies)]
+    q, k, v, dc, bt = (device.to_device_f32(a) for a in (qv, kv, vv, decay, beta))
+    core = torch.empty((heads, vd), dtype=torch.float32, device=device.device())
+    check = device.to_device_f32(st)
+    attention.delta_net_step(check, q, k, v, dc, bt, core=core)
+    S, want = oatt.delta_net_step(st, qv, kv, vv, decay, beta)
+    torch.cuda.synchronize()
+    if not (np.array_equal(core.cpu().numpy(), want) and np.array_equal(check.cpu().numpy(), S)):
+        raise SystemExit('delta net step differs from the float32 reference loop')
+    stream = torch.cuda.Stream()
+    ms = time_steps(torch, [lambda s_=s_: attention.delta_net_step(s_, q, k, v, dc, bt, core=core, stream=stream)
+                            for s_ in states], stream, args.steps, args.warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_baseline != 'off':
+        cpu = _cpu_port(lambda: oatt.delta_net_step(st, qv, kv, vv, decay, beta), nbytes, 'GB/s',
+                        'delta_net_step 32 x 128 x 128, the reference loop (engine/numba_kernels.py:11-45) '
+                        'restated in float32 NumPy (Numba is not installed here)')
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+            'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
+            'data': 'synthetic (state N(0, 0.01), L2-normalised q / k as engine/qwen35.py:206-208)',
+            'config': {'workload': 'qwen35_delta_net_step_h32_k128_v128', 'heads': heads, 'key_dim': kd,
+                       'value_dim': vd, 'algorithmic_bytes': nbytes, 'layer_copies_rotated': copies,
+                       'bit_exact_vs_reference_loop': True},
+            'roofline': {'bound': 'hbm', 'kernel': 'delta_net_kernel<128>', 'achieved': round(gbs, 1),
+                         'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4),
+                         'traffic': measured_traffic('delta_net', 'step'), 'us_per_launch': round(ms * 1e3, 3),
+                         'bytes_per_launch': nbytes},
+            'cpu_baseline': cpu}
+
+
 def ctypes_stream(stream):
     import ctypes
     return ctypes.c_void_p(int(stream.cuda_stream))
@@ -740,7 +864,8 @@ def wl_copy(args, torch, device, synth):
 
 FUNCS = {'llama3_8b_decode_layer': 'wl_layer', 'q4k_matvec': 'wl_q4k', 'q8_0_prefill': 'wl_q8_prefill',
          'zaya_moe_decode': 'wl_zaya', 'qwen3_moe_prefill': 'wl_qwen3', 'llama3_8b_layer_chain': 'wl_chain',
-         'hbm_read_floor': 'wl_floor', 'hbm_copy': 'wl_copy'}
+         'hbm_read_floor': 'wl_floor', 'hbm_copy': 'wl_copy', 'llama3_8b_attention_decode': 'wl_attention',
+         'qwen35_delta_net_step': 'wl_delta_net'}
 
 
 def run_workload(name, args, torch, device, synth):

@@ -165,6 +165,46 @@ int localai_hip_layer_chain(const localai_qmat *const *mats, const float *pre_de
  * counterpart in the reference. */
 int localai_hip_layer_error(void *workspace_dev, void *stream);
 
+/* ---- decode-step attention mixers ---------------------------------------- */
+
+/* Bytes of workspace localai_hip_attention_decode needs for any position
+ * below max_seq (per-chunk partial results of the split-sequence decode); 0
+ * for shapes without a kernel, -1 for invalid sizes. Calls on one workspace
+ * must not overlap. */
+int64_t localai_hip_attention_workspace_size(int64_t max_seq, int n_heads, int n_kv_heads, int head_dim);
+
+/* Grouped-query attention of one decode token over one layer's KV cache,
+ * the attention of engine/model.py:222-227 (`forward`) and, with gate_dev,
+ * Qwen3.5's gated full attention (engine/qwen35.py:158-182):
+ *   K[position], V[position] = k_new, v_new    (skipped when k_new_dev is NULL)
+ *   out_h = softmax_s((q_h . K[s]) / sqrt(head_dim)) V[s],  s in [start, position]
+ *   out_h *= 1 / (1 + exp(-clip(gate_h, -80, 80)))          (gate_dev not NULL)
+ * Query head h reads kv head h / (n_heads / n_kv_heads) (np.repeat order,
+ * engine/model.py:225); start = max(0, position + 1 - window) for window > 0,
+ * else 0 (:223). Caches: fp32 [max_seq, n_kv_heads, head_dim]; q, gate and
+ * out [n_heads, head_dim]; k_new, v_new [n_kv_heads, head_dim]; all 16-byte
+ * aligned. head_dim 64, 128 or 256 with at most 16 / (head_dim / 64) query
+ * heads per kv head; other shapes return LOCALAI_ETYPE. fp32 throughout:
+ * within a few fp32 roundings of the reference's float32 einsum path. */
+int localai_hip_attention_decode(const float *q_dev, const float *k_new_dev, const float *v_new_dev,
+                                 float *k_cache_dev, float *v_cache_dev, int64_t position, int64_t max_seq,
+                                 int n_heads, int n_kv_heads, int head_dim, int64_t window,
+                                 const float *gate_dev, float *out_dev, void *workspace_dev,
+                                 int64_t workspace_bytes, void *stream);
+
+/* delta_net_step (engine/numba_kernels.py:11-45): one gated delta-rule step
+ * of Qwen3.5's linear attention, per head h with S = state[h]
+ * ([key_dim, value_dim] fp32, updated in place):
+ *   S *= exp(decay[h]);  pred = S^T k[h];  delta = (v[h] - pred) * beta[h]
+ *   S += k[h] delta^T;   core[h] = S^T q[h]
+ * q, k [heads, key_dim]; v, core [heads, value_dim]; decay, beta [heads].
+ * Every product and sum is rounded on its own in the reference loop's order,
+ * so state and core equal the reference kernel's bit for bit (exp(decay) is
+ * the correctly rounded fp32 exponential). */
+int localai_hip_delta_net_step(float *state_dev, const float *q_dev, const float *k_dev, const float *v_dev,
+                               const float *decay_dev, const float *beta_dev, float *core_dev, int heads,
+                               int key_dim, int value_dim, void *stream);
+
 /* ---- ZAYA router (engine/zaya.py:274-307) -------------------------------- */
 
 /* Everything of ZAYA's router after the first projection r0 = W_inp h

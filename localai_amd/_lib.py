@@ -53,6 +53,10 @@ SIGNATURES = {
     'localai_hip_layer_chain': (_c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _c_int, _c_int,
                                          _vp, _vp, _vp, _vp, _vp, _c_i64, _vp]),
     'localai_hip_layer_error': (_c_int, [_vp, _vp]),
+    'localai_hip_attention_workspace_size': (_c_i64, [_c_i64, _c_int, _c_int, _c_int]),
+    'localai_hip_attention_decode': (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int,
+                                              _c_i64, _vp, _vp, _vp, _c_i64, _vp]),
+    'localai_hip_delta_net_step': (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     'localai_hip_debug_fused_wait': (_c_int, [_c_int, _c_int]),
     'localai_hip_register_host': (_c_int, [_vp, ctypes.c_size_t]),
     'localai_hip_unregister_host': (_c_int, [_vp]),

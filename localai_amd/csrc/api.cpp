@@ -418,6 +418,44 @@ int localai_hip_layer_error(void *ws, void *stream) {
     return LOCALAI_OK;
 }
 
+int64_t localai_hip_attention_workspace_size(int64_t max_seq, int n_heads, int n_kv, int head_dim) {
+    if (max_seq < 1 || n_heads < 1 || n_kv < 1 || n_heads % n_kv || head_dim < 1) return -1;
+    return (int64_t)attention_workspace_bytes(max_seq, n_heads, n_kv, head_dim);
+}
+
+int localai_hip_attention_decode(const float *q, const float *k_new, const float *v_new, float *kc, float *vc,
+                                 int64_t position, int64_t max_seq, int n_heads, int n_kv, int head_dim,
+                                 int64_t window, const float *gate, float *out, void *ws, int64_t ws_bytes,
+                                 void *stream) {
+    clear_error();
+    if (!q || !kc || !vc || !out) return fail(LOCALAI_EARG, "attention: null pointer");
+    if ((k_new == nullptr) != (v_new == nullptr)) return fail(LOCALAI_EARG, "attention: k_new and v_new go together");
+    if (n_heads < 1 || n_kv < 1 || n_heads % n_kv)
+        return fail(LOCALAI_EARG, "attention: n_heads must be a positive multiple of n_kv_heads");
+    if (head_dim < 1) return fail(LOCALAI_EARG, "attention: head_dim must be >= 1");
+    if (max_seq < 1 || position < 0 || position >= max_seq)
+        return fail(LOCALAI_EARG, "attention: position must be in [0, max_seq)");
+    if (window < 0) return fail(LOCALAI_EARG, "attention: window must be >= 0");
+    auto mis = [](const void *p) { return p && (reinterpret_cast<uintptr_t>(p) & 15) != 0; };
+    if (mis(q) || mis(k_new) || mis(v_new) || mis(kc) || mis(vc) || mis(gate) || mis(out) || mis(ws))
+        return fail(LOCALAI_EARG, "attention: every buffer must be 16-byte aligned");
+    if (int st = ensure_device()) return st;
+    return launch_attention_decode(q, k_new, v_new, kc, vc, position, window, n_heads, n_kv, head_dim, gate, out,
+                                   ws, ws_bytes, (hipStream_t)stream);
+}
+
+int localai_hip_delta_net_step(float *state, const float *q, const float *k, const float *v, const float *decay,
+                               const float *beta, float *core, int heads, int key_dim, int value_dim,
+                               void *stream) {
+    clear_error();
+    if (!state || !q || !k || !v || !decay || !beta || !core) return fail(LOCALAI_EARG, "delta net: null pointer");
+    if (heads < 1 || key_dim < 1 || value_dim < 1 || heads > 65535)
+        return fail(LOCALAI_EARG, "delta net: heads in 1..65535, key_dim and value_dim >= 1");
+    if ((int64_t)heads * key_dim * value_dim > ((int64_t)1 << 40)) return fail(LOCALAI_EARG, "delta net: state too large");
+    if (int st = ensure_device()) return st;
+    return launch_delta_net(state, q, k, v, decay, beta, core, heads, key_dim, value_dim, (hipStream_t)stream);
+}
+
 int64_t localai_hip_moe_workspace_size(int64_t T, int64_t E, int k, int64_t H, int64_t I) {
     if (T < 1 || E < 1 || k < 1 || H < 1 || I < 1) return -1;
     return (int64_t)moe_workspace_bytes(T, E, k, H, I);

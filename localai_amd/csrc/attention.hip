@@ -1,0 +1,469 @@
+// The attention mixers of a decode step on the GPU: grouped-query attention
+// of one token over the KV cache, and the gated delta-net recurrent step of
+// Qwen3.5's linear-attention layers.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "dev_common.h"
+#include "internal.h"
+
+namespace lq {
+
+// ---------------------------------------------------------------- GQA decode
+//
+// Counterpart of the decode step's attention, engine/model.py:222-227, and of
+// Qwen3.5's full attention with its output gate, engine/qwen35.py:158-182.
+// For query head h, with kv head h / G (G = n_heads / n_kv_heads; the
+// np.repeat order of engine/model.py:225) and positions s in [start,
+// position] (start = position + 1 - window under a sliding window, else 0):
+//   score_s = (q_h . K[s]) / sqrt(head_dim),   p = softmax_s(score),
+//   out_h   = sum_s p_s V[s]     (times sigmoid(gate_h) when a gate is given)
+// after row `position` of K and V has been set to the token's k and v
+// (engine/model.py:222). The caches are one layer of the reference's
+// KVCache (engine/model.py:6-9): fp32 [max_seq, n_kv_heads, head_dim].
+//
+// Work layout: a workgroup of 4 waves owns one kv head and 16 RF positions,
+// 4 RF per wave (head_dim = 64 NV). K is read 4 positions per load
+// instruction, 16 lanes (one DPP row) per position, lane c holding 4
+// consecutive floats of each 64-value piece; scores are summed across the row
+// with DPP. V is read one position per instruction, lane l holding values
+// NV l .. NV l + NV - 1, so p (broadcast from its position's row with
+// readlane) weights a lane's own V values and o and l need no sums across
+// lanes. Every K and V value of the chunk is requested up front and serves
+// all G query heads of the kv head. Scores are kept in base-2 units
+// (log2(e) / sqrt(head_dim) folded into the scale) so that p is one
+// v_exp_f32; the chunk maximum crosses the wave's rows with gfx950's
+// v_permlane16_swap / v_permlane32_swap, the waves meet in LDS. Each
+// workgroup stores (o, max, l) per query head and
+// attn_merge_kernel combines the chunks (split-sequence decode); with one
+// chunk the workgroup writes the output itself. (A merge inside the same
+// launch, by the last workgroup of each kv head, raised the chunk kernel's
+// registers from about 110 to 255 per lane and was not faster.)
+
+struct AttnArgs {
+    const float *q, *k_new, *v_new, *gate;
+    float *kc, *vc;
+    int64_t position, start;
+    int n_kv, hd, G;
+    float scale;
+    int nsplit;
+    float *part;       // [n_kv, nsplit, G, hd + 2]: o[hd], max, l
+    float *out;        // [n_heads, hd]
+};
+
+constexpr int ATTN_PIECE = 64;   // floats of a row piece (16 lanes x float4)
+constexpr int ATTN_MC = 64;      // chunks a merge thread requests at once
+
+// 1 / (1 + exp(-clip(x, -80, 80))), engine/qwen35.py:17-19
+__device__ __forceinline__ float sigmoid_ref(float x) {
+    return 1.0f / (1.0f + expf(-fminf(fmaxf(x, -80.0f), 80.0f)));
+}
+
+__device__ __forceinline__ float dot4(const float4 &a, const float4 &b) {
+    return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+__device__ __forceinline__ uint32_t fbits(float v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ float bitsf(uint32_t v) { return __builtin_bit_cast(float, v); }
+
+// sum / max over each row of 16 lanes, the same value on every lane of the
+// row: DPP quad xor 1, quad xor 2, half-row mirror, row mirror
+__device__ __forceinline__ float row16_sum(float v) {
+    v += bitsf(dpp_u32<0xB1>(fbits(v)));
+    v += bitsf(dpp_u32<0x4E>(fbits(v)));
+    v += bitsf(dpp_u32<0x141>(fbits(v)));
+    v += bitsf(dpp_u32<0x140>(fbits(v)));
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, bitsf(dpp_u32<0xB1>(fbits(v))));
+    v = fmaxf(v, bitsf(dpp_u32<0x4E>(fbits(v))));
+    v = fmaxf(v, bitsf(dpp_u32<0x141>(fbits(v))));
+    v = fmaxf(v, bitsf(dpp_u32<0x140>(fbits(v))));
+    return v;
+}
+
+// v with lane l ^ 16 and l ^ 32 combined (the four rows of a wave), the same
+// value on every lane: one swap of rows 0/1 and 2/3, then one of the halves
+__device__ __forceinline__ float rows_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(fbits(v), fbits(v), false, false);
+    v = bitsf(a[0]) + bitsf(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(fbits(v), fbits(v), false, false);
+    return bitsf(b[0]) + bitsf(b[1]);
+}
+__device__ __forceinline__ float rows_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(fbits(v), fbits(v), false, false);
+    v = fmaxf(bitsf(a[0]), bitsf(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(fbits(v), fbits(v), false, false);
+    return fmaxf(bitsf(b[0]), bitsf(b[1]));
+}
+
+template <int N> struct AttnVec;
+template <> struct AttnVec<1> { typedef float T; };
+template <> struct AttnVec<2> { typedef float2 T; };
+template <> struct AttnVec<4> { typedef float4 T; };
+
+// N consecutive floats at p (16 N-byte aligned) into v[0..N)
+template <int N>
+__device__ __forceinline__ void ldv(const float *p, float (&v)[N]) {
+    const typename AttnVec<N>::T t = *reinterpret_cast<const typename AttnVec<N>::T *>(p);
+    __builtin_memcpy(&v[0], &t, sizeof(t));
+}
+template <int N>
+__device__ __forceinline__ void stv(float *p, const float (&v)[N]) {
+    typename AttnVec<N>::T t;
+    __builtin_memcpy(&t, &v[0], sizeof(t));
+    *reinterpret_cast<typename AttnVec<N>::T *>(p) = t;
+}
+
+template <int NV, int GT, int RF>
+__global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
+    constexpr int C = 16 * RF, P = 4 * RF;   // positions per workgroup / per wave
+    __shared__ float red_m[4][GT], red_l[4][GT];
+    __shared__ __attribute__((aligned(16))) float red_o[4][GT * NV * ATTN_PIECE];
+    const int kh = blockIdx.y, split = blockIdx.x;
+    const int wave = wave_id(), lane = lane_id(), pg = lane >> 4, c = lane & 15;
+    const int hd = a.hd, G = a.G;
+    const int64_t row = (int64_t)a.n_kv * hd;
+    const int64_t s0 = a.start + (int64_t)split * C + P * wave;
+
+    float4 qv[GT][NV];
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            qv[g][j] = g < G ? ld4(a.q + (int64_t)(kh * G + g) * hd + ATTN_PIECE * j + 4 * c)
+                             : float4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // every K and V value of the wave's P positions requested before any is
+    // used (the token's own row from k_new / v_new); rows past `position` are
+    // not read. K: row r of 4 positions, 16 lanes per position, lane c holds
+    // values 64 j + 4 c ..; V: position i, lane l holds values NV l .. NV l + NV - 1.
+    float4 kv[RF][NV];
+    bool valid[RF];
+#pragma unroll
+    for (int r = 0; r < RF; ++r) {
+        const int64_t s = s0 + 4 * r + pg;
+        valid[r] = s <= a.position;
+        const bool own = s == a.position && a.k_new;
+        const float *kp = own ? a.k_new + (int64_t)kh * hd : a.kc + (valid[r] ? s : a.start) * row + (int64_t)kh * hd;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) kv[r][j] = ld4(kp + ATTN_PIECE * j + 4 * c);
+    }
+    float vv[P][NV];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const int64_t s = s0 + i;
+        const bool own = s == a.position && a.k_new;
+        const float *vp = own ? a.v_new + (int64_t)kh * hd
+                              : a.vc + (s <= a.position ? s : a.start) * row + (int64_t)kh * hd;
+        ldv<NV>(vp + NV * lane, vv[i]);
+    }
+    // the token's row goes into the cache (no other workgroup reads it)
+    if (a.k_new && a.position >= s0 && a.position < s0 + P) {
+        const int64_t off = a.position * row + (int64_t)kh * hd;
+#pragma unroll
+        for (int r = 0; r < RF; ++r)
+            if (s0 + 4 * r + pg == a.position)
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    *reinterpret_cast<float4 *>(a.kc + off + ATTN_PIECE * j + 4 * c) = kv[r][j];
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+            if (s0 + i == a.position) stv<NV>(a.vc + off + NV * lane, vv[i]);
+    }
+
+    // scores in base-2 units (scale = log2(e) / sqrt(head_dim)): the 16
+    // lanes of a position each hold 4 NV products
+    float sc[RF][GT];
+#pragma unroll
+    for (int r = 0; r < RF; ++r)
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+            float d = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) d += dot4(qv[g][j], kv[r][j]);
+            d = row16_sum(d);
+            sc[r][g] = valid[r] ? d * a.scale : -INFINITY;
+        }
+
+    // chunk maximum per head: the wave's rounds, its four rows, the four waves
+    float mx[GT];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+        float m = sc[0][g];
+#pragma unroll
+        for (int r = 1; r < RF; ++r) m = fmaxf(m, sc[r][g]);
+        m = rows_max(m);
+        if (lane == 0) red_m[wave][g] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+        mx[g] = fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g]));
+
+    // p = 2^(score - max) (masked rows 0), broadcast per position from its
+    // row; l and the p-weighted V rows in each lane's own values
+    float acc[GT][NV], ls[GT];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+        ls[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < NV; ++e) acc[g][e] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < RF; ++r)
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+            const float p = valid[r] ? __builtin_amdgcn_exp2f(sc[r][g] - mx[g]) : 0.0f;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float pb = uniform_f(p, 16 * q4);
+                ls[g] += pb;
+#pragma unroll
+                for (int e = 0; e < NV; ++e) acc[g][e] += pb * vv[4 * r + q4][e];
+            }
+        }
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+        if (lane == 0) red_l[wave][g] = ls[g];
+        stv<NV>(&red_o[wave][g * NV * ATTN_PIECE + NV * lane], acc[g]);
+    }
+    __syncthreads();
+
+    // the workgroup's sums over its 4 waves; thread i handles values i, i + 256, ...
+    const int nval = G * hd;
+    const int64_t rec = hd + 2;
+    float *pw = a.part + ((int64_t)kh * a.nsplit + split) * G * rec;
+    for (int i = threadIdx.x; i < nval; i += 256) {
+        const int g = i / hd, d = i % hd;
+        const int o = g * NV * ATTN_PIECE + d;
+        const float ov = (red_o[0][o] + red_o[1][o]) + (red_o[2][o] + red_o[3][o]);
+        const float lv = (red_l[0][g] + red_l[1][g]) + (red_l[2][g] + red_l[3][g]);
+        if (a.nsplit == 1) {
+            const int64_t h = (int64_t)kh * G + g;
+            float y = ov / lv;
+            if (a.gate) y *= sigmoid_ref(a.gate[h * hd + d]);
+            a.out[h * hd + d] = y;
+        } else {
+            pw[g * rec + d] = ov;
+            if (d == 0) {
+                pw[g * rec + hd] = fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g]));
+                pw[g * rec + hd + 1] = lv;
+            }
+        }
+    }
+}
+
+// Merge of the chunks: workgroup (h, b) writes values 64 b .. 64 b + 63 of
+// query head h. With M the largest chunk maximum (base-2 units), out =
+// sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i, taken over 64 chunks at a
+// time with a running maximum: lane i requests chunk i's (max, l) and every
+// lane its output's 64 chunk values at once; the weights go through LDS.
+__global__ __launch_bounds__(64) void attn_merge_kernel(AttnArgs a) {
+    __shared__ float w_s[ATTN_MC];
+    const int h = blockIdx.x, kh = h / a.G, g = h % a.G, hd = a.hd, ns = a.nsplit, lane = lane_id();
+    const int d = 64 * blockIdx.y + lane;
+    const bool in = d < hd;
+    const int64_t rec = hd + 2, stride = (int64_t)a.G * rec;
+    const float *base = a.part + (int64_t)kh * ns * stride + g * rec;
+    float M = -INFINITY, o = 0.0f, l = 0.0f;
+    for (int c0 = 0; c0 < ns; c0 += ATTN_MC) {
+        const int cn = ns - c0 < ATTN_MC ? ns - c0 : ATTN_MC;
+        const float *pc = base + (int64_t)c0 * stride;
+        const int li = lane < cn ? lane : 0;
+        const float mi = pc[li * stride + hd], lv = pc[li * stride + hd + 1];
+        float v[ATTN_MC];
+#pragma unroll
+        for (int i = 0; i < ATTN_MC; ++i) v[i] = pc[(i < cn ? i : 0) * stride + (in ? d : 0)];
+        const float mc = rows_max(row16_max(lane < cn ? mi : -INFINITY));
+        const float Mn = fmaxf(M, mc);
+        const float rescale = __builtin_amdgcn_exp2f(M - Mn);   // 0 on the first pass (M = -inf)
+        const float w = lane < cn ? __builtin_amdgcn_exp2f(mi - Mn) : 0.0f;
+        w_s[lane] = w;
+        __syncthreads();
+        float oc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < ATTN_MC; ++i) oc += w_s[i] * v[i];
+        o = o * rescale + oc;
+        l = l * rescale + rows_sum(row16_sum(w * lv));
+        M = Mn;
+        __syncthreads();
+    }
+    if (in) {
+        float y = o / l;
+        if (a.gate) y *= sigmoid_ref(a.gate[(int64_t)h * hd + d]);
+        a.out[(int64_t)h * hd + d] = y;
+    }
+}
+
+// rounds of 4 positions per wave: all of a chunk's K / V stays in registers
+// next to the query and accumulator values (GT NV <= 16)
+constexpr int attn_rounds(int nv, int gt) { return gt * nv <= 8 ? 4 : 2; }
+
+static int attn_shape(int hd, int G, int *nv, int *gt) {
+    if (hd % ATTN_PIECE || hd / ATTN_PIECE < 1 || hd / ATTN_PIECE > 4 || hd / ATTN_PIECE == 3) return 1;
+    *nv = hd / ATTN_PIECE;
+    *gt = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 0;
+    if (!*gt || *gt * *nv > 16) return 1;
+    return 0;
+}
+
+size_t attention_workspace_bytes(int64_t max_seq, int n_heads, int n_kv, int hd) {
+    const int G = n_heads / n_kv;
+    int nv, gt;
+    if (attn_shape(hd, G, &nv, &gt)) return 0;
+    const int C = 16 * attn_rounds(nv, gt);
+    const int64_t nsplit = (max_seq + C - 1) / C;
+    return (size_t)((int64_t)n_kv * nsplit * G * (hd + 2) * 4);
+}
+
+int launch_attention_decode(const float *q, const float *k_new, const float *v_new, float *kc, float *vc,
+                            int64_t position, int64_t window, int n_heads, int n_kv, int hd, const float *gate,
+                            float *out, void *ws, int64_t ws_bytes, hipStream_t s) {
+    AttnArgs a{};
+    a.G = n_heads / n_kv;
+    int nv, gt;
+    if (attn_shape(hd, a.G, &nv, &gt))
+        return fail(LOCALAI_ETYPE, "attention: head_dim 64, 128 or 256 and at most 16 / (head_dim / 64) query "
+                                   "heads per kv head");
+    const int C = 16 * attn_rounds(nv, gt);
+    a.q = q; a.k_new = k_new; a.v_new = v_new; a.gate = gate; a.kc = kc; a.vc = vc;
+    a.position = position;
+    a.start = window > 0 && position + 1 - window > 0 ? position + 1 - window : 0;
+    a.n_kv = n_kv; a.hd = hd;
+    a.scale = (float)(1.4426950408889634 / std::sqrt((double)hd));   // log2(e) / sqrt(head_dim)
+    const int64_t len = position - a.start + 1, nsplit = (len + C - 1) / C;
+    if (nsplit > 65535) return fail(LOCALAI_EARG, "attention: too many positions");
+    a.nsplit = (int)nsplit;
+    a.part = (float *)ws;
+    a.out = out;
+    if (nsplit > 1 && (!ws || ws_bytes < (int64_t)n_kv * nsplit * a.G * (hd + 2) * 4))
+        return fail(LOCALAI_EARG, "attention: workspace too small");
+    const dim3 grid((unsigned)nsplit, (unsigned)n_kv);
+#define LQ_ATT(NV, GT)                                                                                        \
+    if (nv == NV && gt == GT) {                                                                               \
+        hipLaunchKernelGGL((attn_chunk_kernel<NV, GT, attn_rounds(NV, GT)>), grid, dim3(256), 0, s, a);       \
+    }
+    LQ_ATT(1, 1) else LQ_ATT(1, 2) else LQ_ATT(1, 4) else LQ_ATT(1, 8)
+    else LQ_ATT(2, 1) else LQ_ATT(2, 2) else LQ_ATT(2, 4) else LQ_ATT(2, 8)
+    else LQ_ATT(4, 1) else LQ_ATT(4, 2) else LQ_ATT(4, 4)
+#undef LQ_ATT
+    LQ_HIP(hipGetLastError());
+    if (nsplit > 1) {
+        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)n_heads, (unsigned)((hd + 63) / 64)), dim3(64), 0, s, a);
+        LQ_HIP(hipGetLastError());
+    }
+    return LOCALAI_OK;
+}
+
+// ---------------------------------------------------------------- delta net
+//
+// Counterpart of delta_net_step (engine/numba_kernels.py:11-45), the gated
+// delta-rule recurrent step of Qwen3.5's linear attention
+// (engine/qwen35.py:224-252). Per head h, with state S [key_dim, value_dim]:
+//   S *= exp(decay[h]);  pred = S^T k;  delta = (v - pred) * beta[h]
+//   S += k delta^T;      core = S^T q
+// The lane that owns column vi of S runs the reference loop's exact
+// float32 operations in its order: each product and each sum rounded on its
+// own (no fused multiply-add), ki ascending, so state and core equal the
+// reference kernel's bit for bit. exp(decay) is the fp64 exponential rounded
+// once to fp32.
+//
+// delta_net_kernel (key_dim == KF, 64 or 128): a workgroup of 4 waves owns 64
+// value columns of one head. The waves copy the [KF, 64] slab into LDS
+// together (every load in flight at once), wave 0 runs the two ordered chains
+// (lane = column; the scaled column in registers between them) and writes the
+// updated slab to LDS, and the 4 waves store it. delta_net_any_kernel: any
+// key_dim, one wave per 64 columns straight from global memory.
+template <int KF>
+__global__ __launch_bounds__(256) void delta_net_kernel(float *__restrict__ state, const float *__restrict__ q,
+                                                        const float *__restrict__ k, const float *__restrict__ v,
+                                                        const float *__restrict__ decay,
+                                                        const float *__restrict__ beta, float *__restrict__ core,
+                                                        int VD) {
+#pragma clang fp contract(off)
+    __shared__ float S_s[KF][64];
+    __shared__ float k_s[KF], q_s[KF];
+    const int h = blockIdx.y, c0 = blockIdx.x * 64, tid = (int)threadIdx.x, col = tid & 63, w = tid >> 6;
+    const bool in = c0 + col < VD;
+    float *hs = state + (int64_t)h * KF * VD + c0 + (in ? col : 0);
+    // every load requested before any is used (columns past VD read column c0)
+    float t[KF / 4];
+#pragma unroll
+    for (int i = 0; i < KF / 4; ++i) t[i] = hs[(int64_t)(w + 4 * i) * VD];
+#pragma unroll
+    for (int i = 0; i < KF / 4; ++i) S_s[w + 4 * i][col] = in ? t[i] : 0.0f;
+    if (tid < KF) {
+        k_s[tid] = k[(int64_t)h * KF + tid];
+        q_s[tid] = q[(int64_t)h * KF + tid];
+    }
+    __syncthreads();
+    if (w == 0) {
+        const float factor = (float)exp((double)decay[h]);
+        float keep[KF], pred = 0.0f, acc = 0.0f;
+#pragma unroll
+        for (int ki = 0; ki < KF; ++ki) {
+            keep[ki] = S_s[ki][col] * factor;
+            pred = pred + keep[ki] * k_s[ki];
+        }
+        const float delta = in ? (v[(int64_t)h * VD + c0 + col] - pred) * beta[h] : 0.0f;
+#pragma unroll
+        for (int ki = 0; ki < KF; ++ki) {
+            const float val = keep[ki] + k_s[ki] * delta;
+            S_s[ki][col] = val;
+            acc = acc + val * q_s[ki];
+        }
+        if (in) core[(int64_t)h * VD + c0 + col] = acc;
+    }
+    __syncthreads();
+    if (in)
+#pragma unroll
+        for (int i = 0; i < KF / 4; ++i) {
+            const int ki = w + 4 * i;
+            hs[(int64_t)ki * VD] = S_s[ki][col];
+        }
+}
+
+__global__ __launch_bounds__(64) void delta_net_any_kernel(float *__restrict__ state, const float *__restrict__ q,
+                                                           const float *__restrict__ k, const float *__restrict__ v,
+                                                           const float *__restrict__ decay,
+                                                           const float *__restrict__ beta, float *__restrict__ core,
+                                                           int KD, int VD) {
+#pragma clang fp contract(off)
+    const int h = blockIdx.y, vi = blockIdx.x * 64 + (int)threadIdx.x;
+    if (vi >= VD) return;
+    const float factor = (float)exp((double)decay[h]);
+    float *col = state + (int64_t)h * KD * VD + vi;
+    const float *kh = k + (int64_t)h * KD, *qh = q + (int64_t)h * KD;
+    float pred = 0.0f, acc = 0.0f;
+    for (int ki = 0; ki < KD; ++ki) {
+        const float val = col[(int64_t)ki * VD] * factor;
+        col[(int64_t)ki * VD] = val;
+        pred = pred + val * kh[ki];
+    }
+    const float delta = (v[(int64_t)h * VD + vi] - pred) * beta[h];
+    for (int ki = 0; ki < KD; ++ki) {
+        const float val = col[(int64_t)ki * VD] + kh[ki] * delta;
+        col[(int64_t)ki * VD] = val;
+        acc = acc + val * qh[ki];
+    }
+    core[(int64_t)h * VD + vi] = acc;
+}
+
+int launch_delta_net(float *state, const float *q, const float *k, const float *v, const float *decay,
+                     const float *beta, float *core, int heads, int KD, int VD, hipStream_t s) {
+    const dim3 grid((unsigned)((VD + 63) / 64), (unsigned)heads);
+    if (KD == 128)
+        hipLaunchKernelGGL(delta_net_kernel<128>, grid, dim3(256), 0, s, state, q, k, v, decay, beta, core, VD);
+    else if (KD == 64)
+        hipLaunchKernelGGL(delta_net_kernel<64>, grid, dim3(256), 0, s, state, q, k, v, decay, beta, core, VD);
+    else
+        hipLaunchKernelGGL(delta_net_any_kernel, grid, dim3(64), 0, s, state, q, k, v, decay, beta, core, KD, VD);
+    LQ_HIP(hipGetLastError());
+    return LOCALAI_OK;
+}
+
+}  // namespace lq

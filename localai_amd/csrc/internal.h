@@ -100,4 +100,12 @@ int launch_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, const
                         const int32_t *topk_idx, const float *topk_w, int skip, float *out, void *ws,
                         hipStream_t s);
 
+// decode-step attention mixers (attention.hip)
+size_t attention_workspace_bytes(int64_t max_seq, int n_heads, int n_kv, int hd);
+int launch_attention_decode(const float *q, const float *k_new, const float *v_new, float *kc, float *vc,
+                            int64_t position, int64_t window, int n_heads, int n_kv, int hd, const float *gate,
+                            float *out, void *ws, int64_t ws_bytes, hipStream_t s);
+int launch_delta_net(float *state, const float *q, const float *k, const float *v, const float *decay,
+                     const float *beta, float *core, int heads, int KD, int VD, hipStream_t s);
+
 }  // namespace lq

@@ -63,6 +63,20 @@ def test_argument_errors_before_device_use():
                                        None, None, 17, None, None, None, None, None, None) == 1
     assert lib.localai_hip_zaya_scale(None, None, 4, None, None, None) == 1
     assert lib.localai_hip_moe_experts1(None, 64, None, None, 1, None, None, -1, None, None, 0, None) == 1
+    # attention: null buffers, heads not a multiple of kv heads, position past
+    # the cache, k without v, misaligned buffers
+    att = lambda q, kn, vn, pos, nh, nkv, hd: lib.localai_hip_attention_decode(
+        q, kn, vn, one, one, pos, 16, nh, nkv, hd, 0, None, one, None, 0, None)
+    assert att(None, None, None, 0, 8, 2, 128) == 1
+    assert att(one, None, None, 0, 6, 4, 128) == 1
+    assert att(one, None, None, 16, 8, 2, 128) == 1
+    assert att(one, one, None, 0, 8, 2, 128) == 1
+    assert att(ctypes.c_void_p(20), None, None, 0, 8, 2, 128) == 1
+    assert lib.localai_hip_attention_workspace_size(4096, 32, 8, 128) == 8 * 64 * 4 * 130 * 4
+    assert lib.localai_hip_attention_workspace_size(4096, 32, 8, 96) == 0
+    assert lib.localai_hip_attention_workspace_size(4096, 6, 4, 128) == -1
+    assert lib.localai_hip_delta_net_step(*([None] * 7), 32, 128, 128, None) == 1
+    assert lib.localai_hip_delta_net_step(*([one] * 7), 0, 128, 128, None) == 1
     with pytest.raises(_lib.HipError):
         _lib.check(lib.localai_hip_dequant(99, None, 0, None, None))
 
