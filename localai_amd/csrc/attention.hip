@@ -53,7 +53,7 @@ struct AttnArgs {
 };
 
 constexpr int ATTN_PIECE = 64;   // floats of a row piece (16 lanes x float4)
-constexpr int ATTN_MC = 64;      // chunks a merge thread requests at once
+constexpr int ATTN_MC = 32;      // chunks a merge lane requests at once
 
 // 1 / (1 + exp(-clip(x, -80, 80))), engine/qwen35.py:17-19
 __device__ __forceinline__ float sigmoid_ref(float x) {
@@ -134,8 +134,9 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
     for (int g = 0; g < GT; ++g)
 #pragma unroll
         for (int j = 0; j < NV; ++j)
-            qv[g][j] = g < G ? ld4(a.q + (int64_t)(kh * G + g) * hd + ATTN_PIECE * j + 4 * c)
-                             : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            // heads past G (kernel sized for more) repeat head G - 1; their
+            // results are never stored
+            qv[g][j] = ld4(a.q + (int64_t)(kh * G + (g < G ? g : G - 1)) * hd + ATTN_PIECE * j + 4 * c);
 
     // every K and V value of the wave's P positions requested before any is
     // used (the token's own row from k_new / v_new); rows past `position` are
@@ -161,20 +162,6 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
                               : a.vc + (s <= a.position ? s : a.start) * row + (int64_t)kh * hd;
         ldv<NV>(vp + NV * lane, vv[i]);
     }
-    // the token's row goes into the cache (no other workgroup reads it)
-    if (a.k_new && a.position >= s0 && a.position < s0 + P) {
-        const int64_t off = a.position * row + (int64_t)kh * hd;
-#pragma unroll
-        for (int r = 0; r < RF; ++r)
-            if (s0 + 4 * r + pg == a.position)
-#pragma unroll
-                for (int j = 0; j < NV; ++j)
-                    *reinterpret_cast<float4 *>(a.kc + off + ATTN_PIECE * j + 4 * c) = kv[r][j];
-#pragma unroll
-        for (int i = 0; i < P; ++i)
-            if (s0 + i == a.position) stv<NV>(a.vc + off + NV * lane, vv[i]);
-    }
-
     // scores in base-2 units (scale = log2(e) / sqrt(head_dim)): the 16
     // lanes of a position each hold 4 NV products
     float sc[RF][GT];
@@ -218,20 +205,36 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
 #pragma unroll
         for (int g = 0; g < GT; ++g) {
             const float p = valid[r] ? __builtin_amdgcn_exp2f(sc[r][g] - mx[g]) : 0.0f;
+            ls[g] += p;     // the lane's own row; the rows are summed below
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
                 const float pb = uniform_f(p, 16 * q4);
-                ls[g] += pb;
 #pragma unroll
                 for (int e = 0; e < NV; ++e) acc[g][e] += pb * vv[4 * r + q4][e];
             }
         }
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
-        if (lane == 0) red_l[wave][g] = ls[g];
+        const float l = rows_sum(ls[g]);
+        if (lane == 0) red_l[wave][g] = l;
         stv<NV>(&red_o[wave][g * NV * ATTN_PIECE + NV * lane], acc[g]);
     }
     __syncthreads();
+
+    // the token's row goes into the cache (no other workgroup reads it);
+    // last, so that no wait for its values comes before the arithmetic
+    if (a.k_new && a.position >= s0 && a.position < s0 + P) {
+        const int64_t off = a.position * row + (int64_t)kh * hd;
+#pragma unroll
+        for (int r = 0; r < RF; ++r)
+            if (s0 + 4 * r + pg == a.position)
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    *reinterpret_cast<float4 *>(a.kc + off + ATTN_PIECE * j + 4 * c) = kv[r][j];
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+            if (s0 + i == a.position) stv<NV>(a.vc + off + NV * lane, vv[i]);
+    }
 
     // the workgroup's sums over its 4 waves; thread i handles values i, i + 256, ...
     const int nval = G * hd;
@@ -259,41 +262,55 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
 
 // Merge of the chunks: workgroup (h, b) writes values 64 b .. 64 b + 63 of
 // query head h. With M the largest chunk maximum (base-2 units), out =
-// sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i, taken over 64 chunks at a
-// time with a running maximum: lane i requests chunk i's (max, l) and every
-// lane its output's 64 chunk values at once; the weights go through LDS.
-__global__ __launch_bounds__(64) void attn_merge_kernel(AttnArgs a) {
-    __shared__ float w_s[ATTN_MC];
-    const int h = blockIdx.x, kh = h / a.G, g = h % a.G, hd = a.hd, ns = a.nsplit, lane = lane_id();
+// sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i. The workgroup's waves split
+// the chunks ATTN_MC at a time (wave w: chunks 32 w, 32 (w + nw), ...), so a
+// lane requests its ATTN_MC chunk values and the chunks' (max, l) in one round;
+// each wave keeps a running maximum, its weights reach the lanes by readlane,
+// and the waves meet in LDS.
+__global__ __launch_bounds__(512) void attn_merge_kernel(AttnArgs a) {
+    __shared__ float red_m[8], red_l[8], red_o[8][64];
+    const int h = blockIdx.x, kh = h / a.G, g = h % a.G, hd = a.hd, ns = a.nsplit;
+    const int lane = lane_id(), wave = wave_id(), nw = (int)(blockDim.x >> 6);
     const int d = 64 * blockIdx.y + lane;
-    const bool in = d < hd;
     const int64_t rec = hd + 2, stride = (int64_t)a.G * rec;
     const float *base = a.part + (int64_t)kh * ns * stride + g * rec;
     float M = -INFINITY, o = 0.0f, l = 0.0f;
-    for (int c0 = 0; c0 < ns; c0 += ATTN_MC) {
+    for (int c0 = ATTN_MC * wave; c0 < ns; c0 += ATTN_MC * nw) {
         const int cn = ns - c0 < ATTN_MC ? ns - c0 : ATTN_MC;
         const float *pc = base + (int64_t)c0 * stride;
         const int li = lane < cn ? lane : 0;
-        const float mi = pc[li * stride + hd], lv = pc[li * stride + hd + 1];
+        const float mi = lane < cn ? pc[li * stride + hd] : -INFINITY;
+        const float lv = lane < cn ? pc[li * stride + hd + 1] : 0.0f;
         float v[ATTN_MC];
 #pragma unroll
-        for (int i = 0; i < ATTN_MC; ++i) v[i] = pc[(i < cn ? i : 0) * stride + (in ? d : 0)];
-        const float mc = rows_max(row16_max(lane < cn ? mi : -INFINITY));
-        const float Mn = fmaxf(M, mc);
-        const float rescale = __builtin_amdgcn_exp2f(M - Mn);   // 0 on the first pass (M = -inf)
+        for (int i = 0; i < ATTN_MC; ++i) v[i] = pc[(i < cn ? i : 0) * stride + d];
+        const float Mn = fmaxf(M, rows_max(row16_max(mi)));
+        const float f = __builtin_amdgcn_exp2f(M - Mn);   // 0 on the first pass (M = -inf)
         const float w = lane < cn ? __builtin_amdgcn_exp2f(mi - Mn) : 0.0f;
-        w_s[lane] = w;
-        __syncthreads();
         float oc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < ATTN_MC; ++i) oc += w_s[i] * v[i];
-        o = o * rescale + oc;
-        l = l * rescale + rows_sum(row16_sum(w * lv));
+        for (int i = 0; i < ATTN_MC; ++i) oc += uniform_f(w, i) * v[i];
+        o = o * f + oc;
+        l = l * f + rows_sum(row16_sum(w * lv));
         M = Mn;
-        __syncthreads();
     }
-    if (in) {
-        float y = o / l;
+    red_o[wave][lane] = o;
+    if (lane == 0) {
+        red_m[wave] = M;
+        red_l[wave] = l;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float Mw = -INFINITY;
+        for (int w = 0; w < nw; ++w) Mw = fmaxf(Mw, red_m[w]);
+        float ov = 0.0f, lt = 0.0f;
+        for (int w = 0; w < nw; ++w) {
+            // a wave without chunks holds m = -inf and zero sums
+            const float f = red_m[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w] - Mw);
+            ov += f * red_o[w][lane];
+            lt += f * red_l[w];
+        }
+        float y = ov / lt;
         if (a.gate) y *= sigmoid_ref(a.gate[(int64_t)h * hd + d]);
         a.out[(int64_t)h * hd + d] = y;
     }
@@ -353,7 +370,9 @@ int launch_attention_decode(const float *q, const float *k_new, const float *v_n
 #undef LQ_ATT
     LQ_HIP(hipGetLastError());
     if (nsplit > 1) {
-        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)n_heads, (unsigned)((hd + 63) / 64)), dim3(64), 0, s, a);
+        const int nw = (int)((nsplit + ATTN_MC - 1) / ATTN_MC < 8 ? (nsplit + ATTN_MC - 1) / ATTN_MC : 8);
+        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)n_heads, (unsigned)((hd + 63) / 64)), dim3(64 * nw), 0,
+                           s, a);
         LQ_HIP(hipGetLastError());
     }
     return LOCALAI_OK;
