@@ -731,12 +731,13 @@ __global__ __launch_bounds__(256) void moe_grouped_kernel(const uint8_t *__restr
 // mfma_core.h). A workgroup loads its weight tiles once and walks the tokens
 // routed to its expert, restaging x per token.
 
-// gate_up: workgroup (i, slot) = gate tile i (rows 16i ..) and up tile
-// inter / 16 + i of the slot's expert; act[p, 16i + n] = silu(g) * u
-// (engine/zaya.py:303-306) for every perm position p of the expert. With
-// zero != null the slot-0 workgroups also clear zero[0 .. nzero) (the output
-// that the down kernel then adds onto).
-template <int TYPE, int SPW, int MAXT>
+// gate_up: workgroup (i, slot) = gate tiles RT i .. RT i + RT - 1 (rows 16
+// RT i ..) and the matching up tiles inter / 16 + RT i + t of the slot's
+// expert; act[p, 16 (RT i + t) + n] = silu(g) * u (engine/zaya.py:303-306)
+// for every perm position p of the expert. With zero != null the slot-0
+// workgroups also clear zero[0 .. nzero) (the output that the down kernel
+// then adds onto).
+template <int TYPE, int SPW, int MAXT, int RT = 1>
 __global__ __launch_bounds__(MAXT) void moe_mfma_gate_up(const uint8_t *__restrict__ Wt, int64_t mat_bytes, int nb,
                                                          int64_t inter, MoeTables tb, const float *__restrict__ h,
                                                          int64_t H, int k, float *__restrict__ zero,
@@ -752,9 +753,14 @@ __global__ __launch_bounds__(MAXT) void moe_mfma_gate_up(const uint8_t *__restri
     const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
     const int64_t i = blockIdx.x, tile_bytes = (int64_t)nb * mt_block_bytes(TYPE);
     const uint8_t *We = Wt + (int64_t)e * mat_bytes;
-    MtW<TYPE> w[2][SPW];
-    mt_load_tile<TYPE, SPW>(w[0], We + i * tile_bytes, nb, sb0, nsb, lane);
-    mt_load_tile<TYPE, SPW>(w[1], We + (inter / MT_ROWS + i) * tile_bytes, nb, sb0, nsb, lane);
+    const int64_t gtiles = inter / MT_ROWS;
+    MtW<TYPE> w[2 * RT][SPW];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        const int64_t gt = RT * i + t < gtiles ? RT * i + t : gtiles - 1;
+        mt_load_tile<TYPE, SPW>(w[t], We + gt * tile_bytes, nb, sb0, nsb, lane);
+        mt_load_tile<TYPE, SPW>(w[RT + t], We + (gtiles + gt) * tile_bytes, nb, sb0, nsb, lane);
+    }
     __builtin_amdgcn_sched_barrier(0);
     // the expert's tokens; each next token's row is requested before the
     // current token's arithmetic
@@ -768,9 +774,10 @@ __global__ __launch_bounds__(MAXT) void moe_mfma_gate_up(const uint8_t *__restri
         float4 xn[1][SPW];
         if (j + 1 < n) mt_load_x<SPW>(xn[0], h + (int64_t)(tb.perm[p + 1] / k) * H, nb, sb0, lane);
         float *fin;
-        mt_pass<TYPE, SPW, 2, 1>(w, xv, nsb, smem, fin);
+        mt_pass<TYPE, SPW, 2 * RT, 1>(w, xv, nsb, smem, fin);
         const int r = threadIdx.x;
-        if (r < MT_ROWS) tb.act[(int64_t)p * inter + i * MT_ROWS + r] = silu(fin[r]) * fin[MT_ROWS + r];
+        if (r < RT * MT_ROWS && RT * i * MT_ROWS + r < inter)
+            tb.act[(int64_t)p * inter + RT * i * MT_ROWS + r] = silu(fin[r]) * fin[RT * MT_ROWS + r];
         if (j + 1 < n) {
 #pragma unroll
             for (int kk = 0; kk < SPW; ++kk) xv[0][kk] = xn[0][kk];
@@ -778,12 +785,13 @@ __global__ __launch_bounds__(MAXT) void moe_mfma_gate_up(const uint8_t *__restri
     }
 }
 
-// down: workgroup (i, slot) = hidden tile i of the slot's expert;
-// ysl[p, 16i + n] for every perm position p of the expert, or with out !=
-// null (k <= 2, out cleared by gate_up) out[t, 16i + n] += gate * y for the
+// down: workgroup (i, slot) = hidden tiles RT i .. RT i + RT - 1 of the
+// slot's expert; ysl[p, r] for those rows r and every perm position p of the
+// expert, or with out != null (k <= 2, out cleared by gate_up) out[t, r] +=
+// gate * y for the
 // token t of position p: two additions onto zero give the same sum in either
 // order, so the combine is folded in without changing the result's bits
-template <int TYPE, int SPW, int MAXT>
+template <int TYPE, int SPW, int MAXT, int RT = 1>
 __global__ __launch_bounds__(MAXT) void moe_mfma_down(const uint8_t *__restrict__ Wt, int64_t mat_bytes, int nb,
                                                       int64_t hidden, MoeTables tb, int64_t inter,
                                                       float *__restrict__ out, const float *__restrict__ topk_w,
@@ -797,22 +805,29 @@ __global__ __launch_bounds__(MAXT) void moe_mfma_down(const uint8_t *__restrict_
     const int64_t i = blockIdx.x;
     float4 xv[1][SPW];
     mt_load_x<SPW>(xv[0], tb.act + (int64_t)base * inter, nb, sb0, lane);
-    MtW<TYPE> w[1][SPW];
-    mt_load_tile<TYPE, SPW>(w[0], Wt + (int64_t)e * mat_bytes + i * nb * mt_block_bytes(TYPE), nb, sb0, nsb, lane);
+    const int64_t tiles = (hidden + MT_ROWS - 1) / MT_ROWS;
+    MtW<TYPE> w[RT][SPW];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        const int64_t ti = RT * i + t < tiles ? RT * i + t : tiles - 1;
+        mt_load_tile<TYPE, SPW>(w[t], Wt + (int64_t)e * mat_bytes + ti * nb * mt_block_bytes(TYPE), nb, sb0, nsb,
+                                lane);
+    }
     __builtin_amdgcn_sched_barrier(0);
     for (int j = 0; j < n; ++j) {
         const int p = base + j;
         float4 xn[1][SPW];
         if (j + 1 < n) mt_load_x<SPW>(xn[0], tb.act + (int64_t)(p + 1) * inter, nb, sb0, lane);
         float *fin;
-        mt_pass<TYPE, SPW, 1, 1>(w, xv, nsb, smem, fin);
+        mt_pass<TYPE, SPW, RT, 1>(w, xv, nsb, smem, fin);
         const int r = threadIdx.x;
-        if (r < MT_ROWS && i * MT_ROWS + r < hidden) {
+        const int64_t row = RT * i * MT_ROWS + r;
+        if (r < RT * MT_ROWS && row < hidden) {
             if (out) {
                 const int a = tb.perm[p];
-                atomicAdd(out + (int64_t)(a / k) * hidden + i * MT_ROWS + r, topk_w[a] * fin[r]);
+                atomicAdd(out + (int64_t)(a / k) * hidden + row, topk_w[a] * fin[r]);
             } else {
-                tb.ysl[(int64_t)p * hidden + i * MT_ROWS + r] = fin[r];
+                tb.ysl[(int64_t)p * hidden + row] = fin[r];
             }
         }
         if (j + 1 < n) {
@@ -1068,31 +1083,47 @@ static bool moe_mfma_ok(const localai_qmat *gu, const localai_qmat *dn, const fl
            (reinterpret_cast<uintptr_t>(h) & 15) == 0 && I % MT_ROWS == 0 && gu->g.cols == H && dn->g.cols == I;
 }
 
+// Grouped decode kernels. gate_up: one super-block per wave (up to 16
+// waves), or four past 16 super-blocks, one gate and one up tile per
+// workgroup. down: at most 8 waves of SPW super-blocks and RT = 2 row tiles
+// per workgroup (~100 KB of weights each): ZAYA down at 8 tokens 24.8 ->
+// 20.6 us against 16 one-super-block waves on one tile; the same shape for
+// gate_up (2 gate + 2 up tiles, 154 VGPRs) was slower, 33.0 -> 34.3 us.
+template <int TYPE, int SPW, int MAXT, int RT>
+static void launch_moe_mfma_st(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
+                               int64_t H, int64_t I, int k, int slots, float *out, const float *topk_w, int64_t T,
+                               bool gate_up, hipStream_t s) {
+    if (gate_up) {
+        const int nb = (int)gu->g.nb, waves = (nb + SPW - 1) / SPW;
+        const int64_t groups = (I / MT_ROWS + RT - 1) / RT;
+        hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, SPW, MAXT, RT>), dim3((unsigned)groups, slots), dim3(64 * waves),
+                           mt_lds_bytes(TYPE, waves, SPW, 1, 2 * RT), s, gu->tiles, gu->tile_bytes, nb, I, tb, h, H, k,
+                           out, T * H);
+    } else {
+        const int nb = (int)dn->g.nb, waves = (nb + SPW - 1) / SPW;
+        const int64_t groups = ((H + MT_ROWS - 1) / MT_ROWS + RT - 1) / RT;
+        hipLaunchKernelGGL((moe_mfma_down<TYPE, SPW, MAXT, RT>), dim3((unsigned)groups, slots), dim3(64 * waves),
+                           mt_lds_bytes(TYPE, waves, SPW, 1, RT), s, dn->tiles, dn->tile_bytes, nb, H, tb, I, out,
+                           topk_w, k);
+    }
+}
+
 template <int TYPE>
 static int launch_moe_mfma_t(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
                              int64_t H, int64_t I, int k, int slots, float *out, const float *topk_w, int64_t T,
                              hipStream_t s) {
-    {
-        const int nb = (int)gu->g.nb, spw = nb <= 16 ? 1 : 4, waves = (nb + spw - 1) / spw;
-        dim3 grid((unsigned)(I / MT_ROWS), slots), block(64 * waves);
-        const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 2);
-        if (spw == 1)
-            hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, 1, 1024>), grid, block, lds, s, gu->tiles, gu->tile_bytes, nb,
-                               I, tb, h, H, k, out, T * H);
-        else
-            hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, 4, 512>), grid, block, lds, s, gu->tiles, gu->tile_bytes, nb,
-                               I, tb, h, H, k, out, T * H);
-        LQ_HIP(hipGetLastError());
-    }
-    const int nb = (int)dn->g.nb, spw = nb <= 16 ? 1 : 4, waves = (nb + spw - 1) / spw;
-    const unsigned tiles = (unsigned)((H + MT_ROWS - 1) / MT_ROWS);
-    const size_t lds = mt_lds_bytes(TYPE, waves, spw, 1, 1);
-    if (spw == 1)
-        hipLaunchKernelGGL((moe_mfma_down<TYPE, 1, 1024>), dim3(tiles, slots), dim3(64 * waves), lds, s, dn->tiles,
-                           dn->tile_bytes, nb, H, tb, I, out, topk_w, k);
+    // nb <= 32 for both (moe_mfma_ok)
+    if (gu->g.nb <= 16)
+        launch_moe_mfma_st<TYPE, 1, 1024, 1>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, true, s);
     else
-        hipLaunchKernelGGL((moe_mfma_down<TYPE, 4, 512>), dim3(tiles, slots), dim3(64 * waves), lds, s, dn->tiles,
-                           dn->tile_bytes, nb, H, tb, I, out, topk_w, k);
+        launch_moe_mfma_st<TYPE, 4, 512, 1>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, true, s);
+    LQ_HIP(hipGetLastError());
+    if (dn->g.nb <= 8)
+        launch_moe_mfma_st<TYPE, 1, 512, 2>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, false, s);
+    else if (dn->g.nb <= 16)
+        launch_moe_mfma_st<TYPE, 2, 512, 2>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, false, s);
+    else
+        launch_moe_mfma_st<TYPE, 4, 512, 1>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, false, s);
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
 }
