@@ -1051,6 +1051,90 @@ int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok) {
     return xh + ntok * 4;
 }
 
+// The tiled layout with whole-line stores: workgroup b converts tokens
+// 8 b .. 8 b + 7, one wave each, with the same per-row scale as
+// x_to_f16_kernel, and writes them through LDS 64 value groups at a time. In
+// the 1 KB slice of a 16-token group, the eight tokens' slots of one value
+// octet are 128 contiguous bytes, so every store of the workgroup fills whole
+// 128-byte lines (the one-wave kernel's scattered 16-byte stores wrote twice
+// the bytes). Workgroup (b, y) stores chunks i = y, y + gridDim.y, ... Rows
+// of at most 64 NG groups (NG <= 8); tokens ntok .. of the last 16-token
+// group are written as zeros.
+template <int NG>
+__global__ __launch_bounds__(512) void x_to_f16_tiles_kernel(const float *__restrict__ X, int64_t ldx, int cols,
+                                                             const int32_t *__restrict__ rows_map, int k,
+                                                             int64_t ntok, _Float16 *__restrict__ Xh, int ldh,
+                                                             float *__restrict__ inv, int vec) {
+    __shared__ uint4 stage[64 * 8];   // [lane = 4 quad + octet][token, swizzled]
+    const int lane = lane_id(), tw = wave_id();
+    const int64_t t0 = (int64_t)blockIdx.x * 8, t = t0 + tw;
+    const bool real = t < ntok;
+    const int64_t src = real ? (rows_map ? (int64_t)(rows_map[t] / k) : t) : 0;
+    const float *x = X + src * ldx;
+    const int ngx = cols >> 3, nq = ldh >> 5;
+    lq_f4 lo[NG], hi[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const int gi = lane + 64 * i;
+        lo[i] = hi[i] = lq_f4{0.f, 0.f, 0.f, 0.f};
+        if (real && gi < ngx) {
+            if (vec) {
+                lo[i] = *reinterpret_cast<const lq_f4 *>(x + 8 * gi);
+                hi[i] = *reinterpret_cast<const lq_f4 *>(x + 8 * gi + 4);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    lo[i][c] = x[8 * gi + c];
+                    hi[i][c] = x[8 * gi + 4 + c];
+                }
+            }
+        }
+    }
+    // the largest magnitude as ordered bits; NaN counts as zero (fmaxf's rule)
+    uint32_t mb = 0;
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float a = lo[i][c], b = hi[i][c];
+            const uint32_t ua = __builtin_bit_cast(uint32_t, a) & 0x7fffffffu;
+            const uint32_t ub = __builtin_bit_cast(uint32_t, b) & 0x7fffffffu;
+            mb = max(mb, max(ua > 0x7f800000u ? 0u : ua, ub > 0x7f800000u ? 0u : ub));
+        }
+    const float m = __builtin_bit_cast(float, wave_max_u32(mb));
+    int s = 0;
+    if (m > 0.0f && m <= 3.4e38f) {
+        int e;
+        frexpf(m, &e);          // m < 2^e <= 2m
+        s = 15 - e;             // m * 2^s in [2^14, 2^15)
+        s = s > 120 ? 120 : s < -120 ? -120 : s;
+    }
+    const float sc = ldexpf(1.0f, s);
+    const int64_t blk0 = (t0 >> 4) * nq;         // 1 KB slice of quad 0 of this 16-token group
+    const int half = (int)((t0 >> 3) & 1);       // tokens 8 half .. 8 half + 7 of the group
+    const int j = threadIdx.x, L = j >> 3, tk = j & 7;   // store: lane L's slot of token tk
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        if (i % (int)gridDim.y != (int)blockIdx.y) continue;   // this workgroup's share of the chunks
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        h8 o;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            o[c] = (_Float16)(lo[i][c] * sc);
+            o[4 + c] = (_Float16)(hi[i][c] * sc);
+        }
+        stage[lane * 8 + (tw ^ (lane & 7))] = __builtin_bit_cast(uint4, o);
+        __syncthreads();
+        const int q = 16 * i + (L >> 2);          // quad (32-value slice) of lane L's group
+        if (q < nq) {
+            const int64_t slot = ((blk0 + q) << 6) + 8 * half + tk + 16 * (L & 3);
+            *reinterpret_cast<uint4 *>(Xh + 8 * slot) = stage[L * 8 + (tk ^ (L & 7))];
+        }
+        __syncthreads();
+    }
+    if (real && lane == 0) inv[t] = ldexpf(1.0f, -s);
+}
+
 int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *rows_map, int k, int64_t ntok,
                     _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s, int tiled) {
     if (ntok <= 0) return LOCALAI_OK;
@@ -1059,6 +1143,21 @@ int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *ro
     const int vec = (uintptr_t)X % 16 == 0 && ldx % 4 == 0;
     const int per = (int)((ldh / 8 + 63) / 64);   // 8-value groups per lane
     const int64_t npad = tiled ? (ntok + 15) / 16 * 16 : ntok;
+    if (tiled && per <= 8) {
+        // the chunks of an 8-token group split over up to 4 workgroups (each
+        // reads the whole rows for their maxima, mostly from L2), so that
+        // 512 tokens occupy 256 workgroups
+        const dim3 g8((unsigned)(npad / 8), (unsigned)(per < 4 ? per : 4));
+        auto gt = [&](auto kern) {
+            hipLaunchKernelGGL(kern, g8, dim3(512), 0, s, X, ldx, (int)cols, rows_map, k, ntok, Xh, (int)ldh, inv, vec);
+        };
+        if (per <= 1) gt(x_to_f16_tiles_kernel<1>);
+        else if (per <= 2) gt(x_to_f16_tiles_kernel<2>);
+        else if (per <= 4) gt(x_to_f16_tiles_kernel<4>);
+        else gt(x_to_f16_tiles_kernel<8>);
+        LQ_HIP(hipGetLastError());
+        return LOCALAI_OK;
+    }
     // one token per wave; one-wave workgroups below 1024 tokens, so that 512
     // tokens reach every CU (four-wave workgroups left half of them idle)
     const int wpg = npad < 1024 ? 1 : 4;
