@@ -148,16 +148,26 @@ int64_t localai_hip_layer_workspace_size(int64_t dim, int64_t ffn);
  * mats: the seven handles in the order attn_output, ffn_gate, ffn_up,
  * ffn_down, attn_q, attn_k, attn_v of layer L+1 (w_attn is its attn_norm),
  * each a Q4_K or Q6_K matrix with the tile form; dim and ffn multiples of
- * 256. One launch: the stages' workgroups run in stage order and each waits
- * on device for the stage before it, after requesting its own weights.
- * Matvec results are those of localai_hip_matvec on the same inputs.
- * ETYPE for shapes or types without a kernel (the caller then runs the
- * separate matvecs). Calls on one workspace must not overlap. */
+ * 256; w_ffn / w_attn 16-byte aligned. By default the chain runs as four
+ * launches on `stream` (o; gate + up; down; q + k + v) with the norms,
+ * SiLU*up, the residual adds and RoPE fused into the matvec kernels'
+ * prologues and epilogues (dim at most 8192, ffn at most 18432; larger
+ * layers run as one launch). localai_hip_layer_chain_mode(1) selects one
+ * launch always, whose stages' workgroups run in stage order and
+ * each wait on the device for the stage before it after requesting their
+ * own weights. Matvec arithmetic is that of localai_hip_matvec. ETYPE for
+ * shapes or types without a kernel (the caller then runs the separate
+ * matvecs). Calls on one workspace must not overlap. */
 int localai_hip_layer_chain(const localai_qmat *const *mats, const float *pre_dev, const float *att_dev,
                             const float *w_ffn_dev, const float *w_attn_dev, float eps,
                             const float *rope_cos_dev, const float *rope_sin_dev, int head_dim,
                             int rope_half, float *x_out_dev, float *q_dev, float *k_dev, float *v_dev,
                             void *workspace_dev, int64_t workspace_bytes, void *stream);
+
+/* Process-wide choice of how localai_hip_layer_chain runs: 0 (the default)
+ * four launches with the glue fused into the matvecs, 1 one launch with
+ * device-side waits between the stages. No counterpart in the reference. */
+int localai_hip_layer_chain_mode(int one_launch);
 
 /* Waits for `stream`, then reports whether a wait between the stages of the
  * last localai_hip_layer_chain launches on this workspace ran out

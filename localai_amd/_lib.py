@@ -52,6 +52,7 @@ SIGNATURES = {
     'localai_hip_layer_workspace_size': (_c_i64, [_c_i64, _c_i64]),
     'localai_hip_layer_chain': (_c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _c_int, _c_int,
                                          _vp, _vp, _vp, _vp, _vp, _c_i64, _vp]),
+    'localai_hip_layer_chain_mode': (_c_int, [_c_int]),
     'localai_hip_layer_error': (_c_int, [_vp, _vp]),
     'localai_hip_attention_workspace_size': (_c_i64, [_c_i64, _c_int, _c_int, _c_int]),
     'localai_hip_attention_decode': (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int,

@@ -401,11 +401,16 @@ int localai_hip_layer_chain(const localai_qmat *const *mats, const float *pre, c
         return fail(LOCALAI_EARG, "layer chain: RoPE needs an even head_dim and rope_half <= head_dim / 2");
     if (ws_bytes < (int64_t)layer_workspace_bytes(dim, ffn)) return fail(LOCALAI_EARG, "layer chain: workspace too small");
     auto mis = [](const void *p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & m) != 0; };
-    if (mis(pre, 15) || mis(att, 15) || mis(x_out, 15) || mis(ws, 255))
-        return fail(LOCALAI_EARG, "layer chain: pre, att and x_out 16-byte, workspace 256-byte aligned");
+    if (mis(pre, 15) || mis(att, 15) || mis(x_out, 15) || mis(w_ffn, 15) || mis(w_attn, 15) || mis(ws, 255))
+        return fail(LOCALAI_EARG, "layer chain: pre, att, x_out and the norm weights 16-byte, workspace 256-byte aligned");
     if (int st = ensure_device()) return st;
     return launch_layer_chain(mats, pre, att, w_ffn, w_attn, eps, rope_cos, rope_sin, head_dim, rope_half, x_out,
                               q_out, k_out, v_out, ws, (hipStream_t)stream);
+}
+
+int localai_hip_layer_chain_mode(int one_launch) {
+    clear_error();
+    return set_layer_mode(one_launch);
 }
 
 int localai_hip_layer_error(void *ws, void *stream) {

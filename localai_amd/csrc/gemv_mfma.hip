@@ -121,42 +121,153 @@ int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_
     return LOCALAI_OK;
 }
 
-// RT row tiles of one matrix, workgroup index blk within the matrix.
-// PIPE: the wave's super-blocks stream through two register sets
-// (mt_pass_pipe) instead of being requested all at once (long rows, where a
-// wave holds several blocks and their dot products would otherwise all wait
-// for the last load).
-template <int TYPE, int SPW, int RT, bool PIPE = false>
+// The decode step's glue around a matvec (the layer path of
+// localai_hip_layer_chain, engine/model.py:229-233 and :181-213):
+//   prologue PRO   X:    y = W x
+//                  NORM: y = inv * (W x), x = src * w already (the launch
+//                        that wrote src also wrote src * w, epilogue RES
+//                        with y_next), inv = 1 / sqrt(mean(src^2) + eps)
+//                        (engine/model.py:82) from the per-tile partial sums
+//                        of squares that launch left in ssq_in; W (x * w)
+//                        scaled by inv is the reference's W (x * inv * w)
+//                        up to rounding
+//   epilogue EPI   Y:    y as it is
+//                  RES:  y = res + y (the residual adds, :229, :233); with
+//                        ssq_out also the sum of y^2 over each 16-row tile,
+//                        with y_next also y_next = y * w_next
+//                  ROPE: adjacent-pair RoPE of rows (2j, 2j + 1) of each
+//                        head, for jobs < rope_jobs (q and k, :205-210)
+//                  SILU: the workgroup's two tiles are tile blk of W (gate)
+//                        and tile blk of W2 (up): y = silu(gate) * up (:232)
+// Every input of the glue is loaded before the weights (loads complete in
+// order, so the glue then waits for none of the weight bytes), unconditionally
+// at clamped indices (a conditional load is split into waits that hold back
+// the loads behind it).
+
+// Partial sums of squares of one vector: MT_SSQ floats, those past the
+// vector's tiles zero (its producer writes only its own tiles). Lane l holds
+// 4l .. 4l + 3 and 256 + 4l .. 256 + 4l + 3.
+struct MtSsq {
+    float4 a, b;
+};
+__device__ __forceinline__ MtSsq mt_load_ssq(const float *__restrict__ p, int lane) {
+    const float4 *p4 = reinterpret_cast<const float4 *>(p);
+    MtSsq s;
+    s.a = p4[lane];
+    s.b = p4[64 + lane];
+    return s;
+}
+// 1 / sqrt(sum / n_vals + eps): each lane adds its eight partials in a fixed
+// order in fp64, then the 64 lanes in an xor butterfly; every step of it adds
+// the same two values in either order, so every lane, wave and workgroup
+// gets the same bits
+__device__ __forceinline__ float mt_norm_inv(const MtSsq &p, int n_vals, float eps) {
+    double s = (((double)p.a.x + (double)p.a.y) + ((double)p.a.z + (double)p.a.w)) +
+               (((double)p.b.x + (double)p.b.y) + ((double)p.b.z + (double)p.b.w));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)(s / (double)n_vals), eps)));
+}
+
+// RT row tiles of one matrix, workgroup index blk within the matrix (job
+// `job` of a fused launch). PIPE: the wave's super-blocks stream through
+// two register sets (mt_pass_pipe) instead of being requested all at once
+// (long rows, where a wave holds several blocks and their dot products would
+// otherwise all wait for the last load).
+template <int TYPE, int SPW, int RT, bool PIPE = false, int PRO = MT_PRO_X, int EPI = MT_EPI_Y>
 __device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
                                                 int64_t tiles, const float *__restrict__ x,
-                                                float *__restrict__ y, int64_t blk) {
+                                                float *__restrict__ y, int64_t blk, const MtGlue &gl = MtGlue{},
+                                                int job = 0) {
+    static_assert(EPI != MT_EPI_SILU || RT == 2, "the SiLU epilogue pairs a gate tile with an up tile");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    const int lane = lane_id(), wv = wave_id(), sb0 = wv * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    const int i = threadIdx.x;
+    // tile t of the workgroup and the row of thread i (i < RT * 16) in it
+    auto tile_of = [&](int t) -> int64_t { return EPI == MT_EPI_SILU ? blk : blk * RT + t; };
+    const int64_t tile = tile_of((i >> 4) & (RT - 1)), row = tile * MT_ROWS + (i & 15);
+    const bool mine = i < RT * 16 && tile < tiles && row < rows;
+    const int64_t rowc = row < rows ? row : rows - 1;
     float4 xv[1][SPW];
     mt_load_x<SPW>(xv[0], x, nb, sb0, lane);   // x first: it is consumed first
+    MtSsq ssq;
+    if constexpr (PRO == MT_PRO_NORM)
+        if (wv == 0) ssq = mt_load_ssq(gl.ssq_in, lane);
+    float res = 0.0f, wn = 0.0f, rc = 0.0f, rs = 0.0f;
+    if constexpr (EPI == MT_EPI_RES) {
+        res = gl.res[rowc];
+        if (gl.y_next) wn = gl.w_next[rowc];
+    }
+    if constexpr (EPI == MT_EPI_ROPE) {
+        if (gl.rope_half > 0) {
+            int pj = (int)(rowc % gl.head_dim) >> 1;
+            pj = pj < gl.rope_half ? pj : gl.rope_half - 1;
+            rc = gl.cos[pj];
+            rs = gl.sin[pj];
+        }
+    }
+    float inv = 1.0f;
+    // run once the weights are requested: the norm factor (wave 0, which
+    // writes the results)
+    auto prep = [&](const float4 (&in)[SPW], float4 (&out)[SPW]) {
+        if constexpr (PRO == MT_PRO_NORM)
+            if (wv == 0) inv = mt_norm_inv(ssq, gl.n, gl.eps);
+#pragma unroll
+        for (int k = 0; k < SPW; ++k) out[k] = in[k];
+    };
     float *fin;
     if constexpr (PIPE) {
-        const uint8_t *tile[RT];
+        static_assert(EPI != MT_EPI_SILU, "paired tiles are for rows of at most 32 super-blocks");
+        const uint8_t *tp[RT];
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            const int64_t tl = blk * RT + t < tiles ? blk * RT + t : tiles - 1;
-            tile[t] = Wt + tl * nb * mt_block_bytes(TYPE);
+            const int64_t tl = tile_of(t) < tiles ? tile_of(t) : tiles - 1;
+            tp[t] = Wt + tl * nb * mt_block_bytes(TYPE);
         }
-        mt_pass_pipe<TYPE, SPW, RT>(tile, nb, sb0, nsb, xv[0], smem, fin);
+        mt_pass_pipe<TYPE, SPW, RT>(tp, nb, sb0, nsb, xv[0], smem, fin, prep);
     } else {
         MtW<TYPE> w[RT][SPW];
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            const int64_t tile = blk * RT + t < tiles ? blk * RT + t : tiles - 1;
-            mt_load_tile<TYPE, SPW>(w[t], Wt + tile * nb * mt_block_bytes(TYPE), nb, sb0, nsb, lane);
+            const int64_t tl = tile_of(t) < tiles ? tile_of(t) : tiles - 1;
+            const uint8_t *base = (EPI == MT_EPI_SILU && t == 1) ? gl.Wt2 : Wt;
+            mt_load_tile<TYPE, SPW>(w[t], base + tl * nb * mt_block_bytes(TYPE), nb, sb0, nsb, lane);
         }
         __builtin_amdgcn_sched_barrier(0);
-        mt_pass<TYPE, SPW, RT, 1>(w, xv, nsb, smem, fin);
+        float4 xp[1][SPW];
+        prep(xv[0], xp[0]);
+        mt_pass<TYPE, SPW, RT, 1>(w, xp, nsb, smem, fin);
     }
-    const int i = threadIdx.x;
-    if (i < RT * 16) {
-        const int64_t tile = blk * RT + (i >> 4), row = tile * MT_ROWS + (i & 15);
-        if (tile < tiles && row < rows) y[row] = fin[i];
+    float v = 0.0f;
+    if constexpr (EPI == MT_EPI_SILU) {
+        if (i < 16 && tile < tiles && row < rows)
+            y[row] = __fmul_rn(silu(__fmul_rn(fin[i], inv)), __fmul_rn(fin[16 + i], inv));
+        return;
+    }
+    if (mine) {
+        v = __fmul_rn(fin[i], inv);
+        if constexpr (EPI == MT_EPI_RES) v = __fadd_rn(res, v);
+        if constexpr (EPI == MT_EPI_ROPE) {
+            const int dd = (int)(row % gl.head_dim), pj = dd >> 1;
+            if (job < gl.rope_jobs && pj < gl.rope_half) {
+                const float other = __fmul_rn(fin[i ^ 1], inv);
+                v = (dd & 1) ? __fadd_rn(__fmul_rn(other, rs), __fmul_rn(v, rc))
+                             : __fsub_rn(__fmul_rn(v, rc), __fmul_rn(other, rs));
+            }
+        }
+        y[row] = v;
+        if constexpr (EPI == MT_EPI_RES)
+            if (gl.y_next) gl.y_next[row] = __fmul_rn(v, wn);
+    }
+    if constexpr (EPI == MT_EPI_RES) {
+        // wave 0 (all of its lanes, for the shuffles): the sum of y^2 over
+        // each 16-row tile, lanes 16t .. 16t + 15 in an xor butterfly
+        if (gl.ssq_out && i < 64) {
+            double q = mine ? (double)v * (double)v : 0.0;
+#pragma unroll
+            for (int m = 8; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+            if (i < RT * 16 && (i & 15) == 0 && tile < tiles) gl.ssq_out[tile] = (float)q;
+        }
     }
 }
 
@@ -194,6 +305,33 @@ void gemv_mfma_many(MtJobs jobs, int nb, const float *__restrict__ x) {
         mt_matvec_block<LQ_Q6_K, SPW, RT, PIPE>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
     else
         mt_matvec_block<LQ_Q4_K, SPW, RT, PIPE>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
+}
+
+// The same kernels with the decode step's glue (MtGlue): one matrix, or
+// fused matrices sharing x (job j of the table)
+// (64 VGPRs only where a workgroup has 16 waves, SPW = 1)
+template <int TYPE, int SPW, int RT, int MAXT, bool PIPE, int PRO, int EPI>
+__global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(MAXT == 1024 && TYPE == LQ_Q4_K && SPW == 1 ? 8 : 1)))
+void gemv_mfma_glue(const uint8_t *__restrict__ Wt, int64_t rows, int nb, int64_t tiles,
+                    const float *__restrict__ x, float *__restrict__ y, MtGlue gl) {
+    mt_matvec_block<TYPE, SPW, RT, PIPE, PRO, EPI>(Wt, rows, nb, tiles, x, y, blockIdx.x, gl, 0);
+}
+
+template <int SPW, int RT, int MAXT, bool Q6, bool PIPE, int PRO, int EPI>
+__global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(MAXT == 1024 && !Q6 && SPW == 1 ? 8 : 1)))
+void gemv_mfma_many_glue(MtJobs jobs, int nb, const float *__restrict__ x, MtGlue gl) {
+    const int64_t b = blockIdx.x;
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < MT_MAX_JOBS; ++i)
+        if (i < jobs.n && b >= jobs.blk0[i]) j = i;
+    const int64_t tiles = (jobs.rows[j] + MT_ROWS - 1) / MT_ROWS;
+    if (Q6 && jobs.type[j] == LQ_Q6_K)
+        mt_matvec_block<LQ_Q6_K, SPW, RT, PIPE, PRO, EPI>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j],
+                                                          b - jobs.blk0[j], gl, j);
+    else
+        mt_matvec_block<LQ_Q4_K, SPW, RT, PIPE, PRO, EPI>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j],
+                                                          b - jobs.blk0[j], gl, j);
 }
 
 // Launch plan: the waves of a workgroup split the super-blocks of one row
@@ -294,6 +432,103 @@ int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const
         else hipLaunchKernelGGL((gemv_mfma_many<S, R, M, false, P>), grid, block, lds, s, jobs, nb, x);        \
     } while (0)
     MT_DISPATCH(MT_L)
+#undef MT_L
+    LQ_HIP(hipGetLastError());
+    return LOCALAI_OK;
+}
+
+int launch_matvec_mfma_glue(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, int pro, int epi,
+                            const MtGlue &gl, hipStream_t s) {
+    if (g.type != LQ_Q4_K && g.type != LQ_Q6_K) return fail(LOCALAI_ETYPE, "mfma matvec: Q4_K / Q6_K only");
+    if (reinterpret_cast<uintptr_t>(x) & 15) return fail(LOCALAI_EARG, "mfma matvec: x must be 16-byte aligned");
+    const int nb = (int)g.nb;
+    if (nb > 72) return fail(LOCALAI_EARG, "mfma matvec: K too large (more than 18432 values)");
+    const bool q6 = g.type == LQ_Q6_K;
+    const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
+    MtPlan p = mt_plan(nb, tiles, q6);
+    if (epi == MT_EPI_SILU) {
+        // gate tile i and up tile i per workgroup, up to 16 waves
+        if (nb > 32 || pro != MT_PRO_NORM || !gl.Wt2)
+            return fail(LOCALAI_ETYPE, "mfma matvec: paired gate / up tiles need rows of at most 8192 values");
+        p.spw = (nb + 15) / 16;
+        p.waves = (nb + p.spw - 1) / p.spw;
+        p.rt = 2;
+        p.pipe = false;
+    }
+    if (pro == MT_PRO_NORM && (nb > 32 || (reinterpret_cast<uintptr_t>(gl.ssq_in) & 15)))
+        return fail(LOCALAI_ETYPE, "mfma matvec: the norm needs rows of at most 8192 values");
+    const dim3 grid((unsigned)(epi == MT_EPI_SILU ? tiles : (tiles + p.rt - 1) / p.rt)), block(64 * p.waves);
+    const size_t lds = mt_lds_bytes(g.type, p.waves, p.spw, 1, p.rt);
+#define MT_L(S, R, M, P)                                                                                    \
+    do {                                                                                                    \
+        if (q6) hipLaunchKernelGGL((gemv_mfma_glue<LQ_Q6_K, S, R, M, P, PRO_, EPI_>), grid, block, lds, s, Wt, \
+                                   g.rows, nb, tiles, x, y, gl);                                            \
+        else hipLaunchKernelGGL((gemv_mfma_glue<LQ_Q4_K, S, R, M, P, PRO_, EPI_>), grid, block, lds, s, Wt,    \
+                                g.rows, nb, tiles, x, y, gl);                                               \
+    } while (0)
+    if (pro == MT_PRO_X && epi == MT_EPI_RES) {
+        constexpr int PRO_ = MT_PRO_X, EPI_ = MT_EPI_RES;
+        MT_DISPATCH(MT_L)
+    } else if (pro == MT_PRO_NORM && epi == MT_EPI_SILU) {
+        constexpr int PRO_ = MT_PRO_NORM, EPI_ = MT_EPI_SILU;
+        if (p.spw == 1) MT_L(1, 2, 1024, false);
+        else MT_L(2, 2, 1024, false);
+    } else {
+        return fail(LOCALAI_ETYPE, "mfma matvec: no kernel for this prologue / epilogue");
+    }
+#undef MT_L
+    LQ_HIP(hipGetLastError());
+    return LOCALAI_OK;
+}
+
+int launch_matvec_mfma_many_glue(int n, const lq_geom *const *g, const uint8_t *const *Wt, const float *x,
+                                 float *const *y, int pro, int epi, const MtGlue &gl, hipStream_t s) {
+    if (n < 1 || n > MT_MAX_JOBS) return fail(LOCALAI_EARG, "mfma matvec: 1..8 matrices per fused launch");
+    if (reinterpret_cast<uintptr_t>(x) & 15) return fail(LOCALAI_EARG, "mfma matvec: x must be 16-byte aligned");
+    const int nb = (int)g[0]->nb;
+    if (nb > 32 || pro != MT_PRO_NORM || (reinterpret_cast<uintptr_t>(gl.ssq_in) & 15))
+        return fail(LOCALAI_ETYPE, "mfma matvec: the norm needs rows of at most 8192 values");
+    int64_t total_tiles = 0;
+    bool any_q6 = false;
+    for (int j = 0; j < n; ++j) {
+        if (g[j]->type != LQ_Q4_K && g[j]->type != LQ_Q6_K) return fail(LOCALAI_ETYPE, "mfma matvec: Q4_K / Q6_K only");
+        if (g[j]->nb != nb) return fail(LOCALAI_EARG, "mfma matvec: fused matrices need the same cols");
+        total_tiles += (g[j]->rows + MT_ROWS - 1) / MT_ROWS;
+        any_q6 |= g[j]->type == LQ_Q6_K;
+    }
+    const MtPlan p = mt_plan(nb, total_tiles, any_q6);
+    MtJobs jobs = {};
+    jobs.n = n;
+    int64_t b = 0;
+    for (int j = 0; j < n; ++j) {
+        jobs.Wt[j] = Wt[j];
+        jobs.y[j] = y[j];
+        jobs.rows[j] = g[j]->rows;
+        jobs.type[j] = g[j]->type;
+        jobs.blk0[j] = b;
+        b += ((g[j]->rows + MT_ROWS - 1) / MT_ROWS + p.rt - 1) / p.rt;
+    }
+    for (int j = n; j <= MT_MAX_JOBS; ++j) jobs.blk0[j] = b;
+    dim3 grid((unsigned)b), block(64 * p.waves);
+    const size_t lds = mt_lds_bytes(any_q6 ? LQ_Q6_K : LQ_Q4_K, p.waves, p.spw, 1, p.rt);
+#define MT_L(S, R, M, P)                                                                                    \
+    do {                                                                                                    \
+        if constexpr (!P) {                                                                                 \
+            if (any_q6) hipLaunchKernelGGL((gemv_mfma_many_glue<S, R, M, true, P, PRO_, EPI_>), grid, block, lds, s, \
+                                           jobs, nb, x, gl);                                                \
+            else hipLaunchKernelGGL((gemv_mfma_many_glue<S, R, M, false, P, PRO_, EPI_>), grid, block, lds, s,  \
+                                    jobs, nb, x, gl);                                                       \
+        }                                                                                                   \
+    } while (0)
+    if (epi == MT_EPI_Y) {
+        constexpr int PRO_ = MT_PRO_NORM, EPI_ = MT_EPI_Y;
+        MT_DISPATCH(MT_L)
+    } else if (epi == MT_EPI_ROPE) {
+        constexpr int PRO_ = MT_PRO_NORM, EPI_ = MT_EPI_ROPE;
+        MT_DISPATCH(MT_L)
+    } else {
+        return fail(LOCALAI_ETYPE, "mfma matvec: no kernel for this prologue / epilogue");
+    }
 #undef MT_L
 #undef MT_DISPATCH
     LQ_HIP(hipGetLastError());

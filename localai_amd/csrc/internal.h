@@ -56,6 +56,28 @@ bool mt_matvec_ok(const lq_geom &g);
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s);
 int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const *Wt, const float *x,
                             float *const *y, hipStream_t s);
+// the decode step's glue around a matvec (gemv_mfma.hip): prologue PRO / epilogue EPI
+enum { MT_PRO_X = 0, MT_PRO_NORM = 1 };
+enum { MT_EPI_Y = 0, MT_EPI_RES = 1, MT_EPI_ROPE = 2, MT_EPI_SILU = 3 };
+constexpr int MT_SSQ = 512;   // floats of a per-tile sums-of-squares buffer
+struct MtGlue {
+    const float *ssq_in;       // NORM: sums of squares of src over its 16-value tiles [MT_SSQ], zero past n / 16
+    int n;                     // NORM: values of src (at most 8192)
+    float eps;
+    const float *res;          // RES: residual [rows]
+    float *ssq_out;            // RES: sums of y^2 over each 16-row tile, or null
+    const float *w_next;       // RES: y_next = y * w_next (the next norm's weight), or null
+    float *y_next;
+    const float *cos, *sin;    // ROPE: [rope_half]
+    int head_dim, rope_half, rope_jobs;
+    const uint8_t *Wt2;        // SILU: the up matrix (tile form), W being the gate
+};
+// one matrix: (X, RES) or (NORM, SILU) over paired gate / up tiles; fused
+// matrices sharing x: (NORM, Y) or (NORM, ROPE)
+int launch_matvec_mfma_glue(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, int pro, int epi,
+                            const MtGlue &gl, hipStream_t s);
+int launch_matvec_mfma_many_glue(int n, const lq_geom *const *g, const uint8_t *const *Wt, const float *x,
+                                 float *const *y, int pro, int epi, const MtGlue &gl, hipStream_t s);
 bool mfma_matvec_enabled();
 
 int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok);
@@ -96,6 +118,7 @@ int launch_layer_chain(const localai_qmat *const *m, const float *pre, const flo
                        hipStream_t s);
 int layer_error_word(void *ws, hipStream_t s, uint32_t *word);
 int set_layer_wait(int spin, int count);
+int set_layer_mode(int one_launch);
 int launch_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, const localai_qmat *dn, int k,
                         const int32_t *topk_idx, const float *topk_w, int skip, float *out, void *ws,
                         hipStream_t s);

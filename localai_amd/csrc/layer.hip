@@ -349,11 +349,68 @@ __global__ __launch_bounds__(LY_THREADS) void layer_chain_kernel(LayerArgs a) {
 
 static size_t ly_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// sync blocks | o [dim] | d [dim] | act [ffn] | per-tile sums of squares
+// [MT_SSQ] (dim / 16 of them written, the rest stays zero). The four-launch
+// form keeps x1 in o and x * w in d.
 size_t layer_workspace_bytes(int64_t dim, int64_t ffn) {
-    return ly_align(4 * D1_WORDS * 4) + ly_align(dim * 4) * 2 + ly_align(ffn * 4);
+    return ly_align(4 * D1_WORDS * 4) + ly_align(dim * 4) * 2 + ly_align(ffn * 4) + ly_align(MT_SSQ * 4);
 }
 
-static std::atomic<int> g_ly_spin{D1_SPIN_LIMIT}, g_ly_count{1};
+static std::atomic<int> g_ly_spin{D1_SPIN_LIMIT}, g_ly_count{1}, g_ly_mode{0};
+
+int set_layer_mode(int one_launch) {
+    g_ly_mode.store(one_launch ? 1 : 0);
+    return LOCALAI_OK;
+}
+
+// The chain as four launches, the glue fused into the matvec kernels
+// (gemv_mfma.hip), each launch waiting for the one before it on the stream
+// (nothing waits on the device):
+//   o       x1 = pre + W_o att; also xs = x1 * w_ffn and x1's per-tile sums
+//           of squares
+//   gate/up act = silu(inv W_gate xs) * (inv W_up xs), inv = the norm factor
+//           of x1 from its sums of squares; a workgroup holds gate tile i and
+//           up tile i
+//   down    x_out = x1 + W_down act; also xs = x_out * w_attn and x_out's sums
+//           of squares
+//   q/k/v   inv' (W_q xs), inv' (W_k xs), inv' (W_v xs), RoPE of q and k
+static int ly_launch_glue(const localai_qmat *const *m, const float *pre, const float *att, const float *w_ffn,
+                          const float *w_attn, float eps, const float *rope_cos, const float *rope_sin,
+                          int head_dim, int rope_half, float *x_out, float *q_out, float *k_out, float *v_out,
+                          float *x1, float *xs, float *act, float *ssq, hipStream_t s) {
+    const int64_t dim = m[0]->g.rows;
+    MtGlue gl{};
+    gl.res = pre;
+    gl.ssq_out = ssq;
+    gl.w_next = w_ffn;
+    gl.y_next = xs;
+    if (int st = launch_matvec_mfma_glue(m[0]->g, m[0]->tiles, att, x1, MT_PRO_X, MT_EPI_RES, gl, s)) return st;
+    gl = MtGlue{};
+    gl.ssq_in = ssq;
+    gl.n = (int)dim;
+    gl.eps = eps;
+    gl.Wt2 = m[2]->tiles;
+    if (int st = launch_matvec_mfma_glue(m[1]->g, m[1]->tiles, xs, act, MT_PRO_NORM, MT_EPI_SILU, gl, s)) return st;
+    gl = MtGlue{};
+    gl.res = x1;
+    gl.ssq_out = ssq;   // the norm before it has read ssq and xs (stream order)
+    gl.w_next = w_attn;
+    gl.y_next = xs;
+    if (int st = launch_matvec_mfma_glue(m[3]->g, m[3]->tiles, act, x_out, MT_PRO_X, MT_EPI_RES, gl, s)) return st;
+    gl = MtGlue{};
+    gl.ssq_in = ssq;
+    gl.n = (int)dim;
+    gl.eps = eps;
+    gl.cos = rope_cos;
+    gl.sin = rope_sin;
+    gl.head_dim = rope_cos ? head_dim : 2;
+    gl.rope_half = rope_cos ? rope_half : 0;
+    gl.rope_jobs = rope_cos ? 2 : 0;
+    const lq_geom *g[3] = {&m[4]->g, &m[5]->g, &m[6]->g};
+    const uint8_t *w[3] = {m[4]->tiles, m[5]->tiles, m[6]->tiles};
+    float *y[3] = {q_out, k_out, v_out};
+    return launch_matvec_mfma_many_glue(3, g, w, xs, y, MT_PRO_NORM, rope_cos ? MT_EPI_ROPE : MT_EPI_Y, gl, s);
+}
 
 int set_layer_wait(int spin, int count) {
     g_ly_spin.store(spin > 0 ? spin : D1_SPIN_LIMIT);
@@ -419,6 +476,12 @@ int launch_layer_chain(const localai_qmat *const *m, const float *pre, const flo
     a.d_buf = (float *)p;
     p += ly_align(dim * 4);
     a.act_buf = (float *)p;
+    p += ly_align(ffn * 4);
+    // the glued matvecs take rows of at most 8192 (norm prologue) and 18432
+    // (down) values; larger layers run as one launch
+    if (g_ly_mode.load() == 0 && dim <= 8192 && ffn <= 18432)
+        return ly_launch_glue(m, pre, att, w_ffn, w_attn, eps, rope_cos, rope_sin, head_dim, rope_half, x_out, q_out,
+                              k_out, v_out, a.o_buf, a.d_buf, a.act_buf, (float *)p, s);
     a.n1 = (int)(dim / MT_ROWS);
     a.n2 = (int)(ffn / MT_ROWS);
     a.n3 = 2 * (int)(dim / MT_ROWS);

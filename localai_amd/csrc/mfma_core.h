@@ -417,11 +417,21 @@ __device__ __forceinline__ void mt_pass(const MtW<TYPE> (&w)[RT][SPW], const flo
 // wave's super-blocks of RT tiles stream through two register sets, so the
 // dot products of block k run while blocks k + 1 and k + 2 are in flight and
 // a wave never holds more than two blocks of weights. tile[t]: block 0 of
-// tile t; the caller has loaded xv (its x loads go out before the weights).
+// tile t; the caller has loaded xv (its x loads go out before the weights),
+// and prep(xv, x) makes the x that is multiplied, once the first weight
+// blocks are requested (a copy when there is nothing else to do).
 // Same arithmetic and summation order as mt_pass (identical results).
-template <int TYPE, int SPW, int RT>
+struct MtCopyX {
+    template <int SPW>
+    __device__ void operator()(const float4 (&in)[SPW], float4 (&out)[SPW]) const {
+#pragma unroll
+        for (int k = 0; k < SPW; ++k) out[k] = in[k];
+    }
+};
+template <int TYPE, int SPW, int RT, typename Prep = MtCopyX>
 __device__ __forceinline__ void mt_pass_pipe(const uint8_t *const (&tile)[RT], int nb, int sb0, int nsb,
-                                             const float4 (&xv)[SPW], uint8_t *smem, float *&fin) {
+                                             const float4 (&xv)[SPW], uint8_t *smem, float *&fin,
+                                             const Prep &prep = Prep{}) {
     constexpr int XB = mt_xbytes(TYPE);
     const int lane = lane_id(), wv = wave_id(), nw = blockDim.x >> 6;
     uint8_t *wl = smem + wv * SPW * XB;
@@ -437,8 +447,10 @@ __device__ __forceinline__ void mt_pass_pipe(const uint8_t *const (&tile)[RT], i
     load(w[0], 0);
     if (SPW > 1) load(w[1], 1);
     __builtin_amdgcn_sched_barrier(0);
+    float4 xp[SPW];
+    prep(xv, xp);
 #pragma unroll
-    for (int k = 0; k < SPW; ++k) mt_stage<TYPE>(xv[k], wl + k * XB, lane);
+    for (int k = 0; k < SPW; ++k) mt_stage<TYPE>(xp[k], wl + k * XB, lane);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const MtLane<TYPE> L = mt_lane<TYPE>(lane);
     float acc[RT];

@@ -1,4 +1,4 @@
-"""The matvec chain of one decode layer as one launch (localai_hip_layer_chain).
+"""The matvec chain of one decode layer (localai_hip_layer_chain).
 
 DecodeLayerChain holds the seven weight handles of the chain -- attn_output,
 ffn_gate, ffn_up, ffn_down of layer L and attn_q, attn_k, attn_v of layer
@@ -10,7 +10,10 @@ layer L+1 (engine/model.py:229-233, then :181-185 and :203-210):
     x_out = x1 + W_down act;  v' = norm(x_out) * w_attn
     q, k, v = W_q v', W_k v', W_v v'   (+ adjacent-pair RoPE of q and k)
 
-All of it stays on the device; nothing here computes on the host.
+All of it stays on the device; nothing here computes on the host. By default
+the chain runs as four launches with the glue fused into the matvec kernels;
+set_mode(one_launch=True) selects the single launch with device-side waits
+between its stages.
 """
 from __future__ import annotations
 
@@ -21,6 +24,11 @@ import numpy as np
 from . import _lib, device
 
 ORDER = ('attn_output', 'ffn_gate', 'ffn_up', 'ffn_down', 'attn_q', 'attn_k', 'attn_v')
+
+
+def set_mode(one_launch):
+    """Process-wide: how every DecodeLayerChain runs (False: four launches)."""
+    _lib.check(_lib.load().localai_hip_layer_chain_mode(1 if one_launch else 0))
 
 
 class DecodeLayerChain:

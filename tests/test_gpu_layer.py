@@ -34,6 +34,15 @@ def build(shapes, seed):
     return chain, raws, w_ffn, w_attn, rng
 
 
+@pytest.fixture(params=[False, True], ids=['four_launches', 'one_launch'])
+def mode(request):
+    """Runs a test with the chain as four glued launches and as one launch."""
+    from localai_amd import layer
+    layer.set_mode(request.param)
+    yield request.param
+    layer.set_mode(False)
+
+
 def check_outputs(got, want, tol=1e-4):
     names = ('x_out', 'q', 'k', 'v')
     for n, g, w in zip(names, got, want):
@@ -42,7 +51,7 @@ def check_outputs(got, want, tol=1e-4):
 
 
 @pytest.mark.parametrize('rope', [False, True])
-def test_llama3_8b_chain_matches_oracle(rope):
+def test_llama3_8b_chain_matches_oracle(rope, mode):
     from localai_amd import device, synth
     chain, raws, w_ffn, w_attn, rng = build(LLAMA3_8B, 5 + rope)
     pre, att = synth.activations(rng, 4096), synth.activations(rng, 4096)
@@ -68,7 +77,7 @@ def test_llama3_8b_chain_matches_oracle(rope):
      'ffn_down': (14, 4096, 11008), 'attn_q': (12, 4096, 4096), 'attn_k': (12, 1024, 4096),
      'attn_v': (14, 1024, 4096)},
 ])
-def test_other_shapes_and_types(shapes):
+def test_other_shapes_and_types(shapes, mode):
     from localai_amd import device, synth
     chain, raws, w_ffn, w_attn, rng = build(shapes, 9)
     dim = shapes['attn_output'][1]
@@ -79,7 +88,7 @@ def test_other_shapes_and_types(shapes):
     check_outputs(got, want)
 
 
-def test_repeated_launches_and_graph_replays_are_identical():
+def test_repeated_launches_and_graph_replays_are_identical(mode):
     """The counters return to zero after each launch: 20 launches in a row and
     replays of a captured graph (with eager launches between them) give the
     same bits as the first launch."""
@@ -120,7 +129,7 @@ def test_wait_that_runs_out_is_reported_and_recovers():
     """Producers kept from counting and a bound of four polls: every wait runs
     out, every workgroup exits, outputs are NaN and check() raises; the next
     launch with the defaults matches the oracle."""
-    from localai_amd import _lib, device, synth
+    from localai_amd import _lib, device, layer, synth
     shapes = {'attn_output': (12, 1024, 1024), 'ffn_gate': (12, 2816, 1024), 'ffn_up': (12, 2816, 1024),
               'ffn_down': (14, 1024, 2816), 'attn_q': (12, 1024, 1024), 'attn_k': (12, 256, 1024),
               'attn_v': (14, 256, 1024)}
@@ -128,16 +137,20 @@ def test_wait_that_runs_out_is_reported_and_recovers():
     pre, att = synth.activations(rng, 1024), synth.activations(rng, 1024)
     pd, ad = device.to_device_f32(pre), device.to_device_f32(att)
     lib = _lib.load()
+    layer.set_mode(True)       # the waits are those of the one-launch chain
     try:
-        assert lib.localai_hip_debug_fused_wait(4, 0) == 0
+        try:
+            assert lib.localai_hip_debug_fused_wait(4, 0) == 0
+            got = chain.forward_device(pd, ad)
+            with pytest.raises(_lib.HipError) as err:
+                chain.check()
+            assert err.value.status == 3
+            assert all(o.isnan().all() for o in got[1:])
+        finally:
+            lib.localai_hip_debug_fused_wait(0, 1)
         got = chain.forward_device(pd, ad)
-        with pytest.raises(_lib.HipError) as err:
-            chain.check()
-        assert err.value.status == 3
-        assert all(o.isnan().all() for o in got[1:])
+        chain.check()
     finally:
-        lib.localai_hip_debug_fused_wait(0, 1)
-    got = chain.forward_device(pd, ad)
-    chain.check()
+        layer.set_mode(False)
     want, _ = olayer.chain(raws, pre, att, w_ffn, w_attn, 1e-5)
     check_outputs(got, want)
