@@ -139,6 +139,7 @@ int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_
 //                        head, for jobs < rope_jobs (q and k, :205-210)
 //                  SILU: the workgroup's two tiles are tile blk of W (gate)
 //                        and tile blk of W2 (up): y = silu(gate) * up (:232)
+//                  PAIR: the same two tiles, y = W x and y2 = W2 x
 // Every input of the glue is loaded before the weights (loads complete in
 // order, so the glue then waits for none of the weight bytes), unconditionally
 // at clamped indices (a conditional load is split into waits that hold back
@@ -179,12 +180,13 @@ __device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, 
                                                 int64_t tiles, const float *__restrict__ x,
                                                 float *__restrict__ y, int64_t blk, const MtGlue &gl = MtGlue{},
                                                 int job = 0) {
-    static_assert(EPI != MT_EPI_SILU || RT == 2, "the SiLU epilogue pairs a gate tile with an up tile");
+    constexpr bool PAIR = EPI == MT_EPI_SILU || EPI == MT_EPI_PAIR;
+    static_assert(!PAIR || RT == 2, "paired tiles: one of W, one of W2");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = lane_id(), wv = wave_id(), sb0 = wv * SPW, nsb = mt_nsb(nb, sb0, SPW);
     const int i = threadIdx.x;
     // tile t of the workgroup and the row of thread i (i < RT * 16) in it
-    auto tile_of = [&](int t) -> int64_t { return EPI == MT_EPI_SILU ? blk : blk * RT + t; };
+    auto tile_of = [&](int t) -> int64_t { return PAIR ? blk : blk * RT + t; };
     const int64_t tile = tile_of((i >> 4) & (RT - 1)), row = tile * MT_ROWS + (i & 15);
     const bool mine = i < RT * 16 && tile < tiles && row < rows;
     const int64_t rowc = row < rows ? row : rows - 1;
@@ -217,7 +219,7 @@ __device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, 
     };
     float *fin;
     if constexpr (PIPE) {
-        static_assert(EPI != MT_EPI_SILU, "paired tiles are for rows of at most 32 super-blocks");
+        static_assert(!PAIR, "paired tiles are for rows of at most 32 super-blocks");
         const uint8_t *tp[RT];
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
@@ -230,7 +232,7 @@ __device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, 
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
             const int64_t tl = tile_of(t) < tiles ? tile_of(t) : tiles - 1;
-            const uint8_t *base = (EPI == MT_EPI_SILU && t == 1) ? gl.Wt2 : Wt;
+            const uint8_t *base = (PAIR && t == 1) ? gl.Wt2 : Wt;
             mt_load_tile<TYPE, SPW>(w[t], base + tl * nb * mt_block_bytes(TYPE), nb, sb0, nsb, lane);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -242,6 +244,10 @@ __device__ __forceinline__ void mt_matvec_block(const uint8_t *__restrict__ Wt, 
     if constexpr (EPI == MT_EPI_SILU) {
         if (i < 16 && tile < tiles && row < rows)
             y[row] = __fmul_rn(silu(__fmul_rn(fin[i], inv)), __fmul_rn(fin[16 + i], inv));
+        return;
+    }
+    if constexpr (EPI == MT_EPI_PAIR) {
+        if (mine) (i < 16 ? y : gl.y2)[row] = __fmul_rn(fin[i], inv);
         return;
     }
     if (mine) {
@@ -412,6 +418,19 @@ int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const
         any_q6 |= g[j]->type == LQ_Q6_K;
     }
     const MtPlan p = mt_plan(nb, total_tiles, any_q6);
+    if (n == 2 && !any_q6 && p.spw == 1 && p.rt == 2 && g[0]->rows == g[1]->rows) {
+        // two Q4_K matrices of one shape (gate and up): a workgroup takes
+        // tile i of each
+        const int64_t tiles = (g[0]->rows + MT_ROWS - 1) / MT_ROWS;
+        MtGlue gl{};
+        gl.Wt2 = Wt[1];
+        gl.y2 = y[1];
+        hipLaunchKernelGGL((gemv_mfma_glue<LQ_Q4_K, 1, 2, 1024, false, MT_PRO_X, MT_EPI_PAIR>), dim3((unsigned)tiles),
+                           dim3(64 * p.waves), mt_lds_bytes(LQ_Q4_K, p.waves, 1, 1, 2), s, Wt[0], g[0]->rows, nb, tiles,
+                           x, y[0], gl);
+        LQ_HIP(hipGetLastError());
+        return LOCALAI_OK;
+    }
     MtJobs jobs = {};
     jobs.n = n;
     int64_t b = 0;

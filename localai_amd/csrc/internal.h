@@ -58,7 +58,7 @@ int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const
                             float *const *y, hipStream_t s);
 // the decode step's glue around a matvec (gemv_mfma.hip): prologue PRO / epilogue EPI
 enum { MT_PRO_X = 0, MT_PRO_NORM = 1 };
-enum { MT_EPI_Y = 0, MT_EPI_RES = 1, MT_EPI_ROPE = 2, MT_EPI_SILU = 3 };
+enum { MT_EPI_Y = 0, MT_EPI_RES = 1, MT_EPI_ROPE = 2, MT_EPI_SILU = 3, MT_EPI_PAIR = 4 };
 constexpr int MT_SSQ = 512;   // floats of a per-tile sums-of-squares buffer
 struct MtGlue {
     const float *ssq_in;       // NORM: sums of squares of src over its 16-value tiles [MT_SSQ], zero past n / 16
@@ -70,7 +70,8 @@ struct MtGlue {
     float *y_next;
     const float *cos, *sin;    // ROPE: [rope_half]
     int head_dim, rope_half, rope_jobs;
-    const uint8_t *Wt2;        // SILU: the up matrix (tile form), W being the gate
+    const uint8_t *Wt2;        // SILU, PAIR: the second matrix (tile form; up, W being the gate)
+    float *y2;                 // PAIR: its output
 };
 // one matrix: (X, RES) or (NORM, SILU) over paired gate / up tiles; fused
 // matrices sharing x: (NORM, Y) or (NORM, ROPE)

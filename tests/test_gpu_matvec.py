@@ -262,6 +262,9 @@ def test_tile_counts_not_multiple_of_xcds(t, rows, cols):
     [(12, 100, 14336), (14, 37, 14336)],
     # a matrix without a tile form (Q8_0) runs beside the fused Q4_K / Q6_K launch
     [(8, 64, 2048), (14, 200, 2048), (12, 1, 2048), (12, 33, 2048)],
+    # two Q4_K matrices of one shape with the paired-tile launch (tile i of
+    # each per workgroup) and, singly, the two-tile plan: ragged last tile
+    [(12, 12300, 4096), (12, 12300, 4096)],
 ])
 def test_matvec_many_matches_single(shapes):
     """localai_hip_matvec_many gives bit-identical results to one matvec per
