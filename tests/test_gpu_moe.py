@@ -250,6 +250,52 @@ def test_one_token_layer_repeated_and_graph_replayed():
         check(h, out.cpu().numpy(), idx.cpu().numpy(), gates.cpu().numpy())
 
 
+def test_prefill_repeated_and_graph_replayed():
+    """The prefill path (routing kernels, f16 conversions, expert GEMMs,
+    combine): eager calls with new tokens, and replays of a captured HIP graph
+    (new tokens copied and an eager call of another size between replays),
+    all match the oracle."""
+    import torch
+    from localai_amd import synth, device
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(91)
+    E, H, I, k, t, T = 32, 1024, 256, 4, 12, 96
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    layer = MoELayer(rw, gu, dn, t, E, H, I, k)
+
+    def check(h, out, idx, g):
+        rout, ridx, rg, _ = omoe.moe_forward(h, rw, gu, dn, t, E, k, I)
+        np.testing.assert_array_equal(idx, ridx)
+        np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
+        assert normwise_rel(out, rout) < 1e-3
+
+    for _ in range(2):
+        h = synth.activations(rng, T, H)
+        check(h, *layer.forward(h))
+    stream = torch.cuda.Stream()
+    hd = device.to_device_f32(synth.activations(rng, T, H))
+    out = torch.empty((T, H), dtype=torch.float32, device=hd.device)
+    idx = torch.empty((T, k), dtype=torch.int32, device=hd.device)
+    gates = torch.empty((T, k), dtype=torch.float32, device=hd.device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        layer.forward_device(hd, out=out, idx=idx, gates=gates, stream=stream)
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            layer.forward_device(hd, out=out, idx=idx, gates=gates, stream=stream)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        h = synth.activations(rng, T, H)
+        hd.copy_(torch.from_numpy(h).to(hd.device))
+        out.fill_(0.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        check(h, out.cpu().numpy(), idx.cpu().numpy(), gates.cpu().numpy())
+        h2 = synth.activations(rng, 40, H)
+        check(h2, *layer.forward(h2))
+
+
 def test_fused_wait_that_runs_out_is_reported():
     """The one-token fused expert kernel with its gate_up workgroups kept from
     counting themselves done and a bound of four polls: every wait runs out,
