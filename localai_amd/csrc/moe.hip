@@ -35,6 +35,7 @@
 
 #include "gemv_core.h"
 #include "internal.h"
+#include "f16rows.h"
 #include "fused_sync.h"
 #include "mfma_core.h"
 
@@ -509,11 +510,23 @@ __global__ __launch_bounds__(256) void moe_route_logits_kernel(const float *__re
 }
 
 // Expert selection for many tokens from logits[T, E]: one wave per token.
+// CONV >= 0 (prefill): the wave also writes token t's f16 row of h for the
+// gate_up GEMM (x_to_f16_row<CONV>), which saves that conversion its own
+// launch.
+struct F16Rows {
+    const float *X;
+    _Float16 *Xh;
+    float *inv;
+    int cols, ldh, vec;
+};
+template <int CONV>
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float *__restrict__ logits, int T, int E, int k,
                                                        int32_t *__restrict__ topk_idx,
-                                                       float *__restrict__ topk_w) {
+                                                       float *__restrict__ topk_w, F16Rows cv) {
     const int t = blockIdx.x * 4 + wave_id();
     if (t >= T) return;
+    if constexpr (CONV >= 0)
+        x_to_f16_row<CONV>(t, cv.X, cv.cols, cv.cols, nullptr, 1, T, cv.Xh, cv.ldh, cv.inv, cv.vec, 0, T);
     route_select_any(logits + (int64_t)t * E, E, k, t, topk_idx, topk_w, MoeTables{}, 0);
 }
 
@@ -1203,6 +1216,7 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
                    ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, -1, tb.logits)
                    : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, -1, tb.logits);
     }
+    bool h_f16_done = false;   // the f16 rows of h for the expert GEMMs written
     if (T >= ROUTE_TILE_TOKENS) {
         const bool part = H % 256 != 0;
         const dim3 lgrid((unsigned)((T + RL_TOK - 1) / RL_TOK), (unsigned)((E + RL_EXP - 1) / RL_EXP));
@@ -1213,8 +1227,23 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
             hipLaunchKernelGGL(moe_route_logits_kernel<false>, lgrid, dim3(256), 0, s, h, (int)T, (int)H, rw, rb,
                                (int)E, tb.logits);
         LQ_HIP(hipGetLastError());
-        hipLaunchKernelGGL(moe_topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, tb.logits, (int)T,
-                           (int)E, k, topk_idx, topk_w);
+        const dim3 tgrid((unsigned)((T + 3) / 4));
+        if (tb.tile_w > 0 && gu->g.cols == H && H % 8 == 0 && f16_stride(H) <= 8 * 64 * 8) {
+            // prefill: the f16 rows of h that gate_up reads come with the selection
+            const F16Rows cv{h, tb.xh_gu, tb.inv_gu, (int)H, (int)f16_stride(H), (int)((uintptr_t)h % 16 == 0 && H % 4 == 0)};
+            const int per = (int)((f16_stride(H) / 8 + 63) / 64);
+            auto go = [&](auto kern) {
+                hipLaunchKernelGGL(kern, tgrid, dim3(256), 0, s, tb.logits, (int)T, (int)E, k, topk_idx, topk_w, cv);
+            };
+            if (per <= 1) go(moe_topk_kernel<1>);
+            else if (per <= 2) go(moe_topk_kernel<2>);
+            else if (per <= 4) go(moe_topk_kernel<4>);
+            else go(moe_topk_kernel<8>);
+            h_f16_done = true;
+        } else {
+            hipLaunchKernelGGL(moe_topk_kernel<-1>, tgrid, dim3(256), 0, s, tb.logits, (int)T, (int)E, k, topk_idx,
+                               topk_w, F16Rows{});
+        }
     } else {
         const size_t head = (size_t)((E + 3) & ~3) * 4;   // logits
         const bool lds_h = head + (size_t)H * 8 <= ROUTE_LDS_BYTES;
@@ -1241,7 +1270,8 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
         const int64_t N = T * k;
         if (gu->g.cols != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe: expert shapes");
         // gate_up reads the f16 rows of h through the permutation (perm[p] / k)
-        if (int st = launch_x_to_f16(h, H, H, nullptr, 1, T, tb.xh_gu, f16_stride(H), tb.inv_gu, s)) return st;
+        if (!h_f16_done)
+            if (int st = launch_x_to_f16(h, H, H, nullptr, 1, T, tb.xh_gu, f16_stride(H), tb.inv_gu, s)) return st;
         if (int st = launch_moe_gemm(gu->g, gu->data, gu->tiles, gu->tile_bytes, true, tb.xh_gu, f16_stride(H),
                                      tb.inv_gu, tb.perm, k, tb.act, I, I, tb.tile_e, tb.tile_p0, tb.tile_n,
                                      tb.n_tiles, tb.max_tiles, s))
