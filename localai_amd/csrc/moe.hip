@@ -356,15 +356,16 @@ __global__ __launch_bounds__(64) void moe_route1_kernel(const float *__restrict_
 // experts, a workgroup RL_WT x RL_WE such tiles, i.e. RL_TOK token rows and
 // RL_EXP expert rows.
 constexpr int RL_T = 4, RL_E = 8;
-constexpr int RL_WT = 2, RL_WE = 2;
+constexpr int RL_WT = 4, RL_WE = 2;
+constexpr int RL_NW = RL_WT * RL_WE;        // waves per workgroup
 constexpr int RL_TOK = RL_T * RL_WT, RL_EXP = RL_E * RL_WE;
 constexpr int RL_ROWS = RL_TOK + RL_EXP;   // rows of a 256-element chunk, 1 KiB each
-constexpr int RL_RPW = RL_ROWS / 4;        // rows each wave copies per chunk
+constexpr int RL_RPW = RL_ROWS / RL_NW;    // rows each wave copies per chunk
 constexpr int RL_STAGES = 3;               // chunks in LDS: one summed, two in flight
 constexpr int RL_PAIRS = 16;               // (token, expert) pairs reduced per LDS round
 constexpr int RL_LD = 68;                  // LDS row of a pair: 64 lane partials + 4 doubles of bank skew
-static_assert(RL_ROWS % 4 == 0 && RL_RPW == 6, "the chunk wait below counts 6 copies per wave");
-static_assert(4 * RL_PAIRS * RL_LD * 8 <= RL_STAGES * RL_ROWS * 1024, "reduction fits the chunk stages");
+static_assert(RL_ROWS % RL_NW == 0 && RL_RPW == 4, "the chunk wait below counts 4 copies per wave");
+static_assert(RL_NW * RL_PAIRS * RL_LD * 8 <= RL_STAGES * RL_ROWS * 1024, "reduction fits the chunk stages");
 
 // Router logits for many tokens, equal bit for bit to moe_route_kernel's:
 // lane l of each wave accumulates, for each (token, expert) pair of its
@@ -381,7 +382,7 @@ static_assert(4 * RL_PAIRS * RL_LD * 8 <= RL_STAGES * RL_ROWS * 1024, "reduction
 // across lanes (offsets 2, 1). Logits go to logits[T, E] as fp32 plus the
 // bias. PART: H is not a multiple of 256 (the last chunk is partial).
 template <bool PART>
-__global__ __launch_bounds__(256) void moe_route_logits_kernel(const float *__restrict__ h, int T, int H,
+__global__ __launch_bounds__(64 * RL_NW) void moe_route_logits_kernel(const float *__restrict__ h, int T, int H,
                                                                const float *__restrict__ rw,
                                                                const float *__restrict__ rb, int E,
                                                                float *__restrict__ logits) {
@@ -389,11 +390,11 @@ __global__ __launch_bounds__(256) void moe_route_logits_kernel(const float *__re
     const int lane = lane_id(), w = wave_id();
     const int wt = w / RL_WE, we = w % RL_WE;
     const int tb = blockIdx.x * RL_TOK, eb = blockIdx.y * RL_EXP;
-    // copies: wave w fills rows w, w + 4, ...; rows past T or E repeat the last one
+    // copies: wave w fills rows w, w + RL_NW, ...; rows past T or E repeat the last one
     const float *src[RL_RPW];
 #pragma unroll
     for (int i = 0; i < RL_RPW; ++i) {
-        const int r = w + 4 * i;
+        const int r = w + RL_NW * i;
         src[i] = (r < RL_TOK ? h + (int64_t)min(tb + r, T - 1) * H : rw + (int64_t)min(eb + r - RL_TOK, E - 1) * H) +
                  4 * lane;
     }
@@ -405,7 +406,7 @@ __global__ __launch_bounds__(256) void moe_route_logits_kernel(const float *__re
 #pragma unroll
         for (int i = 0; i < RL_RPW; ++i)
             __builtin_amdgcn_global_load_lds((const void *)(src[i] + o),
-                                             (__attribute__((address_space(3))) void *)&stage[b][w + 4 * i][0], 16,
+                                             (__attribute__((address_space(3))) void *)&stage[b][w + RL_NW * i][0], 16,
                                              0, 0);
     };
     double acc[RL_T][RL_E];
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(256) void moe_route_logits_kernel(const float *__re
     for (int j = 0; j < nch; ++j) {
         // this wave's copies of chunk j are done once only chunk j + 1's remain
         if (j + 1 < nch)
-            asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+            asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         // every wave's copies of chunk j have landed, and every wave has read
@@ -1221,10 +1222,10 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
         const bool part = H % 256 != 0;
         const dim3 lgrid((unsigned)((T + RL_TOK - 1) / RL_TOK), (unsigned)((E + RL_EXP - 1) / RL_EXP));
         if (part)
-            hipLaunchKernelGGL(moe_route_logits_kernel<true>, lgrid, dim3(256), 0, s, h, (int)T, (int)H, rw, rb,
+            hipLaunchKernelGGL(moe_route_logits_kernel<true>, lgrid, dim3(64 * RL_NW), 0, s, h, (int)T, (int)H, rw, rb,
                                (int)E, tb.logits);
         else
-            hipLaunchKernelGGL(moe_route_logits_kernel<false>, lgrid, dim3(256), 0, s, h, (int)T, (int)H, rw, rb,
+            hipLaunchKernelGGL(moe_route_logits_kernel<false>, lgrid, dim3(64 * RL_NW), 0, s, h, (int)T, (int)H, rw, rb,
                                (int)E, tb.logits);
         LQ_HIP(hipGetLastError());
         const dim3 tgrid((unsigned)((T + 3) / 4));
