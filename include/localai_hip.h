@@ -77,13 +77,20 @@ int localai_hip_f32_matvec(const float *w_dev, int64_t rows, int64_t cols, const
  * matrix, = experts for a 3-D expert tensor, engine/zaya.py:139-150).
  * `src_is_device` says whether ggml_bytes is a device address. Types:
  * Q4_0, Q8_0, Q4_K, Q5_K, Q6_K (the reference's native types,
- * engine/native_quant.py:104). cols must be a multiple of the block size. */
+ * engine/native_quant.py:104). cols must be a multiple of the block size.
+ * Q4_K and Q6_K handles hold the MFMA tile form only (the same bytes as
+ * GGML, reordered); the row-plane form that the several-vector matvec and
+ * the fallback MoE paths read is built from it on the first such call
+ * (which allocates and waits for the stream, so not under graph capture:
+ * LOCALAI_ESTATE there) and then kept. Q8_0 handles hold both forms (the
+ * one-vector matvec reads the row planes, the GEMM the tile form); other
+ * types hold the row planes. */
 int localai_hip_qmat_create(int ggml_type, int64_t rows, int64_t cols, int64_t batch,
                             const void *ggml_bytes, int src_is_device, void *stream,
                             localai_qmat **out);
 int localai_hip_qmat_destroy(localai_qmat *m);
 
-/* Device bytes held by the handle (repacked form). */
+/* Device bytes held by the handle (tile form, and row planes once built). */
 int64_t localai_hip_qmat_device_bytes(const localai_qmat *m);
 
 /* Write the GGML bytes back out (inverse of the repack) to out_dev. */

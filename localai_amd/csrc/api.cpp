@@ -70,6 +70,42 @@ size_t max_lds_per_block() {
     return (size_t)v;
 }
 
+// The row planes of a handle that keeps only the tile form, built once:
+// tile form -> GGML bytes (a temporary buffer) -> row planes, on `s`, which
+// is then synchronised. Not under graph capture (it allocates and waits).
+static std::mutex g_planes_mu;
+
+const uint8_t *qmat_planes(const localai_qmat *cm, hipStream_t s, int *status) {
+    localai_qmat *m = const_cast<localai_qmat *>(cm);
+    std::lock_guard<std::mutex> lk(g_planes_mu);
+    *status = LOCALAI_OK;
+    if (m->data) return m->data;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        *status = fail(LOCALAI_ESTATE, "qmat: this call needs the row planes, which are built on first use; "
+                                       "make the call once outside graph capture first");
+        return nullptr;
+    }
+    uint8_t *planes = nullptr, *ggml = nullptr;
+    hipError_t e = hipMalloc(&planes, (size_t)(m->g.matrix_bytes * m->g.batch));
+    if (e == hipSuccess) e = hipMalloc(&ggml, (size_t)(m->g.ggml_matrix_bytes * m->g.batch));
+    int st = e == hipSuccess ? LOCALAI_OK : hip_fail(e, "hipMalloc(qmat row planes)");
+    if (!st) st = launch_mt_unpack(m->g, m->tiles, m->tile_bytes, ggml, s);
+    if (!st) st = launch_repack(m->g, ggml, planes, 0, s);
+    if (!st) {
+        e = hipStreamSynchronize(s);
+        if (e != hipSuccess) st = hip_fail(e, "qmat row planes");
+    }
+    if (ggml) hipFree(ggml);
+    if (st) {
+        if (planes) hipFree(planes);
+        *status = st;
+        return nullptr;
+    }
+    m->data = planes;
+    return planes;
+}
+
 }  // namespace lq
 
 using namespace lq;
@@ -166,8 +202,14 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
     m->tiles = nullptr;
     m->tile_bytes = 0;
     hipGetDevice(&m->device);
+    // Q4_K / Q6_K keep only the tile form, which their one-vector matvec,
+    // GEMM and MoE kernels read; the row planes are built on first use
+    // (qmat_planes). Q8_0 keeps both (its one-vector matvec reads the row
+    // planes, its GEMM the tile form); other types keep the row planes.
+    const bool tiled = mfma_matvec_enabled() && mt_matrix_bytes(g) > 0;
+    const bool planes_now = !tiled || g.type == LQ_Q8_0;
     size_t nbytes = (size_t)(g.matrix_bytes * batch);
-    hipError_t e = hipMalloc(&m->data, nbytes);
+    hipError_t e = planes_now ? hipMalloc(&m->data, nbytes) : hipSuccess;
     if (e != hipSuccess) { delete m; return hip_fail(e, "hipMalloc(qmat)"); }
     const uint8_t *dsrc = (const uint8_t *)src;
     void *staging = nullptr;
@@ -183,8 +225,8 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
         }
         dsrc = (const uint8_t *)staging;
     }
-    int st = launch_repack(g, dsrc, m->data, 0, s);
-    if (st == LOCALAI_OK && mfma_matvec_enabled() && mt_matrix_bytes(g) > 0) {
+    int st = planes_now ? launch_repack(g, dsrc, m->data, 0, s) : LOCALAI_OK;
+    if (st == LOCALAI_OK && tiled) {
         m->tile_bytes = mt_matrix_bytes(g);
         e = hipMalloc(&m->tiles, (size_t)(m->tile_bytes * batch));
         if (e != hipSuccess) {
@@ -212,20 +254,22 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
 int localai_hip_qmat_destroy(localai_qmat *m) {
     clear_error();
     if (!m) return LOCALAI_OK;
-    hipFree(m->data);
+    if (m->data) hipFree(m->data);
     if (m->tiles) hipFree(m->tiles);
     delete m;
     return LOCALAI_OK;
 }
 
 int64_t localai_hip_qmat_device_bytes(const localai_qmat *m) {
-    return m ? m->g.matrix_bytes * m->g.batch : 0;
+    if (!m) return 0;
+    return (m->data ? m->g.matrix_bytes * m->g.batch : 0) + (m->tiles ? m->tile_bytes * m->g.batch : 0);
 }
 
 int localai_hip_qmat_unpack(const localai_qmat *m, void *out, void *stream) {
     clear_error();
     if (!m || !out) return fail(LOCALAI_EARG, "null pointer");
     if (int st = ensure_device()) return st;
+    if (!m->data) return launch_mt_unpack(m->g, m->tiles, m->tile_bytes, (uint8_t *)out, (hipStream_t)stream);
     return launch_repack(m->g, m->data, (uint8_t *)out, 1, (hipStream_t)stream);
 }
 
@@ -239,7 +283,8 @@ int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out, 
     one.batch = 1;
     void *tmp = nullptr;
     LQ_HIP(hipMalloc(&tmp, (size_t)one.ggml_matrix_bytes));
-    int st = launch_repack(one, m->data + expert * m->g.matrix_bytes, (uint8_t *)tmp, 1, s);
+    int st = m->data ? launch_repack(one, m->data + expert * m->g.matrix_bytes, (uint8_t *)tmp, 1, s)
+                     : launch_mt_unpack(one, m->tiles + expert * m->tile_bytes, m->tile_bytes, (uint8_t *)tmp, s);
     if (st == LOCALAI_OK) st = launch_dequant_ggml(m->g.type, tmp, one.rows * one.cols, out, s);
     hipError_t e = hipStreamSynchronize(s);
     hipFree(tmp);
@@ -258,7 +303,10 @@ int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x, fl
     one.batch = 1;
     if (m->tiles && ntok == 1 && mt_matvec_ok(one))
         return launch_matvec_mfma(one, m->tiles + expert * m->tile_bytes, x, y, (hipStream_t)stream);
-    return launch_matvec(one, m->data + expert * m->g.matrix_bytes, x, m->g.cols, y, m->g.rows, ntok,
+    int st;
+    const uint8_t *planes = qmat_planes(m, (hipStream_t)stream, &st);
+    if (!planes) return st;
+    return launch_matvec(one, planes + expert * m->g.matrix_bytes, x, m->g.cols, y, m->g.rows, ntok,
                          (hipStream_t)stream);
 }
 
@@ -291,9 +339,12 @@ int localai_hip_matvec_many(int n, const localai_qmat *const *mats, const int64_
             wt[nf] = mats[j]->tiles + e * mats[j]->tile_bytes;
             yp[nf] = ys[j];
             ++nf;
-        } else if (int st = launch_matvec(one, mats[j]->data + e * mats[j]->g.matrix_bytes, x, one.cols, ys[j],
-                                          one.rows, 1, s)) {
-            return st;
+        } else {
+            int st;
+            const uint8_t *planes = qmat_planes(mats[j], s, &st);
+            if (!planes) return st;
+            if ((st = launch_matvec(one, planes + e * mats[j]->g.matrix_bytes, x, one.cols, ys[j], one.rows, 1, s)))
+                return st;
         }
     }
     return nf ? launch_matvec_mfma_many(nf, gp, wt, x, yp, s) : LOCALAI_OK;
@@ -316,8 +367,9 @@ int localai_hip_matmul(const localai_qmat *m, int64_t expert, const float *x, in
     lq_geom one = m->g;
     one.batch = 1;
     const int64_t ts = y_layout == 0 ? m->g.rows : 1, rs = y_layout == 0 ? 1 : tokens;
-    return launch_gemm(one, m->data + expert * m->g.matrix_bytes, m->tiles ? m->tiles + expert * m->tile_bytes : nullptr,
-                       x, tokens, y, ts, rs, ws, ws_bytes,
+    // the GEMM reads the tile form where there is one, else the row planes
+    return launch_gemm(one, m->tiles ? nullptr : m->data + expert * m->g.matrix_bytes,
+                       m->tiles ? m->tiles + expert * m->tile_bytes : nullptr, x, tokens, y, ts, rs, ws, ws_bytes,
                        (hipStream_t)stream);
 }
 

@@ -24,9 +24,18 @@ bool mt_matvec_ok(const lq_geom &g) {
     return (g.type == LQ_Q4_K || g.type == LQ_Q6_K) && g.nb <= 72;
 }
 
-// GGML -> tile form, one thread per (matrix, row, super-block). Rows past
-// the end of the last tile stay zero (the caller clears the buffer).
-__global__ void mt_repack_q4k(lq_geom g, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+// GGML <-> tile form, one thread per (matrix, row, super-block); UNPACK
+// moves the bytes back to GGML order through the same index expressions.
+// Packing: rows past the end of the last tile stay zero (the caller clears
+// the buffer).
+template <bool UNPACK>
+__device__ __forceinline__ void mt_mv(uint8_t *ggml, uint8_t *tile) {
+    if (UNPACK) *ggml = *tile;
+    else *tile = *ggml;
+}
+
+template <bool UNPACK>
+__global__ void mt_repack_q4k(lq_geom g, uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
                               int64_t dst_matrix_bytes) {
     const int64_t total = g.batch * g.rows * g.nb;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
@@ -34,16 +43,15 @@ __global__ void mt_repack_q4k(lq_geom g, const uint8_t *__restrict__ src, uint8_
         const int64_t e = i / (g.rows * g.nb);
         const int64_t rem = i - e * g.rows * g.nb;
         const int64_t row = rem / g.nb, sb = rem - row * g.nb;
-        const uint8_t *s = src + e * g.ggml_matrix_bytes + row * g.ggml_row_bytes + sb * 144;
+        uint8_t *s = src + e * g.ggml_matrix_bytes + row * g.ggml_row_bytes + sb * 144;
         uint8_t *blk = dst + e * dst_matrix_bytes + ((row / MT_ROWS) * g.nb + sb) * MT_Q4K_BLOCK;
         const int n = (int)(row % MT_ROWS);
         for (int c = 0; c < 4; ++c) {
             const int L = n + 16 * c;
             for (int p = 0; p < 4; ++p)
-                for (int b = 0; b < 8; ++b)
-                    blk[(p >> 1) * 1024 + L * 16 + (p & 1) * 8 + b] = s[16 + 32 * p + 8 * c + b];
+                for (int b = 0; b < 8; ++b) mt_mv<UNPACK>(&s[16 + 32 * p + 8 * c + b], &blk[(p >> 1) * 1024 + L * 16 + (p & 1) * 8 + b]);
         }
-        for (int b = 0; b < 16; ++b) blk[2048 + n * 16 + b] = s[b];
+        for (int b = 0; b < 16; ++b) mt_mv<UNPACK>(&s[b], &blk[2048 + n * 16 + b]);
     }
 }
 
@@ -51,7 +59,8 @@ __global__ void mt_repack_q4k(lq_geom g, const uint8_t *__restrict__ src, uint8_
 //   ql piece h (h = 0, 1) [64][16 B]: ql[64h + 8c ..+7], ql[64h + 32 + 8c ..+7]
 //   qh piece [64][16 B]:             qh[8c ..+7],       qh[32 + 8c ..+7]
 //   scales [16 rows][16 B] (int8), d [16 rows][2 B]
-__global__ void mt_repack_q6k(lq_geom g, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+template <bool UNPACK>
+__global__ void mt_repack_q6k(lq_geom g, uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
                               int64_t dst_matrix_bytes) {
     const int64_t total = g.batch * g.rows * g.nb;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
@@ -59,27 +68,28 @@ __global__ void mt_repack_q6k(lq_geom g, const uint8_t *__restrict__ src, uint8_
         const int64_t e = i / (g.rows * g.nb);
         const int64_t rem = i - e * g.rows * g.nb;
         const int64_t row = rem / g.nb, sb = rem - row * g.nb;
-        const uint8_t *s = src + e * g.ggml_matrix_bytes + row * g.ggml_row_bytes + sb * 210;
+        uint8_t *s = src + e * g.ggml_matrix_bytes + row * g.ggml_row_bytes + sb * 210;
         uint8_t *blk = dst + e * dst_matrix_bytes + ((row / MT_ROWS) * g.nb + sb) * MT_Q6K_BLOCK;
         const int n = (int)(row % MT_ROWS);
         for (int c = 0; c < 4; ++c) {
             const int L = n + 16 * c;
             for (int h = 0; h < 2; ++h)
                 for (int b = 0; b < 8; ++b) {
-                    blk[h * 1024 + L * 16 + b] = s[64 * h + 8 * c + b];
-                    blk[h * 1024 + L * 16 + 8 + b] = s[64 * h + 32 + 8 * c + b];
-                    blk[2048 + L * 16 + 8 * h + b] = s[128 + 32 * h + 8 * c + b];
+                    mt_mv<UNPACK>(&s[64 * h + 8 * c + b], &blk[h * 1024 + L * 16 + b]);
+                    mt_mv<UNPACK>(&s[64 * h + 32 + 8 * c + b], &blk[h * 1024 + L * 16 + 8 + b]);
+                    mt_mv<UNPACK>(&s[128 + 32 * h + 8 * c + b], &blk[2048 + L * 16 + 8 * h + b]);
                 }
         }
-        for (int b = 0; b < 16; ++b) blk[3072 + n * 16 + b] = s[192 + b];
-        blk[3328 + 2 * n] = s[208];
-        blk[3328 + 2 * n + 1] = s[209];
+        for (int b = 0; b < 16; ++b) mt_mv<UNPACK>(&s[192 + b], &blk[3072 + n * 16 + b]);
+        mt_mv<UNPACK>(&s[208], &blk[3328 + 2 * n]);
+        mt_mv<UNPACK>(&s[209], &blk[3328 + 2 * n + 1]);
     }
 }
 
 // Q8_0: one thread per (matrix, row, 256-value block); GGML blocks are
 // d (2 B) then 32 int8 quants. Blocks past the row end stay zero.
-__global__ void mt_repack_q80(lq_geom g, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+template <bool UNPACK>
+__global__ void mt_repack_q80(lq_geom g, uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
                               int64_t dst_matrix_bytes) {
     const int64_t nsb = mt_nsb(g);
     const int64_t total = g.batch * g.rows * nsb;
@@ -88,37 +98,49 @@ __global__ void mt_repack_q80(lq_geom g, const uint8_t *__restrict__ src, uint8_
         const int64_t e = i / (g.rows * nsb);
         const int64_t rem = i - e * g.rows * nsb;
         const int64_t row = rem / nsb, sb = rem - row * nsb;
-        const uint8_t *srow = src + e * g.ggml_matrix_bytes + row * g.ggml_row_bytes;
+        uint8_t *srow = src + e * g.ggml_matrix_bytes + row * g.ggml_row_bytes;
         uint8_t *blk = dst + e * dst_matrix_bytes + ((row / MT_ROWS) * nsb + sb) * MT_Q80_BLOCK;
         const int n = (int)(row % MT_ROWS);
         for (int j = 0; j < 8; ++j) {
             const int64_t b = sb * 8 + j;
             if (b >= g.nb) break;
-            const uint8_t *s = srow + b * 34;
-            blk[4096 + n * 16 + 2 * j] = s[0];
-            blk[4096 + n * 16 + 2 * j + 1] = s[1];
+            uint8_t *s = srow + b * 34;
+            mt_mv<UNPACK>(&s[0], &blk[4096 + n * 16 + 2 * j]);
+            mt_mv<UNPACK>(&s[1], &blk[4096 + n * 16 + 2 * j + 1]);
             for (int c = 0; c < 4; ++c)
                 for (int q = 0; q < 8; ++q)
-                    blk[(j >> 1) * 1024 + (n + 16 * c) * 16 + 8 * (j & 1) + q] = s[2 + 8 * c + q];
+                    mt_mv<UNPACK>(&s[2 + 8 * c + q], &blk[(j >> 1) * 1024 + (n + 16 * c) * 16 + 8 * (j & 1) + q]);
         }
     }
 }
 
-int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_t dst_matrix_bytes,
-                     hipStream_t s) {
+// direction 0: GGML -> tile form (the buffer cleared first); 1: tile form -> GGML
+static int mt_repack_launch(const lq_geom &g, uint8_t *ggml, uint8_t *tiles, int64_t tile_matrix_bytes, int unpack,
+                            hipStream_t s) {
     const int64_t total = g.batch * g.rows * mt_nsb(g);
-    LQ_HIP(hipMemsetAsync(dst, 0, (size_t)(dst_matrix_bytes * g.batch), s));
+    if (!unpack) LQ_HIP(hipMemsetAsync(tiles, 0, (size_t)(tile_matrix_bytes * g.batch), s));
     if (total <= 0) return LOCALAI_OK;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    if (g.type == LQ_Q8_0)
-        hipLaunchKernelGGL(mt_repack_q80, dim3((unsigned)blocks), dim3(256), 0, s, g, ggml, dst, dst_matrix_bytes);
-    else if (g.type == LQ_Q6_K)
-        hipLaunchKernelGGL(mt_repack_q6k, dim3((unsigned)blocks), dim3(256), 0, s, g, ggml, dst, dst_matrix_bytes);
-    else
-        hipLaunchKernelGGL(mt_repack_q4k, dim3((unsigned)blocks), dim3(256), 0, s, g, ggml, dst, dst_matrix_bytes);
+#define MT_R(K)                                                                                                   \
+    if (unpack) hipLaunchKernelGGL(K<true>, dim3((unsigned)blocks), dim3(256), 0, s, g, ggml, tiles, tile_matrix_bytes); \
+    else hipLaunchKernelGGL(K<false>, dim3((unsigned)blocks), dim3(256), 0, s, g, ggml, tiles, tile_matrix_bytes)
+    if (g.type == LQ_Q8_0) { MT_R(mt_repack_q80); }
+    else if (g.type == LQ_Q6_K) { MT_R(mt_repack_q6k); }
+    else { MT_R(mt_repack_q4k); }
+#undef MT_R
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
+}
+
+int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_t dst_matrix_bytes,
+                     hipStream_t s) {
+    return mt_repack_launch(g, const_cast<uint8_t *>(ggml), dst, dst_matrix_bytes, 0, s);
+}
+
+int launch_mt_unpack(const lq_geom &g, const uint8_t *tiles, int64_t tile_matrix_bytes, uint8_t *ggml,
+                     hipStream_t s) {
+    return mt_repack_launch(g, ggml, const_cast<uint8_t *>(tiles), tile_matrix_bytes, 1, s);
 }
 
 // The decode step's glue around a matvec (the layer path of

@@ -9,7 +9,8 @@
 
 struct localai_qmat {
     lq_geom g;
-    uint8_t *data;      // device, g.matrix_bytes * g.batch (row planes, qformat.h)
+    uint8_t *data;      // device, g.matrix_bytes * g.batch (row planes, qformat.h); for types with a
+                        // tile form null until qmat_planes builds it
     int device;
     uint8_t *tiles;     // device, MFMA tile form (gemv_mfma.hip) or null
     int64_t tile_bytes; // per matrix of the tile form
@@ -52,6 +53,12 @@ int launch_matvec(const lq_geom &g, const uint8_t *packed, const float *x, int64
 
 int64_t mt_matrix_bytes(const lq_geom &g);
 int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_t dst_matrix_bytes, hipStream_t s);
+// tile form -> GGML bytes (the inverse of launch_mt_repack)
+int launch_mt_unpack(const lq_geom &g, const uint8_t *tiles, int64_t tile_matrix_bytes, uint8_t *ggml,
+                     hipStream_t s);
+// The row planes of a handle (built from the tile form on first use, then
+// kept; not under graph capture); null with *status set on failure
+const uint8_t *qmat_planes(const localai_qmat *m, hipStream_t s, int *status);
 bool mt_matvec_ok(const lq_geom &g);
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s);
 int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const *Wt, const float *x,

@@ -107,14 +107,21 @@ int run(int t, const uint8_t *raw, const float *x, float *out, int rows, int col
     if (!st && gemm) {
         const int64_t wsb = gemm_workspace_bytes(m->g, tokens);
         st = grow(&g_ws, &g_ws_cap, (size_t)(wsb + 3) / 4);
-        if (!st) st = launch_gemm(m->g, m->data, m->tiles, g_x, tokens, g_y, 1, tokens, g_ws, wsb, nullptr);
+        if (!st) st = launch_gemm(m->g, m->tiles ? nullptr : m->data, m->tiles, g_x, tokens, g_y, 1, tokens, g_ws, wsb,
+                                  nullptr);
         if (!st) {
             hipError_t e = hipMemcpy(out, g_y, (size_t)tokens * rows * 4, hipMemcpyDeviceToHost);
             if (e != hipSuccess) st = hip_fail(e, "download y");
         }
     } else {
-        if (!st) st = (m->tiles && tokens == 1 && mt_matvec_ok(m->g)) ? launch_matvec_mfma(m->g, m->tiles, g_x, g_y, nullptr)
-                                                : launch_matvec(m->g, m->data, g_x, cols, g_y, rows, tokens, nullptr);
+        if (!st) {
+            if (m->tiles && tokens == 1 && mt_matvec_ok(m->g)) {
+                st = launch_matvec_mfma(m->g, m->tiles, g_x, g_y, nullptr);
+            } else {
+                const uint8_t *planes = qmat_planes(m, nullptr, &st);
+                if (planes) st = launch_matvec(m->g, planes, g_x, cols, g_y, rows, tokens, nullptr);
+            }
+        }
         if (!st) {
             if (!transpose_out) {
                 hipError_t e = hipMemcpy(out, g_y, (size_t)tokens * rows * 4, hipMemcpyDeviceToHost);

@@ -1042,8 +1042,9 @@ static MoeTables carve(void *ws, int64_t T, int64_t E, int64_t k, int64_t H, int
 }
 
 template <int T, bool GATE_UP, int NT>
-static void launch_grouped_t(const localai_qmat *m, int lpr, int waves, const MoeTables &tb, const float *xsrc,
-                             int64_t x_stride, int k, int slots, int64_t max_tokens, hipStream_t s) {
+static void launch_grouped_t(const localai_qmat *m, const uint8_t *planes, int lpr, int waves, const MoeTables &tb,
+                             const float *xsrc, int64_t x_stride, int k, int slots, int64_t max_tokens,
+                             hipStream_t s) {
     const lq_geom &g = m->g;
     const int64_t half = GATE_UP ? g.rows / 2 : g.rows;
     const int64_t tile = (int64_t)(moe_rows<T, NT>() / (GATE_UP ? 2 : 1)) * (64 / lpr);
@@ -1051,13 +1052,13 @@ static void launch_grouped_t(const localai_qmat *m, int lpr, int waves, const Mo
         block(64 * waves);
     const size_t lds = (size_t)waves * NT * 16 * lpr * 16;
     if (lpr == 16)
-        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 16, NT>), grid, block, lds, s, m->data, g, tb, xsrc,
+        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 16, NT>), grid, block, lds, s, planes, g, tb, xsrc,
                            x_stride, k);
     else if (lpr == 32)
-        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 32, NT>), grid, block, lds, s, m->data, g, tb, xsrc,
+        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 32, NT>), grid, block, lds, s, planes, g, tb, xsrc,
                            x_stride, k);
     else
-        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 64, NT>), grid, block, lds, s, m->data, g, tb, xsrc,
+        hipLaunchKernelGGL((moe_grouped_kernel<T, GATE_UP, 64, NT>), grid, block, lds, s, planes, g, tb, xsrc,
                            x_stride, k);
 }
 
@@ -1074,11 +1075,14 @@ static int launch_grouped(const localai_qmat *m, const MoeTables &tb, const floa
     if ((size_t)waves * nt * 16 * lpr * 16 > max_lds_per_block())
         return fail(LOCALAI_EARG, "moe: x windows exceed the LDS per workgroup");
     if ((max_tokens + nt - 1) / nt > 65535) return fail(LOCALAI_EARG, "moe: too many tokens for the matvec path");
+    int st;
+    const uint8_t *planes = qmat_planes(m, s, &st);   // this path reads the row planes
+    if (!planes) return st;
     switch (g.type) {
 #define LQ_G(TT)                                                                                      \
     case TT:                                                                                          \
-        if (nt == 2) launch_grouped_t<TT, GATE_UP, 2>(m, lpr, waves, tb, xsrc, x_stride, k, slots, max_tokens, s); \
-        else launch_grouped_t<TT, GATE_UP, 1>(m, lpr, waves, tb, xsrc, x_stride, k, slots, max_tokens, s);        \
+        if (nt == 2) launch_grouped_t<TT, GATE_UP, 2>(m, planes, lpr, waves, tb, xsrc, x_stride, k, slots, max_tokens, s); \
+        else launch_grouped_t<TT, GATE_UP, 1>(m, planes, lpr, waves, tb, xsrc, x_stride, k, slots, max_tokens, s);        \
         break;
         LQ_G(LQ_Q4_K) LQ_G(LQ_Q5_K) LQ_G(LQ_Q6_K) LQ_G(LQ_Q8_0) LQ_G(LQ_Q4_0)
 #undef LQ_G
@@ -1273,12 +1277,19 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
         // gate_up reads the f16 rows of h through the permutation (perm[p] / k)
         if (!h_f16_done)
             if (int st = launch_x_to_f16(h, H, H, nullptr, 1, T, tb.xh_gu, f16_stride(H), tb.inv_gu, s)) return st;
-        if (int st = launch_moe_gemm(gu->g, gu->data, gu->tiles, gu->tile_bytes, true, tb.xh_gu, f16_stride(H),
+        // the expert GEMMs read the tile form where there is one (gate_up
+        // with inter a multiple of 16), else the row planes
+        int st = LOCALAI_OK;
+        const uint8_t *wgu = gu->tiles && I % MT_ROWS == 0 ? nullptr : qmat_planes(gu, s, &st);
+        if (st) return st;
+        const uint8_t *wdn = dn->tiles ? nullptr : qmat_planes(dn, s, &st);
+        if (st) return st;
+        if (int st = launch_moe_gemm(gu->g, wgu, gu->tiles && I % MT_ROWS == 0 ? gu->tiles : nullptr, gu->tile_bytes, true, tb.xh_gu, f16_stride(H),
                                      tb.inv_gu, tb.perm, k, tb.act, I, I, tb.tile_e, tb.tile_p0, tb.tile_n,
                                      tb.n_tiles, tb.max_tiles, s))
             return st;
         if (int st = launch_x_to_f16(tb.act, I, I, nullptr, 1, N, tb.xh_dn, f16_stride(I), tb.inv_dn, s)) return st;
-        if (int st = launch_moe_gemm(dn->g, dn->data, dn->tiles, dn->tile_bytes, false, tb.xh_dn, f16_stride(I),
+        if (int st = launch_moe_gemm(dn->g, wdn, dn->tiles, dn->tile_bytes, false, tb.xh_dn, f16_stride(I),
                                      tb.inv_dn, nullptr, 1, tb.ysl, H, I, tb.tile_e, tb.tile_p0, tb.tile_n,
                                      tb.n_tiles, tb.max_tiles, s))
             return st;

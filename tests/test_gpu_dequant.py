@@ -4,6 +4,7 @@ import numpy as np
 import pytest
 
 from oracle import quant
+from tests.conftest import normwise_rel
 from tests.gpu_util import bits, random_ggml
 
 pytestmark = pytest.mark.gpu
@@ -129,3 +130,34 @@ def test_dequant_every_fp16_scale_pattern(t):
     with np.errstate(invalid='ignore', over='ignore'):
         ref = quant.dequantize(raw, t, (nb * block,))
     _nan_aware_equal(got, ref)
+
+
+@pytest.mark.parametrize('t', (12, 14))
+def test_tile_form_only_until_row_planes_are_needed(t):
+    """Q4_K / Q6_K handles hold the tile form only (as many bytes as GGML, up
+    to the padding of the last 16-row tile); the first several-vector matvec
+    builds the row planes from it. Results and the GGML bytes read back are
+    the same before and after."""
+    from localai_amd import device
+    rng = np.random.default_rng(500 + t)
+    rows, cols, batch = 100, 1024, 2
+    raw = random_ggml(rng, t, batch * rows * cols)
+    q = device.QMat.from_ggml(raw, t, rows, cols, batch)
+    try:
+        before = q.device_bytes
+        tiles = batch * ((rows + 15) // 16) * 16 * (cols // 256) * {12: 144, 14: 210}[t]
+        assert tiles <= before <= tiles + 256 * batch
+        x = rng.standard_normal((3, cols)).astype(np.float32)
+        xd = device.to_device_f32(x)
+        one = q.matvec(xd[0], expert=1).cpu().numpy()
+        assert q.device_bytes == before
+        per = len(raw) // batch
+        want = np.stack([quant.matvec_exact(raw[per:], t, rows, cols, x[i]) for i in range(3)])
+        got = q.matvec(xd, expert=1).cpu().numpy()
+        assert q.device_bytes > before
+        for i in range(3):
+            assert normwise_rel(got[i], want[i]) < 1e-5
+        assert q.unpack().cpu().numpy().tobytes() == raw
+        np.testing.assert_array_equal(bits(q.matvec(xd[0], expert=1).cpu().numpy()), bits(one))
+    finally:
+        q.close()
