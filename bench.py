@@ -362,7 +362,7 @@ def wl_layer(args, torch, device, synth):
     for name, o in outs.items():
         if not torch.isfinite(o).all():
             raise SystemExit(f'non-finite output in {name}')
-    roof = gate_roofline(args, torch, device, host['ffn_gate'], xs['h2'], stream)
+    roof = gate_up_roofline(args, torch, device, host['ffn_gate'], host['ffn_up'], xs['h2'], stream)
     cpu = None
     if args.cpu_baseline != 'off' and ref_ok():
         log('timing CPU baseline (reference AVX2 kernels)')
@@ -385,6 +385,28 @@ def wl_layer(args, torch, device, synth):
                    'algorithmic_bytes_per_layer': layer_bytes, 'weight_copies_rotated': copies,
                    'launch': 'one hip graph per rotation of layer copies; q/k/v and gate/up each one fused launch (shared input)'},
         'roofline': roof, 'cpu_baseline': cpu}
+
+
+def gate_up_roofline(args, torch, device, gate_host, up_host, x, stream):
+    """The layer's dominant kernel: the fused ffn_gate + ffn_up launch (two
+    Q4_K 14336 x 4096 matvecs on one x), rotated over > 2x MALL, timed
+    alone."""
+    nbytes = 2 * 14336 * 16 * 144 + 4 * 4096 + 2 * 4 * 14336
+    nrot = rotations(2 * 14336 * 16 * 144)
+    pairs = [(device.QMat.from_ggml(gate_host, 12, 14336, 4096), device.QMat.from_ggml(up_host, 12, 14336, 4096))
+             for _ in range(nrot)]
+    gout = [torch.empty(14336, dtype=torch.float32, device=device.device()) for _ in range(2)]
+    log('timing dominant kernel')
+    kms = time_steps(torch, [lambda p=p: device.matvec_many(list(p), x, outs=gout, stream=stream) for p in pairs],
+                     stream, args.steps, args.warmup)
+    achieved = nbytes / (kms * 1e-3) / 1e9
+    for p in pairs:
+        for m in p:
+            m.close()
+    return {'bound': 'hbm', 'kernel': 'gemv_mfma_glue<Q4_K, paired tiles> ffn_gate + ffn_up 2 x 14336x4096',
+            'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+            'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': measured_traffic('layer', 'gate_up'),
+            'us_per_launch': round(kms * 1e3, 3), 'bytes_per_launch': nbytes}
 
 
 def gate_roofline(args, torch, device, gate_host, x, stream):
