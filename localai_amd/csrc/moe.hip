@@ -867,6 +867,30 @@ __global__ void moe_combine_kernel(const float *__restrict__ ysl, const int32_t 
     out[(int64_t)t * H + hcol] = s;
 }
 
+// The same sums for K = k known at compile time and H % 4 == 0 (16-byte
+// rows): every one of the token's K rows is requested before the first is
+// added (the loop above waits for each load in turn), four columns per
+// thread; the additions keep the top-k order, so the bits are the same.
+template <int K>
+__global__ void moe_combine_vec_kernel(const float *__restrict__ ysl, const int32_t *__restrict__ pos,
+                                       const float *__restrict__ topk_w, int H, float *__restrict__ out) {
+    const int t = blockIdx.y;
+    const int c4 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (4 * c4 >= H) return;
+    float4 y[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+        y[j] = reinterpret_cast<const float4 *>(ysl + (int64_t)pos[t * K + j] * H)[c4];
+    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        const float w = topk_w[t * K + j];
+        s = make_float4(__builtin_fmaf(w, y[j].x, s.x), __builtin_fmaf(w, y[j].y, s.y), __builtin_fmaf(w, y[j].z, s.z),
+                        __builtin_fmaf(w, y[j].w, s.w));
+    }
+    reinterpret_cast<float4 *>(out + (int64_t)t * H)[c4] = s;
+}
+
 // ------------------------------------------------- one-token decode, fused
 
 // The expert part of the MoE layer for one token with k <= 2 in one launch,
@@ -1312,8 +1336,17 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
         if (int st = launch_grouped<true>(gu, tb, h, H, k, slots, T, s)) return st;
         if (int st = launch_grouped<false>(dn, tb, tb.act, I, k, slots, T, s)) return st;
     }
-    dim3 grid((unsigned)((H + 255) / 256), (unsigned)T);
-    hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, s, tb.ysl, tb.pos, topk_w, k, (int)H, out);
+    const bool vec = H % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    const dim3 vgrid((unsigned)((H / 4 + 255) / 256), (unsigned)T);
+    if (vec && k == 8)
+        hipLaunchKernelGGL(moe_combine_vec_kernel<8>, vgrid, dim3(256), 0, s, tb.ysl, tb.pos, topk_w, (int)H, out);
+    else if (vec && k == 4)
+        hipLaunchKernelGGL(moe_combine_vec_kernel<4>, vgrid, dim3(256), 0, s, tb.ysl, tb.pos, topk_w, (int)H, out);
+    else if (vec && k == 2)
+        hipLaunchKernelGGL(moe_combine_vec_kernel<2>, vgrid, dim3(256), 0, s, tb.ysl, tb.pos, topk_w, (int)H, out);
+    else
+        hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s,
+                           tb.ysl, tb.pos, topk_w, k, (int)H, out);
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
 }
