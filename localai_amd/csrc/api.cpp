@@ -79,7 +79,7 @@ const uint8_t *qmat_planes(const localai_qmat *cm, hipStream_t s, int *status) {
     localai_qmat *m = const_cast<localai_qmat *>(cm);
     std::lock_guard<std::mutex> lk(g_planes_mu);
     *status = LOCALAI_OK;
-    if (m->data) return m->data;
+    if (uint8_t *d = __atomic_load_n(&m->data, __ATOMIC_ACQUIRE)) return d;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
         *status = fail(LOCALAI_ESTATE, "qmat: this call needs the row planes, which are built on first use; "
@@ -102,7 +102,7 @@ const uint8_t *qmat_planes(const localai_qmat *cm, hipStream_t s, int *status) {
         *status = st;
         return nullptr;
     }
-    m->data = planes;
+    __atomic_store_n(&m->data, planes, __ATOMIC_RELEASE);   // read without the lock elsewhere
     return planes;
 }
 
@@ -262,15 +262,17 @@ int localai_hip_qmat_destroy(localai_qmat *m) {
 
 int64_t localai_hip_qmat_device_bytes(const localai_qmat *m) {
     if (!m) return 0;
-    return (m->data ? m->g.matrix_bytes * m->g.batch : 0) + (m->tiles ? m->tile_bytes * m->g.batch : 0);
+    const uint8_t *planes = __atomic_load_n(&m->data, __ATOMIC_ACQUIRE);
+    return (planes ? m->g.matrix_bytes * m->g.batch : 0) + (m->tiles ? m->tile_bytes * m->g.batch : 0);
 }
 
 int localai_hip_qmat_unpack(const localai_qmat *m, void *out, void *stream) {
     clear_error();
     if (!m || !out) return fail(LOCALAI_EARG, "null pointer");
     if (int st = ensure_device()) return st;
-    if (!m->data) return launch_mt_unpack(m->g, m->tiles, m->tile_bytes, (uint8_t *)out, (hipStream_t)stream);
-    return launch_repack(m->g, m->data, (uint8_t *)out, 1, (hipStream_t)stream);
+    const uint8_t *planes = __atomic_load_n(&m->data, __ATOMIC_ACQUIRE);
+    if (!planes) return launch_mt_unpack(m->g, m->tiles, m->tile_bytes, (uint8_t *)out, (hipStream_t)stream);
+    return launch_repack(m->g, planes, (uint8_t *)out, 1, (hipStream_t)stream);
 }
 
 int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out, void *stream) {
@@ -283,7 +285,8 @@ int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out, 
     one.batch = 1;
     void *tmp = nullptr;
     LQ_HIP(hipMalloc(&tmp, (size_t)one.ggml_matrix_bytes));
-    int st = m->data ? launch_repack(one, m->data + expert * m->g.matrix_bytes, (uint8_t *)tmp, 1, s)
+    const uint8_t *planes = __atomic_load_n(&m->data, __ATOMIC_ACQUIRE);
+    int st = planes ? launch_repack(one, planes + expert * m->g.matrix_bytes, (uint8_t *)tmp, 1, s)
                      : launch_mt_unpack(one, m->tiles + expert * m->tile_bytes, m->tile_bytes, (uint8_t *)tmp, s);
     if (st == LOCALAI_OK) st = launch_dequant_ggml(m->g.type, tmp, one.rows * one.cols, out, s);
     hipError_t e = hipStreamSynchronize(s);
