@@ -78,13 +78,12 @@ int localai_hip_f32_matvec(const float *w_dev, int64_t rows, int64_t cols, const
  * `src_is_device` says whether ggml_bytes is a device address. Types:
  * Q4_0, Q8_0, Q4_K, Q5_K, Q6_K (the reference's native types,
  * engine/native_quant.py:104). cols must be a multiple of the block size.
- * Q4_K and Q6_K handles hold the MFMA tile form only (the same bytes as
- * GGML, reordered); the row-plane form that the several-vector matvec and
- * the fallback MoE paths read is built from it on the first such call
- * (which allocates and waits for the stream, so not under graph capture:
- * LOCALAI_ESTATE there) and then kept. Q8_0 handles hold both forms (the
- * one-vector matvec reads the row planes, the GEMM the tile form); other
- * types hold the row planes. */
+ * Q4_K, Q6_K and Q8_0 handles hold the MFMA tile form only (the same bytes
+ * as GGML, reordered); the row-plane form that the several-vector matvec,
+ * the Q8_0 matvec of rows that are not whole 256-value super-blocks and the
+ * fallback MoE paths read is built from it on the first such call (which
+ * allocates and waits for the stream, so not under graph capture:
+ * LOCALAI_ESTATE there) and then kept. Other types hold the row planes. */
 int localai_hip_qmat_create(int ggml_type, int64_t rows, int64_t cols, int64_t batch,
                             const void *ggml_bytes, int src_is_device, void *stream,
                             localai_qmat **out);

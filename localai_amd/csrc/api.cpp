@@ -202,12 +202,11 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
     m->tiles = nullptr;
     m->tile_bytes = 0;
     hipGetDevice(&m->device);
-    // Q4_K / Q6_K keep only the tile form, which their one-vector matvec,
-    // GEMM and MoE kernels read; the row planes are built on first use
-    // (qmat_planes). Q8_0 keeps both (its one-vector matvec reads the row
-    // planes, its GEMM the tile form); other types keep the row planes.
+    // Q4_K / Q6_K / Q8_0 keep only the tile form, which their one-vector
+    // matvec, GEMM and MoE kernels read; the row planes are built on first
+    // use (qmat_planes). Other types keep the row planes.
     const bool tiled = mfma_matvec_enabled() && mt_matrix_bytes(g) > 0;
-    const bool planes_now = !tiled || g.type == LQ_Q8_0;
+    const bool planes_now = !tiled;
     size_t nbytes = (size_t)(g.matrix_bytes * batch);
     hipError_t e = planes_now ? hipMalloc(&m->data, nbytes) : hipSuccess;
     if (e != hipSuccess) { delete m; return hip_fail(e, "hipMalloc(qmat)"); }
@@ -326,7 +325,7 @@ int localai_hip_matvec_many(int n, const localai_qmat *const *mats, const int64_
     }
     if (int st = ensure_device()) return st;
     hipStream_t s = (hipStream_t)stream;
-    // matrices with a tile form share one MFMA launch; the rest run one by one
+    // Q4_K / Q6_K matrices with a tile form share one MFMA launch; the rest run one by one
     lq_geom geo[8];
     const lq_geom *gp[8];
     const uint8_t *wt[8];
@@ -336,7 +335,10 @@ int localai_hip_matvec_many(int n, const localai_qmat *const *mats, const int64_
         const int64_t e = experts ? experts[j] : 0;
         lq_geom one = mats[j]->g;
         one.batch = 1;
-        if (mats[j]->tiles && mt_matvec_ok(one)) {
+        if (mats[j]->tiles && mt_matvec_ok(one) && one.type == LQ_Q8_0) {
+            // Q8_0 on MFMA, a launch of its own
+            if (int st = launch_matvec_mfma(one, mats[j]->tiles + e * mats[j]->tile_bytes, x, ys[j], s)) return st;
+        } else if (mats[j]->tiles && mt_matvec_ok(one)) {
             geo[nf] = one;
             gp[nf] = &geo[nf];
             wt[nf] = mats[j]->tiles + e * mats[j]->tile_bytes;

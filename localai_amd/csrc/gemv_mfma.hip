@@ -19,9 +19,11 @@ int64_t mt_matrix_bytes(const lq_geom &g) {
 }
 
 // The decode matvec runs on MFMA for Q4_K / Q6_K up to 72 super-blocks per
-// row (the launch plan below); other matrices use gemv.hip.
+// row, and for Q8_0 rows of whole 256-value super-blocks (up to 72 of them),
+// the launch plan below; other matrices use gemv.hip.
 bool mt_matvec_ok(const lq_geom &g) {
-    return (g.type == LQ_Q4_K || g.type == LQ_Q6_K) && g.nb <= 72;
+    return ((g.type == LQ_Q4_K || g.type == LQ_Q6_K) && g.nb <= 72) ||
+           (g.type == LQ_Q8_0 && g.nb % 8 == 0 && g.nb / 8 <= 72);
 }
 
 // GGML <-> tile form, one thread per (matrix, row, super-block); UNPACK
@@ -405,18 +407,19 @@ static MtPlan mt_plan(int nb, int64_t tiles, bool q6) {
     }
 
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s) {
-    if (g.type != LQ_Q4_K && g.type != LQ_Q6_K) return fail(LOCALAI_ETYPE, "mfma matvec: Q4_K / Q6_K only");
+    if (!mt_matvec_ok(g)) return fail(LOCALAI_ETYPE, "mfma matvec: Q4_K / Q6_K, or Q8_0 with cols % 256 == 0");
     if (reinterpret_cast<uintptr_t>(x) & 15) return fail(LOCALAI_EARG, "mfma matvec: x must be 16-byte aligned");
-    const int nb = (int)g.nb;
+    const int nb = (int)mt_nsb(g);   // 256-value super-blocks per row
     if (nb > 72) return fail(LOCALAI_EARG, "mfma matvec: K too large (more than 18432 values)");
-    const bool q6 = g.type == LQ_Q6_K;
+    const bool q6 = g.type == LQ_Q6_K, q8 = g.type == LQ_Q8_0;
     const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
-    const MtPlan p = mt_plan(nb, tiles, q6);
+    const MtPlan p = mt_plan(nb, tiles, q6 || q8);   // one tile per workgroup for the larger blocks
     dim3 grid((unsigned)((tiles + p.rt - 1) / p.rt)), block(64 * p.waves);
     const size_t lds = mt_lds_bytes(g.type, p.waves, p.spw, 1, p.rt);
 #define MT_L(S, R, M, P)                                                                                        \
     do {                                                                                                        \
         if (q6) hipLaunchKernelGGL((gemv_mfma<LQ_Q6_K, S, R, M, P>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y); \
+        else if (q8) hipLaunchKernelGGL((gemv_mfma<LQ_Q8_0, S, R, M, P>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y); \
         else hipLaunchKernelGGL((gemv_mfma<LQ_Q4_K, S, R, M, P>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, y);    \
     } while (0)
     MT_DISPATCH(MT_L)

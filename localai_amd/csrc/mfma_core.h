@@ -55,7 +55,7 @@ __host__ __device__ constexpr int mt_block_bytes(int t) {
 // 256-value blocks per row in the tile form (Q8_0: eight GGML blocks, the
 // last one zero-padded)
 __host__ __device__ inline int64_t mt_nsb(const lq_geom &g) { return g.type == LQ_Q8_0 ? (g.nb + 7) / 8 : g.nb; }
-__host__ __device__ constexpr int mt_xbytes(int t) { return t == LQ_Q4_K ? MT_XBYTES : MT6_XBYTES; }
+__host__ __device__ constexpr int mt_xbytes(int t) { return t == LQ_Q6_K ? MT6_XBYTES : MT_XBYTES; }
 
 // LDS of a workgroup running mt_pass: per-wave x regions, cross-wave partial
 // sums, final row sums
@@ -158,6 +158,7 @@ __device__ __forceinline__ mt_i4 mt_as_i4(uint32_t a, uint32_t b, uint32_t c, ui
 template <int TYPE> struct MtW;
 template <> struct MtW<LQ_Q4_K> { uint4 q0, q1, hd; };
 template <> struct MtW<LQ_Q6_K> { uint4 l0, l1, qh, sc; uint32_t d; };
+template <> struct MtW<LQ_Q8_0> { uint4 p[4], d; };
 
 template <int TYPE>
 __device__ __forceinline__ MtW<TYPE> mt_load_w(const uint8_t *blk, int lane);
@@ -167,6 +168,14 @@ __device__ __forceinline__ MtW<LQ_Q4_K> mt_load_w<LQ_Q4_K>(const uint8_t *blk, i
     w.q0 = ld16(blk + 16 * lane);
     w.q1 = ld16(blk + 1024 + 16 * lane);
     w.hd = ld16(blk + 2048 + 16 * (lane & 15));
+    return w;
+}
+template <>
+__device__ __forceinline__ MtW<LQ_Q8_0> mt_load_w<LQ_Q8_0>(const uint8_t *blk, int lane) {
+    MtW<LQ_Q8_0> w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w.p[i] = ld16(blk + 1024 * i + 16 * lane);
+    w.d = ld16(blk + 4096 + 16 * (lane & 15));
     return w;
 }
 template <>
@@ -185,7 +194,7 @@ __device__ __forceinline__ MtW<LQ_Q6_K> mt_load_w<LQ_Q6_K>(const uint8_t *blk, i
 //   Q6_K: pieces [sub-block 16][piece 4][k / 8: 2][8 B], then per sub-block
 template <int TYPE>
 __device__ __forceinline__ void mt_stage(float4 v, uint8_t *frag, int lane) {
-    if (TYPE == LQ_Q4_K) {
+    if (TYPE == LQ_Q4_K || TYPE == LQ_Q8_0) {   // groups of 32 values (Q8_0: its blocks)
         const int g = lane >> 3;
         const float2 gd = mt_stage_x<8>(v, frag + g * 128 + ((lane & 7) >> 1) * 8 + 4 * (lane & 1), 32);
         if ((lane & 7) == 0) reinterpret_cast<float2 *>(frag + 1024)[g] = gd;
@@ -215,6 +224,10 @@ template <> struct MtLane<LQ_Q6_K> {
     uint32_t lo, hi;
     int aoff, q;
 };
+template <> struct MtLane<LQ_Q8_0> {
+    uint32_t lo[4], hi[4];   // A masks per MFMA
+    int aoff, q;
+};
 
 template <int TYPE>
 __device__ __forceinline__ MtLane<TYPE> mt_lane(int lane);
@@ -235,6 +248,28 @@ __device__ __forceinline__ MtLane<LQ_Q4_K> mt_lane<LQ_Q4_K>(int lane) {
     L.gd = (q >> 1) + 2 * (q & 1);
     return L;
 }
+// Q8_0: MFMA t takes piece t, whose lane group q holds quants 8q .. 8q + 7
+// of blocks 2t (bytes 0..7) and 2t + 1 (bytes 8..15). MFMAs 0, 1 accumulate
+// into D0 and 2, 3 into D1; MFMA t uses A slots 2 (t % 2) (block 2t, low
+// half) and 2 (t % 2) + 1 (block 2t + 1, high half), so A slot s reads block
+// s (MFMAs 0, 1) or s + 4 (MFMAs 2, 3), and D lane group q ends with block q
+// (D0) and q + 4 (D1).
+template <>
+__device__ __forceinline__ MtLane<LQ_Q8_0> mt_lane<LQ_Q8_0>(int lane) {
+    MtLane<LQ_Q8_0> L;
+    const int m = lane & 15, q = lane >> 4, slot = m >> 2, pc = m & 3;
+    const uint32_t on = pc < 3 ? ~0u : 0u;
+    const uint32_t mlo = (slot & 1) ? 0u : on, mhi = (slot & 1) ? on : 0u;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t act = (t & 1) == (slot >> 1) ? ~0u : 0u;
+        L.lo[t] = mlo & act;
+        L.hi[t] = mhi & act;
+    }
+    L.aoff = slot * 128 + pc * 32 + q * 8;
+    L.q = q;
+    return L;
+}
 template <>
 __device__ __forceinline__ MtLane<LQ_Q6_K> mt_lane<LQ_Q6_K>(int lane) {
     MtLane<LQ_Q6_K> L;
@@ -251,6 +286,7 @@ __device__ __forceinline__ MtLane<LQ_Q6_K> mt_lane<LQ_Q6_K>(int lane) {
 template <int TYPE> struct MtA;
 template <> struct MtA<LQ_Q4_K> { mt_i4 A[4]; float2 x0, x1; };
 template <> struct MtA<LQ_Q6_K> { mt_i4 A[4]; float2 xg[4]; };
+template <> struct MtA<LQ_Q8_0> { mt_i4 A[4]; float2 x0, x1; };
 
 template <int TYPE>
 __device__ __forceinline__ MtA<TYPE> mt_load_a(const uint8_t *frag, const MtLane<TYPE> &L);
@@ -265,6 +301,19 @@ __device__ __forceinline__ MtA<LQ_Q4_K> mt_load_a<LQ_Q4_K>(const uint8_t *frag, 
     a.A[3] = mt_place(r1, L.lo[3], L.hi[3]);
     a.x0 = reinterpret_cast<const float2 *>(frag + 1024)[L.gd];
     a.x1 = reinterpret_cast<const float2 *>(frag + 1024)[L.gd + 4];
+    return a;
+}
+template <>
+__device__ __forceinline__ MtA<LQ_Q8_0> mt_load_a<LQ_Q8_0>(const uint8_t *frag, const MtLane<LQ_Q8_0> &L) {
+    MtA<LQ_Q8_0> a;
+    const uint2 r0 = *reinterpret_cast<const uint2 *>(frag + L.aoff);         // block slot
+    const uint2 r1 = *reinterpret_cast<const uint2 *>(frag + L.aoff + 512);   // block slot + 4
+    a.A[0] = mt_place(r0, L.lo[0], L.hi[0]);
+    a.A[1] = mt_place(r0, L.lo[1], L.hi[1]);
+    a.A[2] = mt_place(r1, L.lo[2], L.hi[2]);
+    a.A[3] = mt_place(r1, L.lo[3], L.hi[3]);
+    a.x0 = reinterpret_cast<const float2 *>(frag + 1024)[L.q];
+    a.x1 = reinterpret_cast<const float2 *>(frag + 1024)[L.q + 4];
     return a;
 }
 template <>
@@ -304,6 +353,23 @@ __device__ __forceinline__ float mt_dot<LQ_Q4_K>(const MtW<LQ_Q4_K> &w, const Mt
     const float v = __builtin_fmaf(sc1 * a.x1.y, mt_pieces(D1), sc0 * a.x0.y * mt_pieces(D0));
     const float u = __builtin_fmaf(mn1, a.x1.x, mn0 * a.x0.x);
     return __builtin_fmaf(-dmin, u, __builtin_fmaf(d, v, acc));
+}
+template <>
+__device__ __forceinline__ float mt_dot<LQ_Q8_0>(const MtW<LQ_Q8_0> &w, const MtA<LQ_Q8_0> &a,
+                                                 const MtLane<LQ_Q8_0> &L, float acc) {
+    // the int8 quants are the B operand as they are (engine/dequant.py:75-78)
+    auto B = [](uint4 v) { return mt_as_i4(v.x, v.y, v.z, v.w); };
+    mt_i4 D0 = mt_i4{0, 0, 0, 0}, D1 = mt_i4{0, 0, 0, 0};
+    D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.A[0], B(w.p[0]), D0, 0, 0, 0);
+    D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.A[1], B(w.p[1]), D0, 0, 0, 0);
+    D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.A[2], B(w.p[2]), D1, 0, 0, 0);
+    D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a.A[3], B(w.p[3]), D1, 0, 0, 0);
+    // d of blocks q and q + 4 of the row (f16 pairs in the header words)
+    const uint32_t w0 = (L.q >> 1) ? w.d.y : w.d.x, w1 = (L.q >> 1) ? w.d.w : w.d.z;
+    const int sh = 16 * (L.q & 1);
+    const float d0 = f16_to_f32(w0 >> sh), d1 = f16_to_f32(w1 >> sh);
+    const float v = __builtin_fmaf(d1 * a.x1.y, mt_pieces(D1), d0 * a.x0.y * mt_pieces(D0));
+    return acc + v;
 }
 template <>
 __device__ __forceinline__ float mt_dot<LQ_Q6_K>(const MtW<LQ_Q6_K> &w, const MtA<LQ_Q6_K> &a,

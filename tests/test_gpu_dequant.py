@@ -132,12 +132,12 @@ def test_dequant_every_fp16_scale_pattern(t):
     _nan_aware_equal(got, ref)
 
 
-@pytest.mark.parametrize('t', (12, 14))
+@pytest.mark.parametrize('t', (12, 14, 8))
 def test_tile_form_only_until_row_planes_are_needed(t):
-    """Q4_K / Q6_K handles hold the tile form only (as many bytes as GGML, up
-    to the padding of the last 16-row tile); the first several-vector matvec
-    builds the row planes from it. Results and the GGML bytes read back are
-    the same before and after."""
+    """Q4_K / Q6_K / Q8_0 handles hold the tile form only (as many bytes as
+    GGML, up to the padding of the last 16-row tile); the first
+    several-vector matvec builds the row planes from it. Results and the GGML
+    bytes read back are the same before and after."""
     from localai_amd import device
     rng = np.random.default_rng(500 + t)
     rows, cols, batch = 100, 1024, 2
@@ -145,7 +145,7 @@ def test_tile_form_only_until_row_planes_are_needed(t):
     q = device.QMat.from_ggml(raw, t, rows, cols, batch)
     try:
         before = q.device_bytes
-        tiles = batch * ((rows + 15) // 16) * 16 * (cols // 256) * {12: 144, 14: 210}[t]
+        tiles = batch * ((rows + 15) // 16) * 16 * (cols // 256) * {12: 144, 14: 210, 8: 272}[t]
         assert tiles <= before <= tiles + 256 * batch
         x = rng.standard_normal((3, cols)).astype(np.float32)
         xd = device.to_device_f32(x)

@@ -8,7 +8,8 @@ Q6_K experts run as the one-launch expert kernel (device-side index and skip
 route, localai_hip_moe_experts1); Q8_0 experts take the matvec path with the
 index read on the host; both are checked.
 
-Tolerances: router state normwise <= 1e-6 (exact products, fp32 sums);
+Tolerances: router state normwise <= 5e-6 (its Q8_0 first projection runs on
+i8 MFMA with x in three int8 pieces, about 1e-6; the rest are fp32 sums);
 probabilities within 2e-6 absolute; the expert index equal wherever the
 oracle's best two routes are more than 1e-4 apart (np.exp's own rounding is
 not restated); block output normwise <= 1e-5 (i8 MFMA expert matvecs).
@@ -102,7 +103,7 @@ def test_block_matches_oracle(base, reader):
             h = rng.standard_normal(H).astype(np.float32)
             moe, state = m._moe(1, h, prev)
             w_moe, w_state, w_probs, w_e, margin = zm.moe_block(t, E, EPS, h, prev)
-            assert normwise_rel(state, w_state) < 1e-6
+            assert normwise_rel(state, w_state) < 5e-6
             if margin > 1e-4:
                 assert normwise_rel(moe, w_moe) < 1e-5, step
                 matched += 1
@@ -138,7 +139,7 @@ def test_router_probabilities_and_expert(base):
             np.testing.assert_allclose(probs.cpu().numpy(), w_probs, rtol=0, atol=2e-6)
             # the chosen route's weight: bit for bit probs[expert]
             assert ew.cpu().numpy().view(np.uint32)[0] == probs.cpu().numpy().view(np.uint32)[int(ex.cpu().item())]
-            assert normwise_rel(state.cpu().numpy(), w_state) < 1e-6
+            assert normwise_rel(state.cpu().numpy(), w_state) < 5e-6
             if margin > 1e-4:
                 assert int(ex.cpu().item()) == w_e
 
@@ -163,8 +164,8 @@ def test_skip_route_and_forced_expert(tmp_path, forced, xt):
         assert m._zaya_cache().get(('experts1', 'blk.1.')) is not False
     w_moe, w_state, w_probs, w_e, _ = zm.moe_block(t, E, EPS, h, None)
     assert w_e == forced
-    assert normwise_rel(state, w_state) < 1e-6
-    assert normwise_rel(moe, w_moe) < (1e-6 if forced == E else 1e-5)
+    assert normwise_rel(state, w_state) < 5e-6
+    assert normwise_rel(moe, w_moe) < (5e-6 if forced == E else 1e-5)
 
 
 @pytest.mark.parametrize('forced', [E, 3])
@@ -186,8 +187,8 @@ def test_matvec_path_for_q8_0_experts(tmp_path, forced):
         assert m._zaya_cache().get(('experts1', 'blk.1.')) is False
     w_moe, w_state, _, w_e, _ = zm.moe_block(t, E, EPS, h, None)
     assert w_e == forced
-    assert normwise_rel(state, w_state) < 1e-6
-    assert normwise_rel(moe, w_moe) < (1e-6 if forced == E else 1e-5)
+    assert normwise_rel(state, w_state) < 5e-6
+    assert normwise_rel(moe, w_moe) < (5e-6 if forced == E else 1e-5)
 
 
 @pytest.fixture(scope='module')
