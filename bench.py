@@ -15,6 +15,7 @@ input, weights already resident in HBM, seeded data from localai_amd/synth.py):
       (localai_hip_matvec_many); the one-launch-per-matvec time is reported
       beside it.
   q4k_matvec        one Q4_K matvec at the ffn_gate shape 14336x4096.
+  q8_0_matvec       one Q8_0 matvec at the same shape.
   q8_0_prefill      Q8_0 GEMM 14336x4096 weights x 512 tokens (TFLOP/s).
   zaya_moe_decode   ZAYA-shaped MoE FFN: hidden 2048, 16 experts, top-2,
       intermediate 4096, Q6_K experts, T = 1 (T = 8 reported alongside).
@@ -70,11 +71,11 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFS = 2500.0      # dense f16/bf16 MFMA
 MALL_BYTES = 256 << 20
 METRIC = 'µs/layer + achieved HBM GB/s (% of peak) for Q4_K/Q6_K matvec & MoE layer'
-WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill',
+WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill',
              'llama3_8b_layer_chain', 'llama3_8b_attention_decode', 'qwen35_delta_net_step', 'hbm_read_floor',
              'hbm_copy']
 # the default run: the headline, then these under "workloads"
-DEFAULT_SUITE = ['q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill', 'llama3_8b_layer_chain',
+DEFAULT_SUITE = ['q4k_matvec', 'q8_0_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill', 'llama3_8b_layer_chain',
                  'llama3_8b_attention_decode', 'qwen35_delta_net_step', 'hbm_read_floor']
 
 
@@ -409,11 +410,13 @@ def gate_up_roofline(args, torch, device, gate_host, up_host, x, stream):
             'us_per_launch': round(kms * 1e3, 3), 'bytes_per_launch': nbytes}
 
 
-def gate_roofline(args, torch, device, gate_host, x, stream):
-    """Q4_K matvec at the ffn_gate shape, rotated over > 2x MALL, timed alone."""
-    gate_bytes = 14336 * 16 * 144 + 4 * 4096 + 4 * 14336
-    nrot = rotations(14336 * 16 * 144)
-    gmats = [device.QMat.from_ggml(gate_host, 12, 14336, 4096) for _ in range(nrot)]
+def gate_roofline(args, torch, device, gate_host, x, stream, t=12):
+    """Q4_K (or Q8_0, t = 8) matvec at the ffn_gate shape, rotated over
+    > 2x MALL, timed alone."""
+    wbytes = 14336 * 16 * 144 if t == 12 else 14336 * 128 * 34
+    gate_bytes = wbytes + 4 * 4096 + 4 * 14336
+    nrot = rotations(wbytes)
+    gmats = [device.QMat.from_ggml(gate_host, t, 14336, 4096) for _ in range(nrot)]
     gout = torch.empty(14336, dtype=torch.float32, device=device.device())
     log('timing dominant kernel')
     kms = time_steps(torch, [lambda m=m: m.matvec(x, out=gout, stream=stream) for m in gmats], stream, args.steps,
@@ -421,7 +424,8 @@ def gate_roofline(args, torch, device, gate_host, x, stream):
     achieved = gate_bytes / (kms * 1e-3) / 1e9
     for m in gmats:
         m.close()
-    return {'bound': 'hbm', 'kernel': 'gemv_mfma_q4k 14336x4096', 'achieved': round(achieved, 1),
+    return {'bound': 'hbm', 'kernel': f"gemv_mfma_{'q4k' if t == 12 else 'q8_0'} 14336x4096",
+            'achieved': round(achieved, 1),
             'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4),
             'traffic': measured_traffic('q4k', 'gate'),
             'us_per_launch': round(kms * 1e3, 3), 'bytes_per_launch': gate_bytes}
@@ -461,6 +465,31 @@ def wl_q4k(args, torch, device, synth):
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
             'data': 'synthetic (seeded GGML Q4_K bytes, fp32 N(0,1) x)',
             'config': {'workload': 'q4k_matvec_14336x4096', 'batch': 1, 'algorithmic_bytes': nbytes},
+            'roofline': roof, 'cpu_baseline': cpu}
+
+
+def wl_q8_matvec(args, torch, device, synth):
+    """Q8_0 decode matvec at the ffn_gate shape (the q8_0_row path of a Q8_0
+    model's decode step): i8 MFMA over the Q8_0 tile form."""
+    rng = np.random.default_rng(args.seed)
+    raw = synth.quant_tensor(rng, 8, 14336, 4096)
+    xv = synth.activations(rng, 4096)
+    x = device.to_device_f32(xv)
+    stream = torch.cuda.Stream()
+    roof = gate_roofline(args, torch, device, raw, x, stream, t=8)
+    nbytes = roof['bytes_per_launch']
+    ms = roof['us_per_launch'] / 1e3
+    cpu = None
+    if args.cpu_baseline != 'off' and ref_ok():
+        from oracle import ref
+        th = reference_threads(14336, 8)
+        cpu = cpu_runs(lambda t: ref.matvec(raw, xv, 14336, 4096, 8, threads=th if t is None else t), th, nbytes,
+                       'GB/s', 'calls of localai_q8_0_matvec 14336x4096')
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+            'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
+            'data': 'synthetic (seeded GGML Q8_0 bytes, fp32 N(0,1) x)',
+            'config': {'workload': 'q8_0_matvec_14336x4096', 'batch': 1, 'algorithmic_bytes': nbytes},
             'roofline': roof, 'cpu_baseline': cpu}
 
 
@@ -898,7 +927,8 @@ def wl_copy(args, torch, device, synth):
             'cpu_baseline': None}
 
 
-FUNCS = {'llama3_8b_decode_layer': 'wl_layer', 'q4k_matvec': 'wl_q4k', 'q8_0_prefill': 'wl_q8_prefill',
+FUNCS = {'llama3_8b_decode_layer': 'wl_layer', 'q4k_matvec': 'wl_q4k', 'q8_0_matvec': 'wl_q8_matvec',
+         'q8_0_prefill': 'wl_q8_prefill',
          'zaya_moe_decode': 'wl_zaya', 'qwen3_moe_prefill': 'wl_qwen3', 'llama3_8b_layer_chain': 'wl_chain',
          'hbm_read_floor': 'wl_floor', 'hbm_copy': 'wl_copy', 'llama3_8b_attention_decode': 'wl_attention',
          'qwen35_delta_net_step': 'wl_delta_net'}
