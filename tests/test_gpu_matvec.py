@@ -65,6 +65,19 @@ def test_k_lengths(t, nblocks):
     assert normwise_rel(got, quant.matvec_exact(raw, t, 70, cols, x)) < 1e-5
 
 
+@pytest.mark.parametrize('nsb', (1, 3, 8, 17, 33, 56, 72))
+def test_q8_0_mfma_k_lengths(nsb):
+    """Q8_0 rows of whole 256-value super-blocks take the i8-MFMA matvec over
+    the tile form (every launch plan: 1..32 super-blocks per row at once,
+    33..72 streamed through two register sets); ragged row count."""
+    rng = np.random.default_rng(nsb * 7 + 1)
+    cols = 256 * nsb
+    raw = random_ggml(rng, 8, 70 * cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = gpu_matvec(raw, 8, 70, cols, x)
+    assert normwise_rel(got, quant.matvec_exact(raw, 8, 70, cols, x)) < 1e-5
+
+
 @pytest.mark.parametrize('t', (12, 14, 8))
 @pytest.mark.parametrize('ntok', (1, 2, 3, 5, 8, 11))
 def test_multi_vector(t, ntok):
