@@ -82,14 +82,14 @@ def _stale(owner) -> bool:
 
 
 def _drop(key):
-    q, _ = _cache.pop(key)
-    _cache_bytes[0] -= q.device_bytes
+    q, _, nbytes = _cache.pop(key)
+    _cache_bytes[0] -= nbytes   # as counted on insertion (a handle can grow later)
     q.close()
 
 
 def weights(raw, rows, cols, ggml_type, batch=1):
     """Device handle for GGML bytes `raw` [batch, rows, cols] (cached when immutable)."""
-    for key in [k for k, (_, o) in _cache.items() if _stale(o)]:
+    for key in [k for k, (_, o, _n) in _cache.items() if _stale(o)]:
         _drop(key)
     addr, nbytes = device.host_address(raw)
     key = (addr, nbytes, int(ggml_type), int(batch), int(rows), int(cols))
@@ -99,8 +99,9 @@ def weights(raw, rows, cols, ggml_type, batch=1):
         return hit[0]
     q = device.QMat.from_ggml(raw, ggml_type, rows, cols, batch)
     if _immutable(raw):
-        _cache[key] = (q, _owner(raw))
-        _cache_bytes[0] += q.device_bytes
+        nbytes = q.device_bytes
+        _cache[key] = (q, _owner(raw), nbytes)
+        _cache_bytes[0] += nbytes
         while _cache_bytes[0] > _cache_limit() and len(_cache) > 1:
             _drop(next(iter(_cache)))
     return q
@@ -108,7 +109,7 @@ def weights(raw, rows, cols, ggml_type, batch=1):
 
 def clear_cache():
     while _cache:
-        _, (q, _) = _cache.popitem()
+        _, (q, _, _n) = _cache.popitem()
         q.close()
     _cache_bytes[0] = 0
 
