@@ -258,6 +258,18 @@ int localai_hip_zaya_scale(const float *gu_dev, const float *x_dev, int64_t n, c
 int64_t localai_hip_moe_workspace_size(int64_t tokens, int64_t experts, int top_k,
                                        int64_t hidden, int64_t inter);
 
+/* Where localai_hip_moe_forward leaves its routing tables in the workspace,
+ * for inspection after the call: offs[0..11] = byte offsets of counts[E],
+ * offsets[E + 1], active[E], n_active, perm[N], pos[N] (int32, N = tokens *
+ * top_k; perm lists the assignments t * top_k + s in (expert, assignment)
+ * order, pos is its inverse), then of the expert GEMM tile list tile_e,
+ * tile_p0, tile_n (int32 [offs[10]] each) and n_tiles -- -1 below 32 tokens,
+ * where the layer runs matvecs -- offs[10] = the tile list's capacity and
+ * offs[11] = tokens per tile (0 below 32 tokens).
+ * No counterpart in the reference (its tables live in Python lists). */
+int localai_hip_moe_table_offsets(int64_t tokens, int64_t experts, int top_k, int64_t hidden,
+                                  int64_t inter, int64_t *offs);
+
 /* Top-k MoE FFN layer; composition of engine/zaya.py:274-307 (router, softmax,
  * expert selection with ties to the lower index, SiLU*up, weighted combine)
  * and engine/zaya.py:139-175 (expert = byte slice of a 3-D tensor):

@@ -40,6 +40,7 @@ SIGNATURES = {
                                          _vp, _c_i64, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     'localai_hip_zaya_scale': (_c_int, [_vp, _vp, _c_i64, _vp, _vp, _vp]),
     'localai_hip_moe_workspace_size': (_c_i64, [_c_i64, _c_i64, _c_int, _c_i64, _c_i64]),
+    'localai_hip_moe_table_offsets': (_c_int, [_c_i64, _c_i64, _c_int, _c_i64, _c_i64, _vp]),
     'localai_hip_moe_experts1': (_c_int, [_vp, _c_i64, _vp, _vp, _c_int, _vp, _vp, ctypes.c_int32, _vp, _vp, _c_i64,
                                           _vp]),
     'localai_hip_moe_forward': (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp, _vp,

@@ -523,6 +523,17 @@ int64_t localai_hip_moe_workspace_size(int64_t T, int64_t E, int k, int64_t H, i
     return (int64_t)moe_workspace_bytes(T, E, k, H, I);
 }
 
+int localai_hip_moe_table_offsets(int64_t T, int64_t E, int k, int64_t H, int64_t I, int64_t *offs) {
+    clear_error();
+    if (T < 1 || E < 1 || k < 1 || H < 1 || I < 1 || !offs)
+        return fail(LOCALAI_EARG, "moe table offsets: sizes must be >= 1 and offs not null");
+    const MoeLayout L = moe_layout(T, E, k, H, I);
+    const int64_t v[12] = {L.counts, L.offsets, L.active, L.n_active, L.perm,  L.pos,
+                           L.tile_e, L.tile_p0, L.tile_n, L.n_tiles, L.max_tiles, L.max_tiles > 0 ? moe_gemm_tile() : 0};
+    for (int i = 0; i < 12; ++i) offs[i] = v[i];
+    return LOCALAI_OK;
+}
+
 int localai_hip_moe_forward(const float *h, int64_t T, int64_t H, const float *rw, const float *rb,
                             int64_t E, int k, const localai_qmat *gu, const localai_qmat *dn, float *out,
                             int32_t *topk_idx, float *topk_w, void *ws, int64_t ws_bytes, void *stream) {

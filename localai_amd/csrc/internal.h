@@ -108,6 +108,12 @@ int launch_zaya_router_tail(const float *r0, const float *b0, const float *prev,
                             hipStream_t s);
 int launch_zaya_scale(const float *gu, const float *x, int64_t n, const float *scale, float *y, hipStream_t s);
 
+struct MoeLayout {
+    int64_t logits, sync, counts, offsets, active, n_active, perm, pos, act, ysl;
+    int64_t tile_e, tile_p0, tile_n, n_tiles, xh_gu, inv_gu, xh_dn, inv_dn;
+    int64_t max_tiles, bytes;
+};
+MoeLayout moe_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I);
 size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I);
 int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const float *rb, int64_t E, int k,
                const localai_qmat *gu, const localai_qmat *dn, float *out, int32_t *topk_idx, float *topk_w,

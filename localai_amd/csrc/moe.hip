@@ -544,70 +544,129 @@ __device__ __forceinline__ uint64_t match_lanes(int e, bool live, int nbits) {
     return m;
 }
 
+// Inclusive sum over the 64 lanes: DPP shifts inside each row of 16 lanes,
+// then the totals of the rows below (read from lanes 15, 31, 47).
+__device__ __forceinline__ int wave_incl_sum(int v, int lane) {
+    const int r = lane & 15;
+    int t;
+    t = (int)dpp_u32<0x111>((uint32_t)v); if (r >= 1) v += t;
+    t = (int)dpp_u32<0x112>((uint32_t)v); if (r >= 2) v += t;
+    t = (int)dpp_u32<0x114>((uint32_t)v); if (r >= 4) v += t;
+    t = (int)dpp_u32<0x118>((uint32_t)v); if (r >= 8) v += t;
+    const int s0 = __builtin_amdgcn_readlane(v, 15), s1 = __builtin_amdgcn_readlane(v, 31);
+    const int s2 = __builtin_amdgcn_readlane(v, 47);
+    return v + (lane >= 16 ? s0 : 0) + (lane >= 32 ? s1 : 0) + (lane >= 48 ? s2 : 0);
+}
+
+constexpr int PERM_WAVES = 16;              // the permute's workgroup: 1024 threads
+constexpr size_t PERM_LDS_MAX = 65536;
+
+// LDS of the permute: cnt[16][E] and off[E + 1] ints, then (8-byte aligned)
+// a region that holds first the wave-private lane masks [16][E] (u64, when
+// `match`) and then the staged perm[N] (ints, when `stage`).
+static inline size_t perm_lds_head(int64_t E) { return (size_t)((17 * E + 2) & ~1) * 4; }
+static inline size_t perm_lds_bytes(int64_t E, int64_t N, bool match, bool stage) {
+    const size_t a = match ? (size_t)(PERM_WAVES * E) * 8 : 0, b = stage ? (size_t)N * 4 : 0;
+    return perm_lds_head(E) + (a > b ? a : b);
+}
+
 // Stable counting sort of the N assignments by expert in one workgroup of
 // 1024 threads. Wave w owns the contiguous range [w per, (w+1) per):
-//   1. per 64 assignments, the lanes with equal experts are matched by
-//      ballots; an assignment's rank among its expert's assignments so far in
-//      the wave is kept (in registers, or in pos[] as scratch until step 4
-//      for long ranges) and the wave's per-expert counts advance in LDS;
-//   2. each expert's wave counts become exclusive bases in wave order;
+//   1. per 64 assignments, the lanes with equal experts are matched -- MATCH:
+//      every lane ORs its bit into the wave's LDS mask of its expert and reads
+//      the mask back; else one ballot per expert-index bit. An assignment's
+//      rank among its expert's assignments so far in the wave is kept (in
+//      registers, or in pos[] as scratch until step 4 for long ranges) and the
+//      wave's per-expert counts advance in LDS;
+//   2. each expert's wave counts become exclusive bases in wave order (eight
+//      lanes per expert, two waves each);
 //   3. wave 0 scans the expert totals (lane l owns a contiguous run of
 //      experts): offsets, counts, the active list and, for the expert GEMMs,
 //      the tile list (tiles of tile_w consecutive perm positions per expert);
-//   4. every assignment lands at offset[e] + wave base + rank.
+//   4. every assignment lands at offset[e] + wave base + rank -- STAGE: in
+//      LDS, copied out to perm[] in order afterwards (the scattered stores stay
+//      off the one CU's address path).
 // The result lists the assignments in (expert, a) order.
+template <bool MATCH, bool STAGE>
 __global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__restrict__ idx, int N, int E,
                                                            MoeTables tb) {
-    extern __shared__ int ws[];            // cnt[16][E], off[E + 1]
+    extern __shared__ __align__(16) int ws[];
     constexpr int U = 8;                   // assignments per lane per batch of loads
-    const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
+    const int lane = lane_id(), w = wave_id();
     int *cnt = ws;
-    int *off = ws + 16 * E;
-    for (int i = threadIdx.x; i < 16 * E; i += blockDim.x) cnt[i] = 0;
-    // the fused one-token kernel's counter block, whose error word
-    // localai_hip_moe_error reads, is unused on the paths that permute
-    for (int i = threadIdx.x; i < D1_WORDS; i += blockDim.x) tb.sync[i] = 0u;
-    __syncthreads();
-    const int nbits = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 0;
-    const int per = (N + nw - 1) / nw;
+    int *off = ws + PERM_WAVES * E;
+    const int head = (17 * E + 2) & ~1;
+    uint64_t *masks = reinterpret_cast<uint64_t *>(ws + head);
+    int *stage = ws + head;
+    const int per = (N + PERM_WAVES - 1) / PERM_WAVES;
     const int a0 = min(N, w * per), a1 = min(N, a0 + per);
-    int *wc = cnt + w * E;
     // a wave range of at most 64 U assignments stays in registers (ev, rv)
     // until step 4; longer ranges keep the ranks in pos[]
     const bool held = a1 - a0 <= 64 * U;
     int ev[U], rv[U];
-    for (int base = a0; base < a1; base += 64 * U) {
+    // expert ids of the first batch, requested before the LDS is cleared
+    // (every load is in bounds; lanes past a1 are masked where used)
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int a = base + 64 * u + lane;
-            ev[u] = a < a1 ? idx[a] : 0;
+    for (int u = 0; u < U; ++u) ev[u] = idx[min(a0 + 64 * u + lane, N - 1)];
+    for (int i = threadIdx.x; i < PERM_WAVES * E; i += blockDim.x) cnt[i] = 0;
+    if constexpr (MATCH)
+        for (int i = threadIdx.x; i < PERM_WAVES * E; i += blockDim.x) masks[i] = 0ull;
+    __syncthreads();
+    const int nbits = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 0;
+    int *wc = cnt + w * E;
+    uint64_t *wm = masks + w * E;
+    for (int base = a0; base < a1; base += 64 * U) {
+        if (base != a0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) ev[u] = idx[min(base + 64 * u + lane, N - 1)];
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (base + 64 * u >= a1) break;   // uniform
             const int a = base + 64 * u + lane;
             const bool live = a < a1;
-            const uint64_t m = match_lanes(ev[u], live, nbits);
+            const int e = ev[u];
+            uint64_t m;
+            if constexpr (MATCH) {
+                if (live) __hip_atomic_fetch_or(wm + e, 1ull << lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                m = live ? __hip_atomic_load(wm + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT) : 0ull;
+            } else {
+                m = match_lanes(e, live, nbits);
+            }
             const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-            const int before = live ? wc[ev[u]] : 0;
+            const int before = live ? wc[e] : 0;
             rv[u] = before + rank;
             if (live && !held) tb.pos[a] = rv[u];
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
             __builtin_amdgcn_wave_barrier();
-            // the highest matching lane advances the expert's count
-            if (live && (m >> lane) == 1) wc[ev[u]] = rv[u] + 1;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            // the highest matching lane advances the expert's count (and
+            // clears its mask), after every lane has read both
+            if (live && (m >> lane) == 1) {
+                wc[e] = before + __builtin_popcountll(m);
+                if constexpr (MATCH) wm[e] = 0ull;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
             __builtin_amdgcn_wave_barrier();
         }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        int r = 0;
-        for (int ww = 0; ww < nw; ++ww) {
-            const int c = cnt[ww * E + e];
-            cnt[ww * E + e] = r;           // exclusive within the expert, wave order
-            r += c;
+    // step 2: lane j of the eight of expert e takes waves 2j and 2j + 1
+    for (int eb = 0; eb < E; eb += 128) {
+        const int e = eb + (int)(threadIdx.x >> 3), j = (int)(threadIdx.x & 7);
+        const bool ok = e < E;
+        const int c0 = ok ? cnt[2 * j * E + e] : 0, c1 = ok ? cnt[(2 * j + 1) * E + e] : 0;
+        const int s = c0 + c1;
+        int incl = s, t;
+        t = (int)dpp_u32<0x111>((uint32_t)incl); if (j >= 1) incl += t;
+        t = (int)dpp_u32<0x112>((uint32_t)incl); if (j >= 2) incl += t;
+        t = (int)dpp_u32<0x114>((uint32_t)incl); if (j >= 4) incl += t;
+        if (ok) {
+            cnt[2 * j * E + e] = incl - s;           // exclusive within the expert, wave order
+            cnt[(2 * j + 1) * E + e] = incl - s + c0;
+            if (j == 7) off[e] = incl;               // the expert's total until the scan below
         }
-        off[e] = r;                        // the expert's total until the scan below
     }
     __syncthreads();
     if (w == 0) {
@@ -621,13 +680,9 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__rest
             sa += c > 0;
             if (tw > 0) st += (c + tw - 1) / tw;
         }
-        // inclusive scan over the lanes, then exclusive starts of this lane's run
-        int io = so, ia = sa, it = st;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int po = __shfl_up(io, d, 64), pa = __shfl_up(ia, d, 64), pt = __shfl_up(it, d, 64);
-            if (lane >= d) { io += po; ia += pa; it += pt; }
-        }
+        // inclusive sums over the lanes, then exclusive starts of this lane's run
+        const int io = wave_incl_sum(so, lane), ia = wave_incl_sum(sa, lane);
+        const int it = tw > 0 ? wave_incl_sum(st, lane) : 0;
         int o = io - so, na = ia - sa, nt = it - st;
         for (int e = e0; e < e1; ++e) {
             const int c = off[e];
@@ -655,9 +710,9 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__rest
         if (!held) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int a = base + 64 * u + lane;
-                ev[u] = a < a1 ? idx[a] : 0;
-                rv[u] = a < a1 ? tb.pos[a] : 0;
+                const int a = min(base + 64 * u + lane, N - 1);
+                ev[u] = idx[a];
+                rv[u] = tb.pos[a];
             }
         }
 #pragma unroll
@@ -665,10 +720,20 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__rest
             const int a = base + 64 * u + lane;
             if (a < a1) {
                 const int p = off[ev[u]] + wc[ev[u]] + rv[u];
-                tb.perm[p] = a;
+                if constexpr (STAGE)
+                    stage[p] = a;
+                else
+                    tb.perm[p] = a;
                 tb.pos[a] = p;
             }
         }
+    }
+    // the fused one-token kernel's counter block, whose error word
+    // localai_hip_moe_error reads, is unused on the paths that permute
+    for (int i = threadIdx.x; i < D1_WORDS; i += blockDim.x) tb.sync[i] = 0u;
+    if constexpr (STAGE) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < N; i += blockDim.x) tb.perm[i] = stage[i];
     }
 }
 
@@ -1016,51 +1081,70 @@ static int64_t moe_max_tiles(int64_t N, int64_t E, int tile_w) {
 // f16 token rows, zero-padded to a multiple of 256 values (gemm.hip)
 static int64_t f16_stride(int64_t cols) { return 256 * ((cols + 255) / 256); }
 
-size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
+// Byte offsets of the workspace's tables, each 256-byte aligned (the expert
+// GEMM tables only from MOE_GEMM_TOKENS tokens on; -1 otherwise).
+MoeLayout moe_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
     const int64_t N = T * k;
-    size_t s = 0;
-    s += align256(T * E * 4);                                        // logits
-    s += 1024;                                                       // fused-layer counters
-    s += align256(E * 4) * 2 + align256((E + 1) * 4) + align256(4);  // counts, offsets, active, n_active
-    s += align256(N * 4) * 2;                                        // perm, pos
-    s += align256(N * I * 4);                                        // act
-    s += align256(N * H * 4);                                        // ysl
+    MoeLayout L;
+    int64_t p = 0;
+    auto take = [&](int64_t n) { const int64_t q = p; p += (int64_t)align256((size_t)n); return q; };
+    L.logits = take(T * E * 4);
+    L.sync = take(D1_WORDS * 4);
+    L.counts = take(E * 4);
+    L.offsets = take((E + 1) * 4);
+    L.active = take(E * 4);
+    L.n_active = take(4);
+    L.perm = take(N * 4);
+    L.pos = take(N * 4);
+    L.act = take(N * I * 4);
+    L.ysl = take(N * H * 4);
+    L.max_tiles = 0;
+    L.tile_e = L.tile_p0 = L.tile_n = L.n_tiles = L.xh_gu = L.inv_gu = L.xh_dn = L.inv_dn = -1;
     if (T >= MOE_GEMM_TOKENS) {
-        const int64_t mt = moe_max_tiles(N, E, moe_gemm_tile());
-        s += align256(mt * 4) * 3 + align256(4);
-        s += align256(T * f16_stride(H) * 2) + align256(T * 4);      // f16 rows of h
-        s += align256(N * f16_stride(I) * 2) + align256(N * 4);      // f16 act rows
+        L.max_tiles = moe_max_tiles(N, E, moe_gemm_tile());
+        L.tile_e = take(L.max_tiles * 4);
+        L.tile_p0 = take(L.max_tiles * 4);
+        L.tile_n = take(L.max_tiles * 4);
+        L.n_tiles = take(4);
+        L.xh_gu = take(T * f16_stride(H) * 2);
+        L.inv_gu = take(T * 4);
+        L.xh_dn = take(N * f16_stride(I) * 2);
+        L.inv_dn = take(N * 4);
     }
-    return s;
+    L.bytes = p;
+    return L;
+}
+
+size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
+    return (size_t)moe_layout(T, E, k, H, I).bytes;
 }
 
 static MoeTables carve(void *ws, int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
-    const int64_t N = T * k;
+    const MoeLayout L = moe_layout(T, E, k, H, I);
     uint8_t *p = (uint8_t *)ws;
     MoeTables tb{};
-    auto take = [&](size_t n) { uint8_t *q = p; p += align256(n); return q; };
-    tb.logits = (float *)take(T * E * 4);
-    tb.sync = (uint32_t *)take(D1_WORDS * 4);
-    tb.counts = (int32_t *)take(E * 4);
-    tb.offsets = (int32_t *)take((E + 1) * 4);
-    tb.active = (int32_t *)take(E * 4);
-    tb.n_active = (int32_t *)take(4);
-    tb.perm = (int32_t *)take(N * 4);
-    tb.pos = (int32_t *)take(N * 4);
-    tb.act = (float *)take(N * I * 4);
-    tb.ysl = (float *)take(N * H * 4);
+    tb.logits = (float *)(p + L.logits);
+    tb.sync = (uint32_t *)(p + L.sync);
+    tb.counts = (int32_t *)(p + L.counts);
+    tb.offsets = (int32_t *)(p + L.offsets);
+    tb.active = (int32_t *)(p + L.active);
+    tb.n_active = (int32_t *)(p + L.n_active);
+    tb.perm = (int32_t *)(p + L.perm);
+    tb.pos = (int32_t *)(p + L.pos);
+    tb.act = (float *)(p + L.act);
+    tb.ysl = (float *)(p + L.ysl);
     tb.tile_w = 0;
-    if (T >= MOE_GEMM_TOKENS) {
+    if (L.max_tiles > 0) {
         tb.tile_w = moe_gemm_tile();
-        tb.max_tiles = (int)moe_max_tiles(N, E, tb.tile_w);
-        tb.tile_e = (int32_t *)take(tb.max_tiles * 4);
-        tb.tile_p0 = (int32_t *)take(tb.max_tiles * 4);
-        tb.tile_n = (int32_t *)take(tb.max_tiles * 4);
-        tb.n_tiles = (int32_t *)take(4);
-        tb.xh_gu = (_Float16 *)take(T * f16_stride(H) * 2);
-        tb.inv_gu = (float *)take(T * 4);
-        tb.xh_dn = (_Float16 *)take(N * f16_stride(I) * 2);
-        tb.inv_dn = (float *)take(N * 4);
+        tb.max_tiles = (int)L.max_tiles;
+        tb.tile_e = (int32_t *)(p + L.tile_e);
+        tb.tile_p0 = (int32_t *)(p + L.tile_p0);
+        tb.tile_n = (int32_t *)(p + L.tile_n);
+        tb.n_tiles = (int32_t *)(p + L.n_tiles);
+        tb.xh_gu = (_Float16 *)(p + L.xh_gu);
+        tb.inv_gu = (float *)(p + L.inv_gu);
+        tb.xh_dn = (_Float16 *)(p + L.xh_dn);
+        tb.inv_dn = (float *)(p + L.inv_dn);
     }
     return tb;
 }
@@ -1187,7 +1271,7 @@ int set_fused_wait(int spin, int count) {
 }
 
 int moe_error_word(const void *ws, int64_t T, int64_t E, hipStream_t s, uint32_t *word) {
-    const uint32_t *sync = (const uint32_t *)((const uint8_t *)ws + align256((size_t)(T * E * 4)));
+    const uint32_t *sync = (const uint32_t *)((const uint8_t *)ws + moe_layout(T, E, 1, 1, 1).sync);
     LQ_HIP(hipStreamSynchronize(s));
     LQ_HIP(hipMemcpy(word, sync + D1_ERROR, 4, hipMemcpyDeviceToHost));
     return LOCALAI_OK;
@@ -1289,8 +1373,17 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
     }
     LQ_HIP(hipGetLastError());
     if (!one) {
-        size_t sh2 = (size_t)(17 * E + 1) * 4;
-        hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), sh2, s, topk_idx, (int)(T * k), (int)E, tb);
+        const int64_t N = T * k;
+        const bool match = perm_lds_bytes(E, N, true, false) <= PERM_LDS_MAX;
+        const bool stage = perm_lds_bytes(E, N, match, true) <= PERM_LDS_MAX;
+        const size_t sh2 = perm_lds_bytes(E, N, match, stage);
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(1), dim3(1024), sh2, s, topk_idx, (int)N, (int)E, tb);
+        };
+        if (match)
+            stage ? go(moe_permute_kernel<true, true>) : go(moe_permute_kernel<true, false>);
+        else
+            stage ? go(moe_permute_kernel<false, true>) : go(moe_permute_kernel<false, false>);
         LQ_HIP(hipGetLastError());
     }
     const int slots = (int)(E < T * k ? E : T * k);

@@ -86,6 +86,30 @@ class MoELayer:
             raise ValueError(f'no forward over {tokens} tokens yet')
         return ws[:tokens * self.E * 4].view(device.torch().float32).reshape(tokens, self.E)
 
+    def last_tables(self, tokens):
+        """Routing tables of the last forward over `tokens` tokens, as numpy
+        int32 arrays: counts, offsets, active (n_active of them), perm, pos and,
+        from 32 tokens on, the expert GEMM tiles (tile_e, tile_p0, tile_n) and
+        their width tile_w."""
+        ws = self._ws.get(tokens)
+        if ws is None:
+            raise ValueError(f'no forward over {tokens} tokens yet')
+        offs = (ctypes.c_int64 * 12)()
+        _lib.check(_lib.load().localai_hip_moe_table_offsets(tokens, self.E, self.k, self.H, self.I, offs))
+        host = ws.cpu().numpy()
+        E, N = self.E, tokens * self.k
+
+        def ints(i, n):
+            return host[offs[i]:offs[i] + 4 * n].view(np.int32).copy()
+
+        t = {'counts': ints(0, E), 'offsets': ints(1, E + 1), 'perm': ints(4, N), 'pos': ints(5, N)}
+        t['active'] = ints(2, int(ints(3, 1)[0]))
+        if offs[9] >= 0:
+            nt = int(ints(9, 1)[0])
+            t['tile_e'], t['tile_p0'], t['tile_n'] = ints(6, nt), ints(7, nt), ints(8, nt)
+            t['tile_w'] = int(offs[11])
+        return t
+
     def check(self, tokens, stream=None):
         """Wait for `stream` and raise if the last forward over `tokens` tokens
         ran the fused one-token expert kernel and one of its device-side checks

@@ -322,3 +322,56 @@ def test_fused_wait_that_runs_out_is_reported():
     (o, i, g), (ro, ri, rg) = run_both(rw, gu, dn, 14, E, H, I, k, h)
     np.testing.assert_array_equal(i, ri)
     assert normwise_rel(o, ro) < 1e-5
+
+
+def expected_tables(idx, E, tile_w):
+    """Stable counting sort of the flat assignments a = t * k + s by expert,
+    its inverse, per-expert counts / offsets / active list and the expert GEMM
+    tiles (runs of tile_w perm positions per expert)."""
+    flat = idx.reshape(-1).astype(np.int64)
+    perm = np.argsort(flat, kind='stable').astype(np.int32)
+    pos = np.empty_like(perm)
+    pos[perm] = np.arange(perm.size, dtype=np.int32)
+    counts = np.bincount(flat, minlength=E).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    want = {'counts': counts, 'offsets': offsets, 'active': np.flatnonzero(counts).astype(np.int32),
+            'perm': perm, 'pos': pos}
+    if tile_w:
+        te, tp, tn = [], [], []
+        for e in np.flatnonzero(counts):
+            for p in range(0, counts[e], tile_w):
+                te.append(e)
+                tp.append(offsets[e] + p)
+                tn.append(min(tile_w, counts[e] - p))
+        want.update(tile_e=np.array(te, np.int32), tile_p0=np.array(tp, np.int32), tile_n=np.array(tn, np.int32))
+    return want
+
+
+@pytest.mark.parametrize('E,T,k', [
+    (16, 1, 2),        # one token: the router writes the tables
+    (1, 40, 1),        # one expert: every assignment matches
+    (16, 31, 4),       # matvec path (no tiles), sixteen waves of eight assignments or fewer
+    (128, 512, 8),     # lane masks in LDS, ranks in registers, perm staged in LDS
+    (128, 1100, 8),    # wave ranges past 512 assignments: ranks kept in pos[] between steps
+    (64, 2200, 8),     # perm too large to stage: scattered stores
+    (512, 200, 8),     # too many experts for the LDS lane masks: ballots
+    (1024, 40, 2),     # the largest expert count
+])
+def test_routing_tables_are_a_stable_sort(E, T, k):
+    """perm lists the assignments in (expert, a) order, pos inverts it, and
+    counts / offsets / active / tiles follow, for every variant of the
+    permutation kernel. Random router weights with a Zipf bias make some
+    experts crowded and others empty."""
+    from localai_amd import synth
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(E * 31 + T)
+    H, I, t = 256, 128, 8
+    rw, gu, dn = make_layer(rng, E, H, I, t, scale=0.05)
+    layer = MoELayer(rw, gu, dn, t, E, H, I, k, router_b=synth.zipf_bias(E) if E > 1 else None)
+    h = synth.activations(rng, T, H)
+    _, idx, _ = layer.forward(h)
+    got = layer.last_tables(T)
+    want = expected_tables(idx, E, got.get('tile_w', 0))
+    assert ('tile_e' in got) == (T >= 32)
+    for name, w in want.items():
+        np.testing.assert_array_equal(got[name], w, err_msg=name)
