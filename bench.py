@@ -773,6 +773,14 @@ def wl_floor(args, torch, device, synth):
     ms = time_steps(torch, [lambda b=b: read(b, 0, 33030144) for b in bufs], stream, args.steps, args.warmup)
     res['one_launch_33MB'] = {'us': round(ms * 1e3, 3), 'GB/s': round(33030144 / (ms * 1e-3) / 1e9, 1),
                               'frac': round(33030144 / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    # each of the four alone: the floor of that launch of the chain
+    res['per_launch_us'] = {}
+    off = 0
+    for name in ('qkv', 'o', 'gate_up', 'down'):
+        ms = time_steps(torch, [lambda b=b, o=off, n=segs[name]: read(b, o, n) for b in bufs], stream, args.steps,
+                        args.warmup)
+        res['per_launch_us'][name] = round(ms * 1e3, 3)
+        off += segs[name]
     ms = time_steps(torch, [lambda b=b: per_layer_chain(b) for b in bufs], stream, args.steps, args.warmup)
     res['layer_as_four_launches'] = {'us': round(ms * 1e3, 3), 'GB/s': round(layer / (ms * 1e-3) / 1e9, 1),
                                      'frac': round(layer / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

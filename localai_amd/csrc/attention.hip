@@ -111,6 +111,14 @@ __device__ __forceinline__ void ldv(const float *p, float (&v)[N]) {
     const typename AttnVec<N>::T t = *reinterpret_cast<const typename AttnVec<N>::T *>(p);
     __builtin_memcpy(&v[0], &t, sizeof(t));
 }
+// the same for cache rows, which a decode step reads once (nontemporal hint)
+template <int N> struct AttnNt { typedef float T __attribute__((ext_vector_type(N))); };
+template <> struct AttnNt<1> { typedef float T; };
+template <int N>
+__device__ __forceinline__ void ldv_nt(const float *p, float (&v)[N]) {
+    const typename AttnNt<N>::T t = __builtin_nontemporal_load(reinterpret_cast<const typename AttnNt<N>::T *>(p));
+    __builtin_memcpy(&v[0], &t, sizeof(t));
+}
 template <int N>
 __device__ __forceinline__ void stv(float *p, const float (&v)[N]) {
     typename AttnVec<N>::T t;
@@ -151,7 +159,11 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
         const bool own = s == a.position && a.k_new;
         const float *kp = own ? a.k_new + (int64_t)kh * hd : a.kc + (valid[r] ? s : a.start) * row + (int64_t)kh * hd;
 #pragma unroll
-        for (int j = 0; j < NV; ++j) kv[r][j] = ld4(kp + ATTN_PIECE * j + 4 * c);
+        for (int j = 0; j < NV; ++j) {
+            float t[4];
+            ldv_nt<4>(kp + ATTN_PIECE * j + 4 * c, t);
+            kv[r][j] = make_float4(t[0], t[1], t[2], t[3]);
+        }
     }
     float vv[P][NV];
 #pragma unroll
@@ -160,7 +172,7 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
         const bool own = s == a.position && a.k_new;
         const float *vp = own ? a.v_new + (int64_t)kh * hd
                               : a.vc + (s <= a.position ? s : a.start) * row + (int64_t)kh * hd;
-        ldv<NV>(vp + NV * lane, vv[i]);
+        ldv_nt<NV>(vp + NV * lane, vv[i]);
     }
     // scores in base-2 units (scale = log2(e) / sqrt(head_dim)): the 16
     // lanes of a position each hold 4 NV products

@@ -32,6 +32,12 @@ namespace lq {
 typedef float lq_float2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+// 16 bytes read once (nontemporal hint)
+__device__ __forceinline__ uint4 ld16_nt(const uint8_t *p) {
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
 __device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 
 // sum_i code_i * x[i] over the 16 nibble codes in q (bytes 0..15, each < 16),
@@ -153,34 +159,34 @@ __device__ __forceinline__ UnitW load_unit_w(const uint8_t *__restrict__ W, cons
     const uint8_t *p1 = W + g.plane[1] + row * g.pitch[1];
     const int c0 = u & ~63, i = u - c0;
     if constexpr (T == LQ_Q4_K) {
-        w.q0 = ld16(p0 + 16 * (2 * c0 + i));
-        w.q1 = ld16(p0 + 16 * (2 * c0 + C + i));
+        w.q0 = ld16_nt(p0 + 16 * (2 * c0 + i));
+        w.q1 = ld16_nt(p0 + 16 * (2 * c0 + C + i));
         w.h0 = ld16(p1 + 16 * (u >> 2));
     } else if constexpr (T == LQ_Q5_K) {
         const uint8_t *p2 = W + g.plane[2] + row * g.pitch[2];
         const int sb = u >> 2, s0 = c0 >> 2, cs = C >> 2;
-        w.q0 = ld16(p0 + 16 * (2 * c0 + i));
-        w.q1 = ld16(p0 + 16 * (2 * c0 + C + i));
+        w.q0 = ld16_nt(p0 + 16 * (2 * c0 + i));
+        w.q1 = ld16_nt(p0 + 16 * (2 * c0 + C + i));
         w.h1 = ld16(p1 + 16 * (2 * s0 + (sb - s0)));        // qh[0..15]
-        w.q2 = ld16(p1 + 16 * (2 * s0 + cs + (sb - s0)));   // qh[16..31]
+        w.q2 = ld16_nt(p1 + 16 * (2 * s0 + cs + (sb - s0)));   // qh[16..31]
         w.h0 = ld16(p2 + 16 * sb);
     } else if constexpr (T == LQ_Q6_K) {
         const uint8_t *p2 = W + g.plane[2] + row * g.pitch[2];
         const uint8_t *p3 = W + g.plane[3] + row * g.pitch[3];
-        w.q0 = ld16(p0 + 16 * (2 * c0 + i));                // ql[16m .. 16m+15] of half h
-        w.q1 = ld16(p0 + 16 * (2 * c0 + C + i));            // ql[32+16m ..]
+        w.q0 = ld16_nt(p0 + 16 * (2 * c0 + i));                // ql[16m .. 16m+15] of half h
+        w.q1 = ld16_nt(p0 + 16 * (2 * c0 + C + i));            // ql[32+16m ..]
         w.h0 = ld16(p1 + 16 * u);                           // qh[16m ..] of half h
         w.sc = ld4(p2 + 4 * u);
         w.d = *reinterpret_cast<const uint16_t *>(p3 + 2 * (u >> 2));
     } else if constexpr (T == LQ_Q8_0) {
-        w.q0 = ld16(p0 + 16 * (4 * c0 + i));
-        w.q1 = ld16(p0 + 16 * (4 * c0 + C + i));
-        w.q2 = ld16(p0 + 16 * (4 * c0 + 2 * C + i));
-        w.q3 = ld16(p0 + 16 * (4 * c0 + 3 * C + i));
+        w.q0 = ld16_nt(p0 + 16 * (4 * c0 + i));
+        w.q1 = ld16_nt(p0 + 16 * (4 * c0 + C + i));
+        w.q2 = ld16_nt(p0 + 16 * (4 * c0 + 2 * C + i));
+        w.q3 = ld16_nt(p0 + 16 * (4 * c0 + 3 * C + i));
         w.sc = ld4(p1 + 4 * u);
     } else {   // Q4_0
-        w.q0 = ld16(p0 + 16 * (2 * c0 + i));
-        w.q1 = ld16(p0 + 16 * (2 * c0 + C + i));
+        w.q0 = ld16_nt(p0 + 16 * (2 * c0 + i));
+        w.q1 = ld16_nt(p0 + 16 * (2 * c0 + C + i));
         w.sc = ld4(p1 + 4 * u);
     }
     return w;

@@ -165,8 +165,8 @@ __device__ __forceinline__ MtW<TYPE> mt_load_w(const uint8_t *blk, int lane);
 template <>
 __device__ __forceinline__ MtW<LQ_Q4_K> mt_load_w<LQ_Q4_K>(const uint8_t *blk, int lane) {
     MtW<LQ_Q4_K> w;
-    w.q0 = ld16(blk + 16 * lane);
-    w.q1 = ld16(blk + 1024 + 16 * lane);
+    w.q0 = ld16_nt(blk + 16 * lane);
+    w.q1 = ld16_nt(blk + 1024 + 16 * lane);
     w.hd = ld16(blk + 2048 + 16 * (lane & 15));
     return w;
 }
@@ -174,16 +174,16 @@ template <>
 __device__ __forceinline__ MtW<LQ_Q8_0> mt_load_w<LQ_Q8_0>(const uint8_t *blk, int lane) {
     MtW<LQ_Q8_0> w;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w.p[i] = ld16(blk + 1024 * i + 16 * lane);
+    for (int i = 0; i < 4; ++i) w.p[i] = ld16_nt(blk + 1024 * i + 16 * lane);
     w.d = ld16(blk + 4096 + 16 * (lane & 15));
     return w;
 }
 template <>
 __device__ __forceinline__ MtW<LQ_Q6_K> mt_load_w<LQ_Q6_K>(const uint8_t *blk, int lane) {
     MtW<LQ_Q6_K> w;
-    w.l0 = ld16(blk + 16 * lane);
-    w.l1 = ld16(blk + 1024 + 16 * lane);
-    w.qh = ld16(blk + 2048 + 16 * lane);
+    w.l0 = ld16_nt(blk + 16 * lane);
+    w.l1 = ld16_nt(blk + 1024 + 16 * lane);
+    w.qh = ld16_nt(blk + 2048 + 16 * lane);
     w.sc = ld16(blk + 3072 + 16 * (lane & 15));
     w.d = *reinterpret_cast<const uint16_t *>(blk + 3328 + 2 * (lane & 15));
     return w;

@@ -942,10 +942,11 @@ __global__ void moe_combine_vec_kernel(const float *__restrict__ ysl, const int3
     const int t = blockIdx.y;
     const int c4 = blockIdx.x * blockDim.x + threadIdx.x;
     if (4 * c4 >= H) return;
-    float4 y[K];
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    f4v y[K];   // expert output rows, each read once
 #pragma unroll
     for (int j = 0; j < K; ++j)
-        y[j] = reinterpret_cast<const float4 *>(ysl + (int64_t)pos[t * K + j] * H)[c4];
+        y[j] = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(ysl + (int64_t)pos[t * K + j] * H) + c4);
     float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int j = 0; j < K; ++j) {
