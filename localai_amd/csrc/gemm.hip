@@ -421,19 +421,18 @@ __device__ __forceinline__ lq_h8 gt_b(const GtRaw<T> &r, int q, uint32_t pair_ab
         // group g = 4 HALF + KK: qs chunk g / 2 (bytes 8 ((g / 2) % 2) ..), nibble g % 2;
         // a value is round(a * q - b) from the exact q (one fused multiply-add)
         constexpr int g = 4 * HALF + KK, hb = (g >> 1) & 1, nib = g & 1;
-        const lq_h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
         const lq_h2 ab = __builtin_bit_cast(lq_h2, pair_ab);
         const lq_h2 a2 = {ab.x, ab.x}, nb2 = {-ab.y, -ab.y};
         const uint32_t w0 = ((hb ? r.qs.z : r.qs.x) >> (4 * nib)) & 0x0F0F0F0Fu;
         const uint32_t w1 = ((hb ? r.qs.w : r.qs.y) >> (4 * nib)) & 0x0F0F0F0Fu;
-        auto pair = [&](uint32_t bits) {
-            const lq_h2 q = __builtin_bit_cast(lq_h2, bits) - k1024;
-            return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a2, nb2));
-        };
-        o.x = pair(f16_bytes_lo(w0));
-        o.y = pair(f16_bytes_hi(w0));
-        o.z = pair(f16_bytes_lo(w1));
-        o.w = pair(f16_bytes_hi(w1));
+        // the byte 0000qqqq read as FP8 e4m3 is exactly q 2^-9 (subnormal
+        // below 8, normal from 8 on); the scaled conversion times 2^9 gives
+        // two f16 q exactly in one instruction
+        auto fma2 = [&](lq_h2 q) { return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a2, nb2)); };
+        o.x = fma2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.0f, false));
+        o.y = fma2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.0f, true));
+        o.z = fma2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.0f, false));
+        o.w = fma2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.0f, true));
     } else if constexpr (T == LQ_Q6_K) {
         // slice g = 4 HALF + KK: values 128 HALF + 32 KK + 8q .. ; ql nibble KK / 2 of
         // bytes 8 (KK % 2) ..; qh bits 2 KK of bytes 8 HALF ..; sub-block 2g + q / 2
