@@ -322,7 +322,8 @@ struct MtJobs {
     int n;
 };
 // Q6 = false: Q4_K jobs only (no Q6_K body compiled in, 64 VGPRs at 1024 threads)
-template <int SPW, int RT, int MAXT, bool Q6, bool PIPE = false>
+// RT6: row tiles per workgroup of the Q6_K jobs (RT those of the Q4_K jobs)
+template <int SPW, int RT, int MAXT, bool Q6, bool PIPE = false, int RT6 = RT>
 __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(MAXT == 1024 && !Q6 ? 8 : 1)))
 void gemv_mfma_many(MtJobs jobs, int nb, const float *__restrict__ x) {
     const int64_t b = blockIdx.x;
@@ -332,7 +333,7 @@ void gemv_mfma_many(MtJobs jobs, int nb, const float *__restrict__ x) {
         if (i < jobs.n && b >= jobs.blk0[i]) j = i;
     const int64_t tiles = (jobs.rows[j] + MT_ROWS - 1) / MT_ROWS;
     if (Q6 && jobs.type[j] == LQ_Q6_K)
-        mt_matvec_block<LQ_Q6_K, SPW, RT, PIPE>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
+        mt_matvec_block<LQ_Q6_K, SPW, RT6, PIPE>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
     else
         mt_matvec_block<LQ_Q4_K, SPW, RT, PIPE>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j], b - jobs.blk0[j]);
 }
@@ -347,7 +348,8 @@ void gemv_mfma_glue(const uint8_t *__restrict__ Wt, int64_t rows, int nb, int64_
     mt_matvec_block<TYPE, SPW, RT, PIPE, PRO, EPI>(Wt, rows, nb, tiles, x, y, blockIdx.x, gl, 0);
 }
 
-template <int SPW, int RT, int MAXT, bool Q6, bool PIPE, int PRO, int EPI>
+// RT6: row tiles per workgroup of the Q6_K jobs (RT those of the Q4_K jobs)
+template <int SPW, int RT, int MAXT, bool Q6, bool PIPE, int PRO, int EPI, int RT6 = RT>
 __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(MAXT == 1024 && !Q6 && SPW == 1 ? 8 : 1)))
 void gemv_mfma_many_glue(MtJobs jobs, int nb, const float *__restrict__ x, MtGlue gl) {
     const int64_t b = blockIdx.x;
@@ -357,8 +359,8 @@ void gemv_mfma_many_glue(MtJobs jobs, int nb, const float *__restrict__ x, MtGlu
         if (i < jobs.n && b >= jobs.blk0[i]) j = i;
     const int64_t tiles = (jobs.rows[j] + MT_ROWS - 1) / MT_ROWS;
     if (Q6 && jobs.type[j] == LQ_Q6_K)
-        mt_matvec_block<LQ_Q6_K, SPW, RT, PIPE, PRO, EPI>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j],
-                                                          b - jobs.blk0[j], gl, j);
+        mt_matvec_block<LQ_Q6_K, SPW, RT6, PIPE, PRO, EPI>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j],
+                                                           b - jobs.blk0[j], gl, j);
     else
         mt_matvec_block<LQ_Q4_K, SPW, RT, PIPE, PRO, EPI>(jobs.Wt[j], jobs.rows[j], nb, tiles, x, jobs.y[j],
                                                           b - jobs.blk0[j], gl, j);
@@ -456,6 +458,9 @@ int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const
         LQ_HIP(hipGetLastError());
         return LOCALAI_OK;
     }
+    // mixed Q4_K / Q6_K groups of the small plan (q/k/v): the Q4_K jobs take
+    // two tiles per workgroup, so each wave's staged x serves two tiles
+    const bool split = any_q6 && !p.pipe && p.spw == 2 && p.rt == 1;
     MtJobs jobs = {};
     jobs.n = n;
     int64_t b = 0;
@@ -465,11 +470,17 @@ int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const
         jobs.rows[j] = g[j]->rows;
         jobs.type[j] = g[j]->type;
         jobs.blk0[j] = b;
-        b += ((g[j]->rows + MT_ROWS - 1) / MT_ROWS + p.rt - 1) / p.rt;
+        const int rt = split && g[j]->type == LQ_Q4_K ? 2 : p.rt;
+        b += ((g[j]->rows + MT_ROWS - 1) / MT_ROWS + rt - 1) / rt;
     }
     for (int j = n; j <= MT_MAX_JOBS; ++j) jobs.blk0[j] = b;
     dim3 grid((unsigned)b), block(64 * p.waves);
-    const size_t lds = mt_lds_bytes(any_q6 ? LQ_Q6_K : LQ_Q4_K, p.waves, p.spw, 1, p.rt);
+    const size_t lds = mt_lds_bytes(any_q6 ? LQ_Q6_K : LQ_Q4_K, p.waves, p.spw, 1, split ? 2 : p.rt);
+    if (split) {
+        hipLaunchKernelGGL((gemv_mfma_many<2, 2, 1024, true, false, 1>), grid, block, lds, s, jobs, nb, x);
+        LQ_HIP(hipGetLastError());
+        return LOCALAI_OK;
+    }
 #define MT_L(S, R, M, P)                                                                        \
     do {                                                                                        \
         if (any_q6) hipLaunchKernelGGL((gemv_mfma_many<S, R, M, true, P>), grid, block, lds, s, jobs, nb, x);  \
@@ -541,6 +552,9 @@ int launch_matvec_mfma_many_glue(int n, const lq_geom *const *g, const uint8_t *
         any_q6 |= g[j]->type == LQ_Q6_K;
     }
     const MtPlan p = mt_plan(nb, total_tiles, any_q6);
+    // mixed Q4_K / Q6_K groups of the small plan (q/k/v): the Q4_K jobs take
+    // two tiles per workgroup, so each wave's staged x serves two tiles
+    const bool split = any_q6 && !p.pipe && p.spw == 2 && p.rt == 1;
     MtJobs jobs = {};
     jobs.n = n;
     int64_t b = 0;
@@ -550,11 +564,24 @@ int launch_matvec_mfma_many_glue(int n, const lq_geom *const *g, const uint8_t *
         jobs.rows[j] = g[j]->rows;
         jobs.type[j] = g[j]->type;
         jobs.blk0[j] = b;
-        b += ((g[j]->rows + MT_ROWS - 1) / MT_ROWS + p.rt - 1) / p.rt;
+        const int rt = split && g[j]->type == LQ_Q4_K ? 2 : p.rt;
+        b += ((g[j]->rows + MT_ROWS - 1) / MT_ROWS + rt - 1) / rt;
     }
     for (int j = n; j <= MT_MAX_JOBS; ++j) jobs.blk0[j] = b;
     dim3 grid((unsigned)b), block(64 * p.waves);
-    const size_t lds = mt_lds_bytes(any_q6 ? LQ_Q6_K : LQ_Q4_K, p.waves, p.spw, 1, p.rt);
+    const size_t lds = mt_lds_bytes(any_q6 ? LQ_Q6_K : LQ_Q4_K, p.waves, p.spw, 1, split ? 2 : p.rt);
+    if (split) {
+        if (epi == MT_EPI_Y)
+            hipLaunchKernelGGL((gemv_mfma_many_glue<2, 2, 1024, true, false, MT_PRO_NORM, MT_EPI_Y, 1>), grid, block,
+                               lds, s, jobs, nb, x, gl);
+        else if (epi == MT_EPI_ROPE)
+            hipLaunchKernelGGL((gemv_mfma_many_glue<2, 2, 1024, true, false, MT_PRO_NORM, MT_EPI_ROPE, 1>), grid,
+                               block, lds, s, jobs, nb, x, gl);
+        else
+            return fail(LOCALAI_ETYPE, "mfma matvec: no kernel for this prologue / epilogue");
+        LQ_HIP(hipGetLastError());
+        return LOCALAI_OK;
+    }
 #define MT_L(S, R, M, P)                                                                                    \
     do {                                                                                                    \
         if constexpr (!P) {                                                                                 \
