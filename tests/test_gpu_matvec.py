@@ -271,6 +271,9 @@ def test_tile_counts_not_multiple_of_xcds(t, rows, cols):
 @pytest.mark.parametrize('shapes', [
     # attn_q / attn_k / attn_v of a Q4_K_M decode step (v in Q6_K): one mixed launch
     [(12, 512, 4096), (12, 128, 4096), (14, 128, 4096)],
+    # the same mix with the Q6_K job first and ragged Q4_K jobs: their
+    # workgroups take two tiles each, the last one only one (63 and 4 tiles)
+    [(14, 77, 4096), (12, 1000, 4096), (12, 53, 4096)],
     # ffn_gate / ffn_up shape family, ragged rows, long K (768-thread plan)
     [(12, 100, 14336), (14, 37, 14336)],
     # a matrix without a tile form (Q8_0) runs beside the fused Q4_K / Q6_K launch
