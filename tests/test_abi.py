@@ -91,3 +91,28 @@ def test_legacy_rejects_misaligned_cols_with_nan_and_status():
                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), 4, 100, 4)
     assert lib.localai_hip_last_status() == 1
     assert np.isnan(out).all()
+
+
+@pytest.mark.parametrize('T,E,k,H,I', [(1, 16, 2, 2048, 4096), (31, 16, 4, 512, 256), (32, 128, 8, 2048, 768),
+                                       (512, 128, 8, 2048, 768)])
+def test_moe_table_offsets_lie_inside_the_workspace(T, E, k, H, I):
+    """localai_hip_moe_table_offsets (host arithmetic only): every table is
+    256-byte aligned, the tables do not overlap and end inside the workspace
+    that localai_hip_moe_workspace_size asks for; the expert GEMM tile list
+    exists from 32 tokens on, with its capacity and tile width."""
+    lib = _lib.load()
+    offs = (ctypes.c_int64 * 12)()
+    assert lib.localai_hip_moe_table_offsets(T, E, k, H, I, offs) == 0
+    ws = lib.localai_hip_moe_workspace_size(T, E, k, H, I)
+    N = T * k
+    sizes = [4 * E, 4 * (E + 1), 4 * E, 4, 4 * N, 4 * N]
+    gemm = T >= 32
+    assert (offs[6] >= 0) == gemm and (offs[11] > 0) == gemm
+    if gemm:
+        sizes += [4 * offs[10]] * 3 + [4]
+    spans = sorted((offs[i], offs[i] + n) for i, n in enumerate(sizes))
+    assert all(o % 256 == 0 for o, _ in spans)
+    assert all(a_end <= b for (_, a_end), (b, _) in zip(spans, spans[1:]))
+    assert spans[-1][1] <= ws
+    assert lib.localai_hip_moe_table_offsets(0, E, k, H, I, offs) == 1
+    assert lib.localai_hip_moe_table_offsets(T, E, k, H, I, None) == 1
