@@ -16,6 +16,11 @@ input, weights already resident in HBM, seeded data from localai_amd/synth.py):
       beside it.
   q4k_matvec        one Q4_K matvec at the ffn_gate shape 14336x4096.
   q8_0_matvec       one Q8_0 matvec at the same shape.
+  vocab_head        the Llama-3-8B vocabulary head, Q6_K 128256x4096 (431 MB).
+  legacy_host_matvec  localai_q4k_matvec with host pointers at the ffn_gate
+      shape, as LocalAI's own native_quant.matvec calls it (weights in a
+      registered host range, cached on the device; x and y copied per call),
+      timed on the host around each call.
   q8_0_prefill      Q8_0 GEMM 14336x4096 weights x 512 tokens (TFLOP/s).
   zaya_moe_decode   ZAYA-shaped MoE FFN: hidden 2048, 16 experts, top-2,
       intermediate 4096, Q6_K experts, T = 1 (T = 8 reported alongside).
@@ -42,15 +47,19 @@ Weight copies beyond 2 x the 256 MB Infinity Cache are rotated so every step
 streams its weights from HBM; one HIP graph holds a whole rotation of steps
 (as a decode step's graph holds every layer), is replayed on the launch
 stream and timed with HIP events on that stream, exactly K steps.
-`step_stats` gives the median and p90 per-step time over at least 100 more
-steps replayed after the timed region. `roofline` is the dominant kernel of
-the workload timed alone the same way (or the whole layer where it is a
-composition of kernels); `cpu_baseline` is the reference's own
+`roofline` is the dominant kernel of the workload timed alone the same way
+(or the whole call where it is a composition of kernels), its `traffic` the
+HBM bytes per launch from the committed rocprofv3 counter passes
+(profiles/traffic.json); `cpu_baseline` is the reference's own
 engine/native_quant.cpp kernels (built from source into oracle/_ref) on a
 bounded sample, on the host cores, pinned (sched_setaffinity) to one logical
 CPU per physical core, at the reference's thread policy and on all cores
 (the reference's pool caps at 8 threads), with the NumPy dequantize + matmul
 path timed beside it for the dense configs.
+
+stdout carries the one JSON line (every workload's time, value, roofline and
+CPU baseline, kept short); stderr carries the full record as a line starting
+`[bench] detail` (step statistics, all-core and NumPy CPU legs, shapes).
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--cpu-baseline auto|off]
 """
@@ -71,12 +80,13 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFS = 2500.0      # dense f16/bf16 MFMA
 MALL_BYTES = 256 << 20
 METRIC = 'µs/layer + achieved HBM GB/s (% of peak) for Q4_K/Q6_K matvec & MoE layer'
-WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill',
-             'llama3_8b_layer_chain', 'llama3_8b_attention_decode', 'qwen35_delta_net_step', 'hbm_read_floor',
-             'hbm_copy']
+WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_matvec', 'vocab_head', 'legacy_host_matvec', 'q8_0_prefill',
+             'zaya_moe_decode', 'qwen3_moe_prefill', 'llama3_8b_layer_chain', 'llama3_8b_attention_decode',
+             'qwen35_delta_net_step', 'hbm_read_floor', 'hbm_copy']
 # the default run: the headline, then these under "workloads"
-DEFAULT_SUITE = ['q4k_matvec', 'q8_0_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill', 'llama3_8b_layer_chain',
-                 'llama3_8b_attention_decode', 'qwen35_delta_net_step', 'hbm_read_floor']
+DEFAULT_SUITE = ['q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill', 'q8_0_matvec', 'vocab_head',
+                 'legacy_host_matvec', 'llama3_8b_layer_chain', 'llama3_8b_attention_decode', 'qwen35_delta_net_step',
+                 'hbm_read_floor']
 
 
 def log(msg):
@@ -299,28 +309,34 @@ def cpu_runs(call, policy_threads, work, unit, sample, scale_us=1.0, min_samples
     the reference's pool), plus the NumPy dequantize + matmul path when
     numpy_call is given. call(None) runs one sample at the policy's thread
     counts, call(n) with n threads everywhere; work is the bytes or flops it
-    represents (GB/s or TFLOP/s from the median)."""
+    represents (GB/s or TFLOP/s from the median). `sample` names the bounded
+    sample in a few words; the host is reported once, at the top of the line."""
     div = 1e9 if unit == 'GB/s' else 1e12
     allc = host()['physical_cores']
-    with pinned(policy_threads) as cpus:
+    with pinned(policy_threads):
         us, n = time_cpu(lambda: call(None), min_samples=min_samples, budget_s=budget_s)
     ta = min(8, allc)
     with pinned(allc):
         us_all, n_all = time_cpu(lambda: call(ta), min_samples=min_samples, budget_s=budget_s)
-    out = {'value': round(work / (us * 1e-6) / div, 5), 'unit': unit, 'cores': policy_threads, 'kind': 'reference',
-           'us_per_layer': round(us * scale_us, 1), 'samples': n,
-           'sample': f'{sample}; median of {n}; {host_note()} ({len(cpus)} for this run)',
-           'host': {k: v for k, v in host().items() if not k.startswith('_')},
-           'all_cores': {'value': round(work / (us_all * 1e-6) / div, 5), 'threads': ta, 'cores': allc,
-                         'us_per_layer': round(us_all * scale_us, 1), 'samples': n_all}}
+    out = {'value': sig(work / (us * 1e-6) / div), 'unit': unit, 'cores': policy_threads, 'kind': 'reference',
+           'sample': sample, 'us': round(us * scale_us, 1), 'samples': n,
+           'all_cores': {'value': sig(work / (us_all * 1e-6) / div), 'threads': ta, 'cores': allc,
+                         'us': round(us_all * scale_us, 1), 'samples': n_all}}
     if numpy_call is not None:
         with pinned(allc):
             us_np, n_np = time_cpu(numpy_call, min_samples=2, budget_s=budget_s, warm=1)
-        out['numpy'] = {'value': round((numpy_work or work) / (us_np * 1e-6) / div, 5), 'unit': unit,
+        out['numpy'] = {'value': sig((numpy_work or work) / (us_np * 1e-6) / div), 'unit': unit,
                         'us': round(us_np, 1), 'samples': n_np,
                         'what': 'oracle restatement of engine/dequant.py dequantize + NumPy matmul '
                                 '(engine/gguf_parser.py:273-288 fallback), all physical cores'}
     return out
+
+
+def sig(v, digits=4):
+    """v rounded to `digits` significant digits (keeps the one-line record short)."""
+    if v is None or v == 0 or not np.isfinite(v):
+        return v
+    return float(f'{v:.{digits}g}')
 
 
 # ---------------------------------------------------------------- workloads
@@ -370,11 +386,9 @@ def wl_layer(args, torch, device, synth):
         from oracle import ref
         calls = [(host[name], vecs[src], rows, cols, t, reference_threads(rows, t))
                  for name, t, rows, cols, src in layer]
-        policy = dict((nm, c[5]) for (nm, *_), c in zip(layer, calls))
         cpu = cpu_runs(lambda th: [ref.matvec(*c[:5], threads=c[5] if th is None else th) for c in calls],
                        max(c[5] for c in calls), layer_bytes, 'GB/s',
-                       f'full layers (7 matvecs) of engine/native_quant.cpp built with g++ -O2 -mavx2 -mfma, '
-                       f'reference thread policy {policy}')
+                       '7 localai_*_matvec per layer')
     gbs = layer_bytes / (ms * 1e-3) / 1e9
     return {
         'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
@@ -404,7 +418,7 @@ def gate_up_roofline(args, torch, device, gate_host, up_host, x, stream):
     for p in pairs:
         for m in p:
             m.close()
-    return {'bound': 'hbm', 'kernel': 'gemv_mfma_glue<Q4_K, paired tiles> ffn_gate + ffn_up 2 x 14336x4096',
+    return {'bound': 'hbm', 'kernel': 'gemv_mfma<Q4_K> gate+up paired',
             'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
             'frac': round(achieved / HBM_PEAK_GBS, 4), 'traffic': measured_traffic('layer', 'gate_up'),
             'us_per_launch': round(kms * 1e3, 3), 'bytes_per_launch': nbytes}
@@ -427,7 +441,7 @@ def gate_roofline(args, torch, device, gate_host, x, stream, t=12):
     return {'bound': 'hbm', 'kernel': f"gemv_mfma_{'q4k' if t == 12 else 'q8_0'} 14336x4096",
             'achieved': round(achieved, 1),
             'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4),
-            'traffic': measured_traffic('q4k', 'gate'),
+            'traffic': measured_traffic('q4k' if t == 12 else 'q8_matvec', 'gate'),
             'us_per_launch': round(kms * 1e3, 3), 'bytes_per_launch': gate_bytes}
 
 
@@ -459,7 +473,7 @@ def wl_q4k(args, torch, device, synth):
         def numpy_path():
             return quant.dequantize(raw, 12, (14336, 4096)) @ xv
         cpu = cpu_runs(lambda t: ref.matvec(raw, xv, 14336, 4096, 12, threads=th if t is None else t), th, nbytes,
-                       'GB/s', 'calls of localai_q4k_matvec 14336x4096', numpy_call=numpy_path)
+                       'GB/s', 'localai_q4k_matvec', numpy_call=numpy_path)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
@@ -484,13 +498,110 @@ def wl_q8_matvec(args, torch, device, synth):
         from oracle import ref
         th = reference_threads(14336, 8)
         cpu = cpu_runs(lambda t: ref.matvec(raw, xv, 14336, 4096, 8, threads=th if t is None else t), th, nbytes,
-                       'GB/s', 'calls of localai_q8_0_matvec 14336x4096')
+                       'GB/s', 'localai_q8_0_matvec')
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
             'data': 'synthetic (seeded GGML Q8_0 bytes, fp32 N(0,1) x)',
             'config': {'workload': 'q8_0_matvec_14336x4096', 'batch': 1, 'algorithmic_bytes': nbytes},
             'roofline': roof, 'cpu_baseline': cpu}
+
+
+def wl_vocab_head(args, torch, device, synth):
+    """The vocabulary head of a Llama-3-8B decode step (engine/model.py:235-237,
+    output.weight 128256 x 4096, Q6_K in a Q4_K_M file): the largest matvec of
+    the step, 431 MB, one launch."""
+    rows, cols, t = 128256, 4096, 14
+    rng = np.random.default_rng(args.seed)
+    raw = synth.quant_tensor(rng, t, rows, cols)
+    xv = synth.activations(rng, cols)
+    x = device.to_device_f32(xv)
+    wbytes = rows * (cols // 256) * 210
+    nbytes = wbytes + 4 * cols + 4 * rows
+    copies = rotations(wbytes)
+    log(f'vocab head: {copies} weight copies ({copies * wbytes / 1e6:.0f} MB)')
+    mats = [device.QMat.from_ggml(raw, t, rows, cols) for _ in range(copies)]
+    out = torch.empty(rows, dtype=torch.float32, device=device.device())
+    stream = torch.cuda.Stream()
+    ms = time_steps(torch, [lambda m=m: m.matvec(x, out=out, stream=stream) for m in mats], stream, args.steps,
+                    args.warmup)
+    if not torch.isfinite(out).all():
+        raise SystemExit('non-finite vocabulary head output')
+    for m in mats:
+        m.close()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_baseline != 'off' and ref_ok():
+        from oracle import ref
+        th = reference_threads(rows, t)
+        cpu = cpu_runs(lambda n: ref.matvec(raw, xv, rows, cols, t, threads=th if n is None else n), th, nbytes,
+                       'GB/s', 'localai_q6k_matvec', min_samples=5, budget_s=8)
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
+            'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
+            'data': 'synthetic (seeded GGML Q6_K bytes, fp32 N(0,1) x)',
+            'config': {'workload': 'llama3_8b_vocab_head_q6k_128256x4096', 'algorithmic_bytes': nbytes,
+                       'weight_copies_rotated': copies},
+            'roofline': {'bound': 'hbm', 'kernel': 'gemv_mfma<Q6_K> 128256x4096', 'achieved': round(gbs, 1),
+                         'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4),
+                         'traffic': measured_traffic('vocab_head', 'head'), 'us_per_launch': round(ms * 1e3, 3),
+                         'bytes_per_launch': nbytes},
+            'cpu_baseline': cpu}
+
+
+def wl_legacy(args, torch, device, synth):
+    """What LocalAI's own native_quant.matvec (engine/native_quant.py:102-126)
+    sees with this library behind its ctypes binding: localai_q4k_matvec with
+    host pointers at the ffn_gate shape, x uploaded and y downloaded by the
+    call, the weights in a registered (GGUF-map-like) host range so their
+    device copy is cached. Timed on the host around each synchronous call;
+    the first, uploading call of an unregistered range is timed beside it."""
+    import ctypes
+    from localai_amd import _lib
+    lib = _lib.load()
+    rows, cols, t = 14336, 4096, 12
+    rng = np.random.default_rng(args.seed)
+    raw = np.frombuffer(synth.quant_tensor(rng, t, rows, cols), dtype=np.uint8).copy()
+    xv = synth.activations(rng, cols)
+    out = np.empty(rows, np.float32)
+    u8, f32 = ctypes.POINTER(ctypes.c_uint8), ctypes.POINTER(ctypes.c_float)
+    rp, xp, op = raw.ctypes.data_as(u8), xv.ctypes.data_as(f32), out.ctypes.data_as(f32)
+    nbytes = raw.nbytes + 4 * cols + 4 * rows
+
+    def call():
+        lib.localai_q4k_matvec(rp, xp, op, rows, cols, 8)
+        if lib.localai_hip_last_status():
+            raise SystemExit('legacy call failed: ' + lib.localai_hip_last_error().decode())
+    t0 = time.perf_counter_ns()
+    call()                                      # unregistered: upload + repack + matvec
+    upload_us = (time.perf_counter_ns() - t0) / 1e3
+    _lib.check(lib.localai_hip_register_host(ctypes.c_void_p(raw.ctypes.data), raw.nbytes))
+    call()                                      # first registered call builds the cached copy
+    samples = []
+    for _ in range(max(50, args.steps)):
+        t0 = time.perf_counter_ns()
+        call()
+        samples.append((time.perf_counter_ns() - t0) / 1e3)
+    _lib.check(lib.localai_hip_unregister_host(ctypes.c_void_p(raw.ctypes.data)))
+    if not np.isfinite(out).all():
+        raise SystemExit('non-finite legacy output')
+    us = float(np.median(samples))
+    gbs = nbytes / (us * 1e-6) / 1e9
+    cpu = None
+    if args.cpu_baseline != 'off' and ref_ok():
+        from oracle import ref
+        th = reference_threads(rows, t)
+        cpu = cpu_runs(lambda n: ref.matvec(raw, xv, rows, cols, t, threads=th if n is None else n), th, nbytes,
+                       'GB/s', 'localai_q4k_matvec', min_samples=10, budget_s=5)
+    return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': us / 1e3, 'us_per_layer': round(us, 2),
+            'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
+            'data': 'synthetic (seeded GGML Q4_K bytes in host memory, fp32 N(0,1) x)',
+            'config': {'workload': 'legacy_host_q4k_matvec_14336x4096', 'p90_us': round(float(np.percentile(samples, 90)), 2),
+                       'unregistered_first_call_us': round(upload_us, 1), 'samples': len(samples)},
+            'roofline': {'bound': 'hbm', 'kernel': 'whole host call',
+                         'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                         'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': measured_traffic('q4k', 'gate'),
+                         'us_per_launch': round(us, 2), 'bytes_per_launch': nbytes},
+            'cpu_baseline': cpu}
 
 
 def wl_q8_prefill(args, torch, device, synth):
@@ -523,15 +634,15 @@ def wl_q8_prefill(args, torch, device, synth):
         def numpy_path():
             return xh @ quant.dequantize(raw[:nrows * (cols // 32) * 34], 8, (nrows, cols)).T
         cpu = cpu_runs(lambda t: ref.matmul(sub, xh, srows, cols, 8, threads=th if t is None else t), th, sflops,
-                       'TFLOP/s', f'calls of localai_q8_0_matmul on {srows} of {rows} rows x {tokens} tokens '
-                       f'(us_per_layer scaled to all rows)', scale_us=rows / srows, min_samples=3, budget_s=12,
+                       'TFLOP/s', f'localai_q8_0_matmul, {srows} rows, us scaled',
+                       scale_us=rows / srows, min_samples=3, budget_s=12,
                        numpy_call=numpy_path, numpy_work=2 * nrows * cols * tokens)
     return {'value': round(tfs, 2), 'unit': 'TFLOP/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'mfma_frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'dtype': 'f16 MFMA, fp32 accumulate',
             'data': 'synthetic (seeded GGML Q8_0 bytes, fp32 N(0,1) activations)',
             'config': {'workload': 'q8_0_prefill_gemm_14336x4096x512', 'tokens': tokens, 'flops': flops,
                        'weight_copies_rotated': copies},
-            'roofline': {'bound': 'mfma', 'kernel': 'x_to_f16 (tiled) + gemm_cu_q80_kernel (whole call)',
+            'roofline': {'bound': 'mfma', 'kernel': 'x_to_f16 + gemm_cu_q80 (call)',
                          'achieved': round(tfs, 1), 'peak': MFMA_F16_PEAK_TFS, 'unit': 'TFLOP/s',
                          'frac': round(tfs / MFMA_F16_PEAK_TFS, 4), 'traffic': measured_traffic('q8', 'gemm'),
                          'us_per_launch': round(ms * 1e3, 3), 'flops_per_launch': flops},
@@ -593,10 +704,39 @@ def experts1_roofline(args, torch, device, E, H, I, k, per_expert):
     ms = time_steps(torch, [lambda L=L: run(L) for L in layers], stream, args.steps, args.warmup)
     nbytes = k * per_expert + 2 * H * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {'bound': 'hbm', 'kernel': 'moe_decode1_kernel (localai_hip_moe_experts1: both experts, gate_up and down)',
+    return {'bound': 'hbm', 'kernel': 'moe_decode1_kernel (2 experts)',
             'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4),
             'traffic': measured_traffic('zaya', 'decode1'), 'us_per_launch': round(ms * 1e3, 3),
             'bytes_per_launch': nbytes}
+
+
+def expert_gemm_roofline(args, torch, device, E, H, I, k, T, distinct):
+    """The prefill layer's dominant kernel, the gate_up expert GEMM (with
+    SiLU*up), run alone (localai_hip_moe_expert_gemm) on the routing tables
+    each rotated layer copy's last forward left in its workspace. Its bytes:
+    the gate_up weights of the touched experts, the f16 rows of h and the
+    fp32 act rows it writes; its flops 2 * T * k * H * 2I. The binding roof is
+    HBM (about 175 flop per byte against a ridge of about 315)."""
+    import ctypes
+    from localai_amd import _lib
+    layers, hd, stream = _moe_gpu.last
+    lib = _lib.load()
+    sp = ctypes.c_void_p(int(stream.cuda_stream))
+
+    def run(L):
+        ws = L.workspace(T)
+        _lib.check(lib.localai_hip_moe_expert_gemm(L.gate_up.handle, L.down.handle, T, E, k, device.ptr(ws),
+                                                   ws.numel(), 0, sp))
+    kms = time_steps(torch, [lambda L=L: run(L) for L in layers], stream, args.steps, args.warmup)
+    gu_bytes = 2 * I * (H // 256) * 144
+    nbytes = distinct * gu_bytes + T * H * 2 + T * k * I * 4
+    flops = 2 * T * k * H * 2 * I
+    gbs = nbytes / (kms * 1e-3) / 1e9
+    tfs = flops / (kms * 1e-3) / 1e12
+    return {'bound': 'hbm', 'kernel': 'gate_up expert GEMM',
+            'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4),
+            'traffic': measured_traffic('qwen3', 'gate_up'), 'us_per_launch': round(kms * 1e3, 3),
+            'bytes_per_launch': nbytes, 'tflops': round(tfs, 1), 'mfma_frac': round(tfs / MFMA_F16_PEAK_TFS, 4)}
 
 
 def _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, T, bias, threads):
@@ -654,8 +794,8 @@ def wl_zaya(args, torch, device, synth):
         gu, dn, rw, h, idx = data
         cpu = cpu_runs(lambda th: _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, 1, None,
                                            threads=4 if th is None else th)(), 4, nbytes, 'GB/s',
-                       'MoE layers at T=1 (numpy router + localai_q6k_matvec per selected expert, threads=4 as '
-                       'engine/zaya.py:161)', min_samples=5, budget_s=8)
+                       'numpy router + localai_q6k_matvec',
+                       min_samples=5, budget_s=8)
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
             'data': 'synthetic (seeded Q6_K experts, router N(0,0.02), h N(0,1))',
@@ -673,6 +813,7 @@ def wl_qwen3(args, torch, device, synth):
     bias = synth.zipf_bias(E)
     ms, nbytes, distinct, copies, data = _moe_gpu(args, torch, device, synth, E, H, I, k, t, T, bias,
                                                   per_expert, 'qwen3')
+    roof = expert_gemm_roofline(args, torch, device, E, H, I, k, T, distinct)
     _moe_gpu.last = None
     flops = 2 * T * k * (H * 2 * I + I * H)
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -683,7 +824,7 @@ def wl_qwen3(args, torch, device, synth):
         th = reference_threads(2 * I, 12)
         cpu = cpu_runs(lambda t_: _moe_cpu(gu, dn, rw, h, idx, E, H, I, k, t, T, bias,
                                            threads=th if t_ is None else t_)(), th, flops, 'TFLOP/s',
-                       'MoE prefill layers (numpy router + localai_q4k_matmul per expert on its gathered tokens)',
+                       'numpy router + localai_q4k_matmul',
                        min_samples=2, budget_s=12)
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'tflops': round(tfs, 2),
@@ -692,10 +833,7 @@ def wl_qwen3(args, torch, device, synth):
             'config': {'workload': 'qwen3_moe_prefill_h2048_e128_top8_i768_q4k_t512', 'tokens': T,
                        'distinct_experts': distinct, 'algorithmic_bytes': nbytes, 'flops': flops,
                        'layer_copies_rotated': copies},
-            'roofline': {'bound': 'hbm', 'kernel': 'whole MoE layer', 'achieved': round(gbs, 1),
-                         'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4),
-                         'traffic': None, 'us_per_launch': round(ms * 1e3, 3), 'bytes_per_launch': nbytes},
-            'cpu_baseline': cpu}
+            'roofline': roof, 'cpu_baseline': cpu}
 
 
 def wl_chain(args, torch, device, synth):
@@ -733,6 +871,11 @@ def wl_chain(args, torch, device, synth):
         set_mode(False)
     ms = time_steps(torch, steps, stream, args.steps, args.warmup)
     gbs = layer_bytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_baseline != 'off' and ref_ok():
+        cpu = cpu_runs(_chain_cpu(host, layer, rng, w1, w2), max(reference_threads(r, t) for _, t, r, _, _ in layer),
+                       layer_bytes, 'GB/s', '7 localai_*_matvec + NumPy glue', min_samples=10,
+                       budget_s=6)
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
             'data': 'synthetic (seeded GGML Q4_K/Q6_K bytes, fp32 N(0,1) activations, norm weights U(0.5,1.5))',
@@ -740,10 +883,48 @@ def wl_chain(args, torch, device, synth):
                        'weight_copies_rotated': copies},
             'one_launch': {'us_per_layer': round(ms1 * 1e3, 3),
                            'GB/s': round(layer_bytes / (ms1 * 1e-3) / 1e9, 1)},
-            'roofline': {'bound': 'hbm', 'kernel': 'the four glued matvec launches', 'achieved': round(gbs, 1),
+            'roofline': {'bound': 'hbm', 'kernel': '4 glued matvec launches', 'achieved': round(gbs, 1),
                          'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None,
                          'us_per_launch': round(ms * 1e3, 3), 'bytes_per_launch': layer_bytes},
-            'cpu_baseline': None}
+            'cpu_baseline': cpu}
+
+
+def _chain_cpu(host, layer, rng, w1, w2):
+    """The reference's decode-layer step on the CPU: its seven native matvecs
+    (reference thread policy) with the float32 NumPy glue of
+    engine/model.py:181-233 between them (residual adds, RMSNorm :82,
+    SiLU * up, RoPE of q and k)."""
+    from oracle import ref
+    x0 = synth_act(rng, 4096)
+    att = synth_act(rng, 4096)
+    cos = np.cos(np.arange(64, dtype=np.float32) * 0.01).astype(np.float32)
+    sin = np.sin(np.arange(64, dtype=np.float32) * 0.01).astype(np.float32)
+    info = {n: (t, r, c) for n, t, r, c, _ in layer}
+
+    def mv(name, x, th):
+        t, r, c = info[name]
+        return ref.matvec(host[name], x, r, c, t, threads=reference_threads(r, t) if th is None else th)
+
+    def norm(x, w):
+        return x * (1.0 / np.sqrt(np.mean(x * x) + np.float32(1e-5))) * w
+
+    def rope(v):                 # adjacent pairs per 128-wide head (engine/model.py:83-100, llama)
+        v = v.reshape(-1, 64, 2)
+        a, b = v[..., 0], v[..., 1]
+        return np.stack([a * cos - b * sin, a * sin + b * cos], axis=-1).reshape(-1)
+
+    def step(th):
+        x1 = x0 + mv('attn_output', att, th)
+        h = norm(x1, w1)
+        g, u = mv('ffn_gate', h, th), mv('ffn_up', h, th)
+        x2 = x1 + mv('ffn_down', (g / (1.0 + np.exp(-g)) * u).astype(np.float32), th)
+        h2 = norm(x2, w2)
+        return rope(mv('attn_q', h2, th)), rope(mv('attn_k', h2, th)), mv('attn_v', h2, th)
+    return step
+
+
+def synth_act(rng, n):
+    return rng.standard_normal(n).astype(np.float32)
 
 
 def wl_floor(args, torch, device, synth):
@@ -802,12 +983,10 @@ def _cpu_port(fn, work, unit, sample):
     compiled reference kernel here, timed on all physical cores (pinned)."""
     div = 1e9 if unit == 'GB/s' else 1e12
     allc = host()['physical_cores']
-    with pinned(allc) as cpus:
+    with pinned(allc):
         us, n = time_cpu(fn, min_samples=5, budget_s=6)
-    return {'value': round(work / (us * 1e-6) / div, 5), 'unit': unit, 'cores': allc, 'kind': 'port',
-            'us_per_layer': round(us, 1), 'samples': n,
-            'sample': f'{sample}; median of {n}; {host_note()} ({len(cpus)} for this run)',
-            'host': {k: v for k, v in host().items() if not k.startswith('_')}}
+    return {'value': sig(work / (us * 1e-6) / div), 'unit': unit, 'cores': allc, 'kind': 'port',
+            'sample': sample, 'us': round(us, 1), 'samples': n}
 
 
 def wl_attention(args, torch, device, synth):
@@ -850,15 +1029,14 @@ def wl_attention(args, torch, device, synth):
     cpu = None
     if args.cpu_baseline != 'off':
         cpu = _cpu_port(lambda: oatt.gqa_decode_f32(qv, kc2, vc2, pos, nh, nkv, hd), nbytes, 'GB/s',
-                        'decode attention over 4096 positions, the reference\'s float32 np.repeat + einsum '
-                        '(engine/model.py:223-227) restated')
+                        'model.py:223-227 NumPy f32')
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
             'data': 'synthetic (N(0,1) fp32 cache, q, k, v)',
             'config': {'workload': 'llama3_8b_attention_decode_ctx4096', 'n_heads': nh, 'n_kv_heads': nkv,
                        'head_dim': hd, 'positions': ctx, 'algorithmic_bytes': nbytes, 'layer_copies_rotated': copies,
                        'normwise_vs_oracle': err},
-            'roofline': {'bound': 'hbm', 'kernel': 'attn_chunk_kernel + attn_merge_kernel (whole call)',
+            'roofline': {'bound': 'hbm', 'kernel': 'attn_chunk + attn_merge (call)',
                          'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                          'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': measured_traffic('attention', 'chunk'),
                          'us_per_launch': round(ms * 1e3, 3), 'bytes_per_launch': nbytes},
@@ -899,8 +1077,7 @@ def wl_delta_net(args, torch, device, synth):
     cpu = None
     if args.cpu_baseline != 'off':
         cpu = _cpu_port(lambda: oatt.delta_net_step(st, qv, kv, vv, decay, beta), nbytes, 'GB/s',
-                        'delta_net_step 32 x 128 x 128, the reference loop (engine/numba_kernels.py:11-45) '
-                        'restated in float32 NumPy (Numba is not installed here)')
+                        'numba_kernels.py:11-45 NumPy f32')
     return {'value': round(gbs, 2), 'unit': 'GB/s', 'ms_per_step': ms, 'us_per_layer': round(ms * 1e3, 3),
             'hbm_frac': round(gbs / HBM_PEAK_GBS, 4), 'dtype': 'fp32',
             'data': 'synthetic (state N(0, 0.01), L2-normalised q / k as engine/qwen35.py:206-208)',
@@ -936,6 +1113,7 @@ def wl_copy(args, torch, device, synth):
 
 
 FUNCS = {'llama3_8b_decode_layer': 'wl_layer', 'q4k_matvec': 'wl_q4k', 'q8_0_matvec': 'wl_q8_matvec',
+         'vocab_head': 'wl_vocab_head', 'legacy_host_matvec': 'wl_legacy',
          'q8_0_prefill': 'wl_q8_prefill',
          'zaya_moe_decode': 'wl_zaya', 'qwen3_moe_prefill': 'wl_qwen3', 'llama3_8b_layer_chain': 'wl_chain',
          'hbm_read_floor': 'wl_floor', 'hbm_copy': 'wl_copy', 'llama3_8b_attention_decode': 'wl_attention',
@@ -948,6 +1126,68 @@ def run_workload(name, args, torch, device, synth):
     if DIST and 'step_stats' not in r:
         r['step_stats'] = DIST[0]
     return r
+
+
+# extra per-workload figures kept in the one-line record (path into the
+# full record -> short key)
+EXTRAS = {
+    'llama3_8b_decode_layer': [(('us_per_layer_one_launch_per_matvec',), 'us_one_launch_per_matvec')],
+    'zaya_moe_decode': [(('config', 'tokens_8', 'us_per_layer'), 'us_t8'), (('config', 'tokens_8', 'GB/s'), 'gbs_t8'),
+                        (('config', 'distinct_experts'), 'experts_t1'),
+                        (('config', 'tokens_8', 'distinct_experts'), 'experts_t8')],
+    'qwen3_moe_prefill': [(('tflops',), 'tflops'), (('mfma_frac',), 'mfma_frac'),
+                          (('config', 'distinct_experts'), 'experts')],
+    'llama3_8b_layer_chain': [(('one_launch', 'us_per_layer'), 'us_one_launch')],
+    'legacy_host_matvec': [(('config', 'unregistered_first_call_us'), 'us_unregistered_first_call')],
+    'hbm_read_floor': [(('floors', 'one_launch_33MB', 'us'), 'us_33MB'),
+                       (('floors', 'layer_as_four_launches', 'us'), 'us_layer_4_launches'),
+                       (('floors', 'layer_as_one_launch', 'us'), 'us_layer_1_launch')],
+}
+
+
+def _dig(d, path):
+    for k in path:
+        if not isinstance(d, dict) or k not in d:
+            return None
+        d = d[k]
+    return d
+
+
+def compact_roofline(rl):
+    if not rl:
+        return None
+    out = {k: rl.get(k) for k in ('bound', 'achieved', 'peak', 'unit', 'frac', 'traffic')}
+    out['achieved'] = sig(out['achieved'])
+    out['kernel'] = rl.get('kernel')
+    out['us'] = sig(rl.get('us_per_launch'))
+    for k in ('tflops', 'mfma_frac'):
+        if k in rl:
+            out[k] = rl[k]
+    return out
+
+
+def compact_cpu(cb):
+    if not cb:
+        return None
+    out = {k: cb.get(k) for k in ('value', 'unit', 'cores', 'kind', 'sample')}
+    out['us'] = round(cb['us']) if cb.get('us') is not None else None
+    return out
+
+
+def compact(name, r):
+    """One workload in the one-line record: time, value, fraction of its
+    roof, the roofline of its dominant kernel and the CPU baseline (the
+    full record goes to stderr)."""
+    c = {'us': sig(r.get('us_per_layer', r['ms_per_step'] * 1e3)),
+         'value': sig(r['value']), 'unit': r['unit'],
+         'frac': r.get('mfma_frac') if r['unit'] == 'TFLOP/s' else r.get('hbm_frac')}
+    for path, key in EXTRAS.get(name, []):
+        v = _dig(r, path)
+        if v is not None:
+            c[key] = sig(v) if isinstance(v, float) else v
+    c['roofline'] = compact_roofline(r.get('roofline'))
+    c['cpu_baseline'] = compact_cpu(r.get('cpu_baseline'))
+    return c
 
 
 def main():
@@ -964,22 +1204,33 @@ def main():
     name = args.workload or 'llama3_8b_decode_layer'
     log(f'workload {name}')
     r = run_workload(name, args, torch, device, synth)
-    suite = {}
+    full = {}
     if args.workload is None:
         for other in DEFAULT_SUITE:
             log(f'workload {other}')
             w = run_workload(other, args, torch, device, synth)
             w['ms_per_step'] = round(w['ms_per_step'], 6)
-            suite[other] = w
+            full[other] = w
             torch.cuda.empty_cache()
-    ms = r.pop('ms_per_step')
-    line = {'metric': METRIC, 'value': r.pop('value'), 'unit': r.pop('unit'), 'n_gpus': 1, 'steps': args.steps,
+    ms = r['ms_per_step']
+    line = {'metric': METRIC, 'value': r['value'], 'unit': r['unit'], 'n_gpus': 1, 'steps': args.steps,
             'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True, 'scaling': 'weak',
-            'vs_baseline': None}
-    line.update(r)
-    if suite:
-        line['workloads'] = suite
-    print(json.dumps(line), flush=True)
+            'vs_baseline': None, 'dtype': r.get('dtype'), 'data': r.get('data'),
+            'config': {k: v for k, v in r.get('config', {}).items() if not isinstance(v, (list, dict)) and k != 'launch'}}
+    head = compact(name, r)
+    for k in ('value', 'unit'):
+        head.pop(k)
+    line.update(head)
+    if args.cpu_baseline != 'off':
+        h = host()
+        line['host'] = f"{h['model']}, {h['physical_cores']} physical cores"
+    if full:
+        line['workloads'] = {k: compact(k, v) for k, v in full.items()}
+    # the full record (step statistics, all-core and NumPy CPU legs, shapes)
+    # on stderr, then the one line on stdout
+    detail = dict(r, workloads=full)
+    print('[bench] detail ' + json.dumps(detail, default=str), file=sys.stderr, flush=True)
+    print(json.dumps(line, separators=(',', ':')), flush=True)
 
 
 if __name__ == '__main__':

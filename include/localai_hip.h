@@ -99,10 +99,15 @@ int localai_hip_qmat_unpack(const localai_qmat *m, void *out_dev, void *stream);
 int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out_dev,
                              void *stream);
 
-/* y[t, r] = sum_c W_e[r, c] * x[t, c] for t < ntok (small-batch decode matvec;
- * vectors are processed two per launch while cols <= 8192, one otherwise).
+/* y[t, r] = sum_c W_e[r, c] * x[t, c] for t < ntok (decode matvec).
  * x_dev is [ntok, cols] fp32 row-major, y_dev is [ntok, rows] fp32.
- * fp32 products of exactly decoded weights, fp32 accumulation. */
+ * One vector (ntok = 1) of a Q4_K, Q6_K or Q8_0 handle whose rows are whole
+ * 256-value super-blocks: int8 MFMA over the raw quants, x split exactly
+ * into three int8 pieces per scale group (21 bits of each value against the
+ * group maximum), the integer dot products exact, recombined and scaled in
+ * fp32 (normwise error about 1e-6). Other types and several vectors: fp32
+ * products of exactly decoded weights, fp32 accumulation (the vectors two
+ * per launch while cols <= 8192, one otherwise). */
 int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x_dev,
                        float *y_dev, int ntok, void *stream);
 
@@ -215,8 +220,11 @@ int localai_hip_attention_decode(const float *q_dev, const float *k_new_dev, con
  *   S += k[h] delta^T;   core[h] = S^T q[h]
  * q, k [heads, key_dim]; v, core [heads, value_dim]; decay, beta [heads].
  * Every product and sum is rounded on its own in the reference loop's order,
- * so state and core equal the reference kernel's bit for bit (exp(decay) is
- * the correctly rounded fp32 exponential). */
+ * so state and core equal the reference loop's bit for bit given the same
+ * fp32 factor exp(decay). The kernel takes the correctly rounded exponential;
+ * the reference's np.exp on float32 (engine/numba_kernels.py:25) can differ
+ * from it in the last bit or two, and the results then differ at that level
+ * (~1e-7 normwise). */
 int localai_hip_delta_net_step(float *state_dev, const float *q_dev, const float *k_dev, const float *v_dev,
                                const float *decay_dev, const float *beta_dev, float *core_dev, int heads,
                                int key_dim, int value_dim, void *stream);
@@ -360,6 +368,16 @@ int localai_hip_debug_fused_wait(int spin_limit, int producers_count);
  * counterpart in the reference. */
 int localai_hip_stream_read(const void *src_dev, int64_t bytes, uint32_t *out_dev, void *stream);
 
+/* Run one expert GEMM of the MoE prefill path again (which = 0: gate_up with
+ * SiLU*up, 1: down) on the routing tables and staged rows that the last
+ * localai_hip_moe_forward over `tokens` tokens (>= 32, the expert GEMM path)
+ * left in workspace_dev, with the same handles: that kernel timed alone.
+ * Results land in the workspace only. No counterpart in the reference
+ * (measurement: bench.py's qwen3_moe_prefill roofline). */
+int localai_hip_moe_expert_gemm(const localai_qmat *gate_up, const localai_qmat *down, int64_t tokens,
+                                int64_t experts, int top_k, void *workspace_dev, int64_t workspace_bytes, int which,
+                                void *stream);
+
 /* ---- host weight registration for the legacy exports -------------------- */
 
 /* Declare [host, host+nbytes) immutable (e.g. a GGUF mmap). Legacy calls whose
@@ -367,6 +385,10 @@ int localai_hip_stream_read(const void *src_dev, int64_t bytes, uint32_t *out_de
  * uploading the bytes on every call. */
 int localai_hip_register_host(const void *host, size_t nbytes);
 int localai_hip_unregister_host(const void *host);
+/* Number of device copies the legacy exports hold for registered ranges
+ * (diagnostics: a repeated call on a registered range adds none). No
+ * reference counterpart. */
+int64_t localai_hip_cache_entries(void);
 /* Drop every cached device copy. */
 int localai_hip_cache_clear(void);
 

@@ -45,6 +45,7 @@ SIGNATURES = {
                                           _vp]),
     'localai_hip_moe_forward': (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp, _vp,
                                          _vp, _vp, _c_i64, _vp]),
+    'localai_hip_moe_expert_gemm': (_c_int, [_vp, _vp, _c_i64, _c_i64, _c_int, _vp, _c_i64, _c_int, _vp]),
     'localai_hip_static_workspace_bytes': (_c_i64, []),
     'localai_hip_moe_forward_static': (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp, _vp,
                                                 _vp, _vp]),
@@ -62,6 +63,7 @@ SIGNATURES = {
     'localai_hip_debug_fused_wait': (_c_int, [_c_int, _c_int]),
     'localai_hip_register_host': (_c_int, [_vp, ctypes.c_size_t]),
     'localai_hip_unregister_host': (_c_int, [_vp]),
+    'localai_hip_cache_entries': (_c_i64, []),
     'localai_hip_cache_clear': (_c_int, []),
 }
 for _n in ('q8_0', 'q4_0', 'q4k', 'q5k', 'q6k'):

@@ -44,14 +44,20 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-# kernels whose global loads are asm with hand-counted waits (isa_check.py)
-COUNTED_LOADS = [('gemm.hip', 'gemm_cu_q80_kernel')]
+# kernels whose global loads are asm with hand-counted waits (isa_check.py):
+# (source, kernel, None) for register loads, (source, kernel, n) for a ring of
+# LDS stages filled by global_load_lds, n copies per stage and wave
+COUNTED_LOADS = [('gemm.hip', 'gemm_cu_q80_kernel', None), ('moe.hip', 'moe_route_logits_kernel', 4)]
 
 
 def _check(item) -> None:
-    from .isa_check import check_source
-    src, kernel = item
-    check_source(HIPCC, COMMON, CSRC / src, kernel, BUILD / (src + '.' + kernel + '.s'))
+    from .isa_check import check_lds_ring, check_source
+    src, kernel, per_stage = item
+    out = BUILD / (src + '.' + kernel + '.s')
+    if per_stage is None:
+        check_source(HIPCC, COMMON, CSRC / src, kernel, out)
+    else:
+        check_lds_ring(HIPCC, COMMON, CSRC / src, kernel, per_stage, out)
 
 
 def build(verbose: bool = False) -> Path:

@@ -74,12 +74,21 @@ size_t max_lds_per_block() {
 // tile form -> GGML bytes (a temporary buffer) -> row planes, on `s`, which
 // is then synchronised. Not under graph capture (it allocates and waits).
 static std::mutex g_planes_mu;
+static thread_local int g_no_alloc = 0;
+
+NoAllocScope::NoAllocScope() { ++g_no_alloc; }
+NoAllocScope::~NoAllocScope() { --g_no_alloc; }
 
 const uint8_t *qmat_planes(const localai_qmat *cm, hipStream_t s, int *status) {
     localai_qmat *m = const_cast<localai_qmat *>(cm);
     std::lock_guard<std::mutex> lk(g_planes_mu);
     *status = LOCALAI_OK;
     if (uint8_t *d = __atomic_load_n(&m->data, __ATOMIC_ACQUIRE)) return d;
+    if (g_no_alloc) {
+        *status = fail(LOCALAI_ETYPE, "this entry point allocates nothing, and the call needs the row planes of a "
+                                      "handle that holds only the tile form");
+        return nullptr;
+    }
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
         *status = fail(LOCALAI_ESTATE, "qmat: this call needs the row planes, which are built on first use; "
@@ -532,6 +541,21 @@ int localai_hip_moe_table_offsets(int64_t T, int64_t E, int k, int64_t H, int64_
                            L.tile_e, L.tile_p0, L.tile_n, L.n_tiles, L.max_tiles, L.max_tiles > 0 ? moe_gemm_tile() : 0};
     for (int i = 0; i < 12; ++i) offs[i] = v[i];
     return LOCALAI_OK;
+}
+
+int localai_hip_moe_expert_gemm(const localai_qmat *gu, const localai_qmat *dn, int64_t T, int64_t E, int k,
+                                void *ws, int64_t ws_bytes, int which, void *stream) {
+    clear_error();
+    if (!gu || !dn || !ws) return fail(LOCALAI_EARG, "moe expert gemm: null pointer");
+    if (which != 0 && which != 1) return fail(LOCALAI_EARG, "moe expert gemm: which is 0 (gate_up) or 1 (down)");
+    if (T < 1 || E < 1 || E > 1024 || k < 1 || k > 16 || k > E || gu->g.batch != E || dn->g.batch != E ||
+        gu->g.rows % 2 || dn->g.rows != gu->g.cols || dn->g.cols != gu->g.rows / 2)
+        return fail(LOCALAI_EARG, "moe expert gemm: sizes as for localai_hip_moe_forward");
+    if (ws_bytes < (int64_t)moe_workspace_bytes(T, E, k, gu->g.cols, gu->g.rows / 2) ||
+        (reinterpret_cast<uintptr_t>(ws) & 255))
+        return fail(LOCALAI_EARG, "moe expert gemm: workspace too small or not 256-byte aligned");
+    if (int st = ensure_device()) return st;
+    return launch_moe_expert_gemm(gu, dn, T, E, k, ws, which, (hipStream_t)stream);
 }
 
 int localai_hip_moe_forward(const float *h, int64_t T, int64_t H, const float *rw, const float *rb,

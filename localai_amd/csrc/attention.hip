@@ -400,8 +400,9 @@ int launch_attention_decode(const float *q, const float *k_new, const float *v_n
 // The lane that owns column vi of S runs the reference loop's exact
 // float32 operations in its order: each product and each sum rounded on its
 // own (no fused multiply-add), ki ascending, so state and core equal the
-// reference kernel's bit for bit. exp(decay) is the fp64 exponential rounded
-// once to fp32.
+// reference loop's bit for bit given the same factor exp(decay). The factor
+// here is the fp64 exponential rounded once to fp32 (correctly rounded); the
+// reference's np.exp on float32 can differ from it in the last bit or two.
 //
 // delta_net_kernel (key_dim == KF, 64 or 128): a workgroup of 4 waves owns 64
 // value columns of one head. The waves copy the [KF, 64] slab into LDS

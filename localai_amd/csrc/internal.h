@@ -115,6 +115,17 @@ struct MoeLayout {
 };
 MoeLayout moe_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I);
 size_t moe_workspace_bytes(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I);
+// one expert GEMM of the prefill path again, on the tables the last launch_moe left in ws
+int launch_moe_expert_gemm(const localai_qmat *gu, const localai_qmat *dn, int64_t T, int64_t E, int k, void *ws,
+                           int which, hipStream_t s);
+// true when launch_moe would build a handle's row planes (allocate) for these sizes
+bool moe_would_build_planes(const float *h, int64_t T, int64_t H, const localai_qmat *gu, const localai_qmat *dn);
+// While set on a thread, qmat_planes refuses to build planes (LOCALAI_ETYPE)
+// instead of allocating: the no-allocation entry points set it around their work.
+struct NoAllocScope {
+    NoAllocScope();
+    ~NoAllocScope();
+};
 int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const float *rb, int64_t E, int k,
                const localai_qmat *gu, const localai_qmat *dn, float *out, int32_t *topk_idx, float *topk_w,
                void *ws, hipStream_t s);

@@ -167,7 +167,10 @@ __device__ __forceinline__ void ly_dot(const MtW<TYPE> (&w)[RT][SPW], const floa
 }
 
 // Workgroup r of stage S1..S3 counts itself done (unless the test control
-// says not to); S4's last workgroup resets every counter block.
+// says not to); S4's last workgroup resets every counter block. The host
+// also clears the blocks before each launch (ly_clear_kernel), so a count
+// that arrives after that reset (a wait that ran out) is not carried into
+// the next launch; the error words then report the last launch.
 __device__ __forceinline__ void ly_done(const LayerArgs &a, int stage, int r, int n, int *flag) {
     d1_drain();
     __syncthreads();
@@ -437,6 +440,14 @@ int layer_error_word(void *ws, hipStream_t s, uint32_t *word) {
 
 static int ly_spw(int nb) { return (nb + 7) / 8; }
 
+// Zeroes the four stage blocks ahead of a one-launch chain (a kernel, not a
+// memset, so the call can be captured in a graph): a launch whose wait ran
+// out may have left a late count behind after S4's reset, and the next
+// launch must not start from it.
+__global__ void ly_clear_kernel(uint32_t *__restrict__ sync, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) sync[i] = 0u;
+}
+
 int launch_layer_chain(const localai_qmat *const *m, const float *pre, const float *att, const float *w_ffn,
                        const float *w_attn, float eps, const float *rope_cos, const float *rope_sin, int head_dim,
                        int rope_half, float *x_out, float *q_out, float *k_out, float *v_out, void *ws,
@@ -496,6 +507,8 @@ int launch_layer_chain(const localai_qmat *const *m, const float *pre, const flo
     const size_t lds = lds_d6 > lds_f6 ? lds_d6 : lds_f6;
     if (lds > max_lds_per_block()) return fail(LOCALAI_ETYPE, "layer chain: dim too large for the LDS");
     const dim3 grid((unsigned)(a.n1 + a.n2 + a.n3 + a.n4)), block(LY_THREADS);
+    hipLaunchKernelGGL(ly_clear_kernel, dim3(1), dim3(256), 0, s, a.sync, 4 * D1_WORDS);
+    LQ_HIP(hipGetLastError());
 #define LY_L(D, F)                                                                                  \
     if (spwd == D && spwf == F) {                                                                   \
         hipLaunchKernelGGL((layer_chain_kernel<D, F>), grid, block, lds, s, a);                     \

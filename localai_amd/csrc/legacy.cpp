@@ -9,12 +9,17 @@
 // upload into a temporary copy. Calls are serialised by one mutex, as the
 // reference serialises its pool (engine/native_quant.cpp:361-363).
 //
+// x and the result travel through pinned host staging buffers (hipHostMalloc,
+// grown on demand) with asynchronous copies on the library's legacy stream,
+// so a call waits once, after the download, rather than once per copy.
+//
 // The exports return void like the reference; a failure leaves NaN in `out`
 // and the status in localai_hip_last_status().
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -30,6 +35,9 @@ std::vector<std::pair<uintptr_t, size_t>> g_ranges;
 std::map<std::tuple<uintptr_t, int, int, int>, localai_qmat *> g_cache;
 float *g_x = nullptr, *g_y = nullptr, *g_ws = nullptr;
 size_t g_x_cap = 0, g_y_cap = 0, g_ws_cap = 0;
+float *g_hx = nullptr, *g_hy = nullptr;   // pinned host staging of x and y
+size_t g_hx_cap = 0, g_hy_cap = 0;
+hipStream_t g_stream = nullptr;           // the legacy calls' stream (default priority)
 // tokens from which the legacy matmul runs the MFMA GEMM (f16 operands, fp32
 // accumulation) instead of the fp32 matvec
 constexpr int kGemmTokens = 32;
@@ -51,6 +59,16 @@ int grow(float **buf, size_t *cap, size_t n) {
     *buf = nullptr;
     *cap = 0;
     LQ_HIP(hipMalloc((void **)buf, n * sizeof(float)));
+    *cap = n;
+    return LOCALAI_OK;
+}
+
+int grow_pinned(float **buf, size_t *cap, size_t n) {
+    if (*cap >= n) return LOCALAI_OK;
+    if (*buf) hipHostFree(*buf);
+    *buf = nullptr;
+    *cap = 0;
+    LQ_HIP(hipHostMalloc((void **)buf, n * sizeof(float), hipHostMallocDefault));
     *cap = n;
     return LOCALAI_OK;
 }
@@ -95,48 +113,53 @@ int run(int t, const uint8_t *raw, const float *x, float *out, int rows, int col
     localai_qmat *m = nullptr;
     bool temp = false;
     if (int st = resolve(raw, t, rows, cols, &m, &temp)) return st;
-    int st = grow(&g_x, &g_x_cap, (size_t)tokens * cols);
-    if (!st) st = grow(&g_y, &g_y_cap, (size_t)tokens * rows);
+    const size_t nx = (size_t)tokens * cols, ny = (size_t)tokens * rows;
+    int st = LOCALAI_OK;
+    if (!g_stream) {
+        hipError_t e = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking);
+        if (e != hipSuccess) st = hip_fail(e, "legacy stream");
+    }
+    if (!st) st = grow(&g_x, &g_x_cap, nx);
+    if (!st) st = grow(&g_y, &g_y_cap, ny);
+    if (!st) st = grow_pinned(&g_hx, &g_hx_cap, nx);
+    if (!st) st = grow_pinned(&g_hy, &g_hy_cap, ny);
+    hipStream_t s = g_stream;
     if (!st) {
-        hipError_t e = hipMemcpy(g_x, x, (size_t)tokens * cols * 4, hipMemcpyHostToDevice);
+        memcpy(g_hx, x, nx * 4);
+        hipError_t e = hipMemcpyAsync(g_x, g_hx, nx * 4, hipMemcpyHostToDevice, s);
         if (e != hipSuccess) st = hip_fail(e, "upload x");
     }
     // many-token calls take the MFMA GEMM and write the reference's [rows, tokens]
-    // layout directly (engine/native_quant.cpp:492); fewer tokens take the fp32 matvec
+    // layout directly (engine/native_quant.cpp:492); fewer tokens take the matvec
     const bool gemm = transpose_out && tokens >= kGemmTokens;
     if (!st && gemm) {
         const int64_t wsb = gemm_workspace_bytes(m->g, tokens);
         st = grow(&g_ws, &g_ws_cap, (size_t)(wsb + 3) / 4);
         if (!st) st = launch_gemm(m->g, m->tiles ? nullptr : m->data, m->tiles, g_x, tokens, g_y, 1, tokens, g_ws, wsb,
-                                  nullptr);
-        if (!st) {
-            hipError_t e = hipMemcpy(out, g_y, (size_t)tokens * rows * 4, hipMemcpyDeviceToHost);
-            if (e != hipSuccess) st = hip_fail(e, "download y");
-        }
-    } else {
-        if (!st) {
-            if (m->tiles && tokens == 1 && mt_matvec_ok(m->g)) {
-                st = launch_matvec_mfma(m->g, m->tiles, g_x, g_y, nullptr);
-            } else {
-                const uint8_t *planes = qmat_planes(m, nullptr, &st);
-                if (planes) st = launch_matvec(m->g, planes, g_x, cols, g_y, rows, tokens, nullptr);
-            }
-        }
-        if (!st) {
-            if (!transpose_out) {
-                hipError_t e = hipMemcpy(out, g_y, (size_t)tokens * rows * 4, hipMemcpyDeviceToHost);
-                if (e != hipSuccess) st = hip_fail(e, "download y");
-            } else {
-                // reference matmul output is [rows, tokens] (engine/native_quant.cpp:492)
-                std::vector<float> tmp((size_t)tokens * rows);
-                hipError_t e = hipMemcpy(tmp.data(), g_y, tmp.size() * 4, hipMemcpyDeviceToHost);
-                if (e != hipSuccess) st = hip_fail(e, "download y");
-                else
-                    for (int tk = 0; tk < tokens; ++tk)
-                        for (int r = 0; r < rows; ++r) out[(size_t)r * tokens + tk] = tmp[(size_t)tk * rows + r];
-            }
+                                  s);
+    } else if (!st) {
+        if (m->tiles && tokens == 1 && mt_matvec_ok(m->g)) {
+            st = launch_matvec_mfma(m->g, m->tiles, g_x, g_y, s);
+        } else {
+            const uint8_t *planes = qmat_planes(m, s, &st);
+            if (planes) st = launch_matvec(m->g, planes, g_x, cols, g_y, rows, tokens, s);
         }
     }
+    if (!st) {
+        hipError_t e = hipMemcpyAsync(g_hy, g_y, ny * 4, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) st = hip_fail(e, "download y");
+    }
+    if (!st) {
+        if (!transpose_out || gemm) {
+            memcpy(out, g_hy, ny * 4);
+        } else {
+            // reference matmul output is [rows, tokens] (engine/native_quant.cpp:492)
+            for (int tk = 0; tk < tokens; ++tk)
+                for (int r = 0; r < rows; ++r) out[(size_t)r * tokens + tk] = g_hy[(size_t)tk * rows + r];
+        }
+    }
+    if (st && g_stream) (void)hipStreamSynchronize(g_stream);   // nothing of this call left in flight
     if (temp) localai_hip_qmat_destroy(m);
     return st;
 }
@@ -179,6 +202,11 @@ int localai_hip_unregister_host(const void *host) {
         else ++it;
     }
     return LOCALAI_OK;
+}
+
+int64_t localai_hip_cache_entries(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return (int64_t)g_cache.size();
 }
 
 int localai_hip_cache_clear(void) {

@@ -414,21 +414,11 @@ __global__ __launch_bounds__(64 * RL_NW) void moe_route_logits_kernel(const floa
     for (int a = 0; a < RL_T; ++a)
 #pragma unroll
         for (int b = 0; b < RL_E; ++b) acc[a][b] = 0.0;
-    issue(0, 0);
-    if (nch > 1) issue(1, 1);
-    int b = 0;   // stage of chunk j
-    for (int j = 0; j < nch; ++j) {
-        // this wave's copies of chunk j are done once only chunk j + 1's remain
-        if (j + 1 < nch)
-            asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-        else
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        // every wave's copies of chunk j have landed, and every wave has read
-        // chunk j - 1 (its reads completed before its sums), whose stage is
-        // refilled next. A bare barrier: __syncthreads' fence would also wait
-        // for the copies still in flight.
-        asm volatile("s_barrier" ::: "memory");
-        if (j + 2 < nch) issue(j + 2, b == 0 ? 2 : b - 1);
+    // chunk j sits in stage j % RL_STAGES; chunk j + 2 is requested while
+    // chunk j is summed. Every wait is unconditional so that the build's
+    // assembly check can prove it (isa_check.lds_ring_violations): the loop
+    // runs while chunk j + 2 exists, then the last two chunks are peeled.
+    auto sum_chunk = [&](int j, int b) {
         // the chunk's rows, read in one block that waits for its own results
         // (the compiler would otherwise wait for every copy in flight first);
         // early-clobber outputs keep the addresses alive through the block
@@ -474,8 +464,32 @@ __global__ __launch_bounds__(64 * RL_NW) void moe_route_logits_kernel(const floa
 #pragma unroll
                 for (int e = 0; e < RL_E; ++e) acc[a][e] = __builtin_fma(hd[a], wd[e], acc[a][e]);
         }
+    };
+    issue(0, 0);
+    if (nch > 1) issue(1, 1);
+    int j = 0, b = 0;   // chunk j in stage b
+    for (; j + 2 < nch; ++j) {
+        // this wave's copies of chunk j are done once only chunk j + 1's remain
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        // every wave's copies of chunk j have landed, and every wave has read
+        // chunk j - 1 (its reads completed before its sums), whose stage is
+        // refilled next. A bare barrier: __syncthreads' fence would also wait
+        // for the copies still in flight.
+        asm volatile("s_barrier" ::: "memory");
+        issue(j + 2, b == 0 ? 2 : b - 1);
+        sum_chunk(j, b);
         b = b == RL_STAGES - 1 ? 0 : b + 1;
     }
+    if (j + 1 < nch) {   // chunk nch - 2: only chunk nch - 1's copies may remain
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+        sum_chunk(j, b);
+        b = b == RL_STAGES - 1 ? 0 : b + 1;
+        ++j;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last chunk
+    asm volatile("s_barrier" ::: "memory");
+    sum_chunk(j, b);
     __syncthreads();   // the stages become the reduction buffer
     double *rd = reinterpret_cast<double *>(&stage[0][0][0]) + w * RL_PAIRS * RL_LD;
     const int q = lane & 3, p = lane >> 2;
@@ -1210,6 +1224,25 @@ static bool moe_mfma_ok(const localai_qmat *gu, const localai_qmat *dn, const fl
            (reinterpret_cast<uintptr_t>(h) & 15) == 0 && I % MT_ROWS == 0 && gu->g.cols == H && dn->g.cols == I;
 }
 
+// Whether launch_moe would have to build the row planes of gu or dn (a
+// hipMalloc, qmat_planes) for these sizes: the same path choice as
+// launch_moe (expert GEMMs from MOE_GEMM_TOKENS tokens on, read the tile
+// form where there is one; below that the MFMA decode kernels, else the
+// grouped VALU kernels over the row planes), true only where the handle does
+// not hold the planes yet.
+bool moe_would_build_planes(const float *h, int64_t T, int64_t H, const localai_qmat *gu, const localai_qmat *dn) {
+    const int64_t I = gu->g.rows / 2;
+    bool need_gu, need_dn;
+    if (T >= MOE_GEMM_TOKENS) {
+        need_gu = !(gu->tiles && I % MT_ROWS == 0);
+        need_dn = !dn->tiles;
+    } else {
+        need_gu = need_dn = !moe_mfma_ok(gu, dn, h, H, I);
+    }
+    auto missing = [](const localai_qmat *m) { return __atomic_load_n(&m->data, __ATOMIC_ACQUIRE) == nullptr; };
+    return (need_gu && missing(gu)) || (need_dn && missing(dn));
+}
+
 // Grouped decode kernels. gate_up: one super-block per wave (up to 16
 // waves), or four past 16 super-blocks, one gate and one up tile per
 // workgroup. down: at most 8 waves of SPW super-blocks and RT = 2 row tiles
@@ -1443,6 +1476,28 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
                            tb.ysl, tb.pos, topk_w, k, (int)H, out);
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
+}
+
+// One of the two expert GEMMs of the prefill path (which = 0: gate_up with
+// SiLU*up into the act rows, 1: down into the per-assignment rows), run again
+// on the routing tables, f16 rows and act rows that the last launch_moe over
+// T tokens left in ws: the measurement of one kernel of the layer alone.
+int launch_moe_expert_gemm(const localai_qmat *gu, const localai_qmat *dn, int64_t T, int64_t E, int k, void *ws,
+                           int which, hipStream_t s) {
+    const int64_t H = gu->g.cols, I = gu->g.rows / 2;
+    MoeTables tb = carve(ws, T, E, k, H, I);
+    if (tb.tile_w <= 0) return fail(LOCALAI_EARG, "moe expert gemm: fewer tokens than the expert GEMM path takes");
+    if (which == 0) {
+        const bool tiled = gu->tiles && I % MT_ROWS == 0;
+        if (!tiled && !gu->data) return fail(LOCALAI_ESTATE, "moe expert gemm: run the layer once first");
+        return launch_moe_gemm(gu->g, tiled ? nullptr : gu->data, tiled ? gu->tiles : nullptr, gu->tile_bytes, true,
+                               tb.xh_gu, f16_stride(H), tb.inv_gu, tb.perm, k, tb.act, I, I, tb.tile_e, tb.tile_p0,
+                               tb.tile_n, tb.n_tiles, tb.max_tiles, s);
+    }
+    if (!dn->tiles && !dn->data) return fail(LOCALAI_ESTATE, "moe expert gemm: run the layer once first");
+    return launch_moe_gemm(dn->g, dn->tiles ? nullptr : dn->data, dn->tiles, dn->tile_bytes, false, tb.xh_dn,
+                           f16_stride(I), tb.inv_dn, nullptr, 1, tb.ysl, H, I, tb.tile_e, tb.tile_p0, tb.tile_n,
+                           tb.n_tiles, tb.max_tiles, s);
 }
 
 // Zeroes the counter block of moe_decode1_kernel (a kernel, not a memset, so

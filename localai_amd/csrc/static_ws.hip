@@ -76,9 +76,16 @@ int localai_hip_moe_forward_static(const float *h, int64_t T, int64_t H, const f
         return fail(LOCALAI_EARG, "moe (static workspace): these sizes need " + std::to_string(need) +
                                       " bytes of workspace, more than the library's " +
                                       std::to_string(STATIC_WS_BYTES));
+    // Paths that read the row planes of a handle holding only the tile form
+    // (Q8_0 experts below 32 tokens, rows over 32 super-blocks, ...) would
+    // build them with hipMalloc: refused before any launch.
+    if (gu->g.rows % 2 == 0 && moe_would_build_planes(h, T, H, gu, dn))
+        return fail(LOCALAI_ETYPE, "moe (static workspace): these experts and sizes take a path that reads row "
+                                   "planes the handles do not hold yet; this entry point allocates nothing");
     if (int st = ensure_device()) return st;
     void *ws = nullptr;
     if (int st = scratch_ptr(&ws)) return st;
+    NoAllocScope no_alloc;   // qmat_planes refuses rather than allocates, whatever the path
     return localai_hip_moe_forward(h, T, H, rw, rb, E, k, gu, dn, out, topk_idx, topk_w, ws, STATIC_WS_BYTES,
                                    stream);
 }

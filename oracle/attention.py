@@ -6,8 +6,10 @@ scores, max-shifted softmax, weighted values) with the output gate of
 engine/qwen35.py:158-182 (sigmoid as engine/qwen35.py:17-19).
 
 delta_net_step restates engine/numba_kernels.py:11-45 in float32 in the
-reference loop's operation order: the state scaled by exp(decay) (the fp64
-exponential rounded once to float32), pred accumulated over ki ascending with
+reference loop's operation order: the state scaled by exp(decay) (by
+default the fp64 exponential rounded once to float32, which is what the GPU
+kernel computes; NumPy's float32 exponential, the reference's own, on
+request), pred accumulated over ki ascending with
 each product and each sum rounded on its own, delta = (v - pred) * beta, then
 the rank-one update and core in the same order. NumPy's float32 elementwise
 operations round exactly as the scalar loop does, so the loop over ki is
@@ -78,16 +80,25 @@ def gqa_decode_f32(q, k_cache, v_cache, position, n_heads, n_kv_heads, head_dim,
     return np.einsum('hl,hld->hd', probs, vh, optimize=True).reshape(-1)
 
 
-def delta_net_step(state, q, k, v, decay, beta):
+def delta_net_step(state, q, k, v, decay, beta, factor_exp='rounded'):
     """engine/numba_kernels.py:11-45 in float32, the loop's rounding order.
-    Returns (state', core) without changing `state`."""
+    Returns (state', core) without changing `state`.
+
+    factor_exp: 'rounded' takes exp(decay) as the fp64 exponential rounded
+    once to float32 (what the GPU kernel computes); 'numpy_f32' takes NumPy's
+    float32 exponential of the float32 decay, as the reference evaluates
+    np.exp on float32 values (engine/numba_kernels.py:25,
+    engine/qwen35.py:242). The two factors can differ in the last bit."""
     S = np.array(state, dtype=np.float32, copy=True)
     q = np.asarray(q, np.float32)
     k = np.asarray(k, np.float32)
     v = np.asarray(v, np.float32)
     beta = np.asarray(beta, np.float32)
     heads, kd, vd = S.shape
-    factor = np.exp(np.asarray(decay, np.float64)).astype(np.float32)    # :25
+    if factor_exp == 'numpy_f32':
+        factor = np.exp(np.asarray(decay, np.float32))                      # :25
+    else:
+        factor = np.exp(np.asarray(decay, np.float64)).astype(np.float32)
     pred = np.zeros((heads, vd), np.float32)
     for ki in range(kd):                                                   # :29-34
         S[:, ki, :] = S[:, ki, :] * factor[:, None]

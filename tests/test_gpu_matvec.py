@@ -107,6 +107,35 @@ def test_llama3_8b_shapes(name, t, rows, cols):
     assert err < 1e-5, f'{name}: {err}'
 
 
+@pytest.mark.parametrize('t', (14, 12))
+def test_vocab_head_128256x4096(t):
+    """The Llama-3-8B vocabulary head (engine/model.py:235-237, output.weight
+    128256 x 4096: Q6_K in a Q4_K_M file, Q4_K checked too), 8016 row tiles
+    in one launch: the first and last 64 rows and 3000 sampled rows against
+    the oracle (its rows sliced out of the GGML bytes), and every output
+    finite and repeatable bit for bit."""
+    from localai_amd import device, synth
+    rows, cols = 128256, 4096
+    rng = np.random.default_rng(128 + t)
+    raw = synth.quant_tensor(rng, t, rows, cols)
+    x = synth.activations(rng, cols)
+    q = device.QMat.from_ggml(raw, t, rows, cols)
+    xd = device.to_device_f32(x)
+    y = q.matvec(xd).cpu().numpy()
+    y2 = q.matvec(xd).cpu().numpy()
+    q.close()
+    assert np.isfinite(y).all()
+    np.testing.assert_array_equal(y.view(np.uint32), y2.view(np.uint32))
+    rowb = (cols // 256) * (210 if t == 14 else 144)
+    sel = np.unique(np.concatenate([np.arange(64), np.arange(rows - 64, rows),
+                                    rng.choice(rows, 3000, replace=False)]))
+    buf = np.frombuffer(raw, np.uint8).reshape(rows, rowb)
+    want = quant.matvec_exact(buf[sel].tobytes(), t, len(sel), cols, x)
+    err = normwise_rel(y[sel], want)
+    print(f'vocab head type {t}: normwise {err:.2e} over {len(sel)} rows', flush=True)
+    assert err < 1e-5
+
+
 def test_expert_slices_of_a_3d_tensor():
     """[E, rows, cols] tensor; expert e is the byte slice of engine/zaya.py:144-150."""
     from localai_amd import device

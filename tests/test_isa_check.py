@@ -88,9 +88,68 @@ def test_lds_dma_writes_no_register():
         s_endpgm''') == []
 
 
+def ring(body, per_stage=2):
+    return isa_check.lds_ring_violations(isa_check.kernel_lines(listing(body), 'kernel'), per_stage)
+
+
+# a two-ahead ring of LDS stages with two copies per stage, shaped like
+# moe_route_logits_kernel: chunks 0 and 1 requested up front; per pass of the
+# loop: wait, barrier, request chunk j + 2, read chunk j; then chunk n - 2
+# (nothing more to request) and the last chunk after a wait for every copy
+RING = '''
+        global_load_lds_dwordx4 v[2:3], off
+        global_load_lds_dwordx4 v[4:5], off
+        global_load_lds_dwordx4 v[2:3], off
+        global_load_lds_dwordx4 v[4:5], off
+.LBB0_1:
+        s_waitcnt vmcnt({loop})
+        s_barrier
+        global_load_lds_dwordx4 v[2:3], off
+        global_load_lds_dwordx4 v[4:5], off
+        ds_read_b128 v[8:11], v1
+        s_cbranch_scc1 .LBB0_1
+        s_waitcnt vmcnt({peel})
+        s_barrier
+        ds_read_b128 v[8:11], v1
+        s_waitcnt vmcnt({last})
+        s_barrier
+        ds_read_b128 v[8:11], v1
+        s_endpgm'''
+
+
+def test_lds_ring_correct_waits_pass():
+    assert ring(RING.format(loop=2, peel=2, last=0)) == []
+
+
+def test_lds_ring_wait_too_lax_is_found():
+    bad = ring(RING.format(loop=3, peel=2, last=0))
+    assert [b[0] for b in bad] == [9]      # a copy of chunk j may not have landed
+
+
+def test_lds_ring_missing_last_wait_is_found():
+    # without the final vmcnt(0) the last chunk's copies (two barriers old
+    # by its read) may still be in flight
+    bad = ring(RING.format(loop=2, peel=2, last=2))
+    assert [b[0] for b in bad] == [16]
+    assert 'two or more barriers old' in bad[0][1]
+
+
+def test_lds_ring_plain_load_in_the_queue():
+    # a plain load issued after the prologue's copies is one more entry the
+    # loop's first wait must let go of: vmcnt(2) still leaves only chunk 1
+    # in flight, vmcnt(3) would leave a copy of chunk 0
+    body = RING.replace('        global_load_lds_dwordx4 v[4:5], off\n.LBB0_1:',
+                        '        global_load_lds_dwordx4 v[4:5], off\n        global_load_dword v20, v11, s[0:1]\n.LBB0_1:')
+    assert ring(body.format(loop=2, peel=2, last=0)) == []
+    assert ring(body.format(loop=3, peel=2, last=0)) != []
+
+
 @pytest.mark.skipif(shutil.which('hipcc') is None and not __import__('os').path.exists('/opt/rocm/bin/hipcc'),
                     reason='hipcc not installed')
 def test_counted_load_kernels_are_clean(tmp_path):
     from localai_amd import build
-    for src, kernel in build.COUNTED_LOADS:
-        isa_check.check_source(build.HIPCC, build.COMMON, build.CSRC / src, kernel, tmp_path / 'k.s')
+    for src, kernel, per_stage in build.COUNTED_LOADS:
+        if per_stage is None:
+            isa_check.check_source(build.HIPCC, build.COMMON, build.CSRC / src, kernel, tmp_path / 'k.s')
+        else:
+            isa_check.check_lds_ring(build.HIPCC, build.COMMON, build.CSRC / src, kernel, per_stage, tmp_path / 'k.s')

@@ -81,3 +81,43 @@ def test_eda_adds_prev_times_eda():
     t['eda'] = None
     _, s2, _, _, _ = zm.moe_block(t, 4, 1e-5, h, prev)
     np.testing.assert_array_equal(s2, s0)
+
+
+def test_softmax_pinned_by_scipy_on_known_logits():
+    """With W_mlp4 zero the logits are exactly its bias b (0 + b in fp32), so
+    the oracle's probabilities must be scipy.special.softmax(b) whatever the
+    router MLP computed: a softmax of 2 * logits, a missing max shift that
+    overflows, or a dropped term all fail here."""
+    from scipy.special import softmax
+    rng = np.random.default_rng(4)
+    t = _tensors(rng)
+    h = rng.standard_normal(64).astype(np.float32)
+    t['mlp4'] = np.zeros_like(t['mlp4'])
+    for scale in (0.1, 1.0, 8.0, 60.0, 200.0):
+        b = (rng.standard_normal(5) * scale).astype(np.float32)
+        t['mlp4_b'] = b
+        _, _, probs, e, _ = zm.moe_block(t, 4, 1e-5, h, None)
+        want = softmax(b.astype(np.float64))
+        big = want > 1e-30
+        # fp32 evaluation: the shifted logit b - max(b) carries its own
+        # rounding, which exp turns into a relative error of |b - max| * 2^-24
+        tol = (np.abs(b.astype(np.float64) - b.max()) + 8.0) * 2.0 ** -23
+        assert np.all(np.abs(probs[big] - want[big]) / want[big] <= tol[big])
+        assert np.all(np.abs(probs[~big]) < 1e-30)
+        assert e == int(np.argmax(b))
+
+
+def test_two_route_softmax_is_the_logistic():
+    """Two routes (one expert + the skip route): probs[1] = expit(b1 - b0)
+    exactly in closed form; the skip route wins when its logit is larger."""
+    from scipy.special import expit
+    rng = np.random.default_rng(5)
+    t = _tensors(rng, E=1)
+    h = rng.standard_normal(64).astype(np.float32)
+    t['mlp4'] = np.zeros_like(t['mlp4'])
+    for d in (-30.0, -5.0, -0.5, 0.25, 3.0, 20.0):
+        t['mlp4_b'] = np.array([0.0, d], np.float32)
+        _, _, probs, e, _ = zm.moe_block(t, 1, 1e-5, h, None)
+        assert abs(float(probs[1]) - expit(d)) <= 1e-6 * expit(d) + 1e-12
+        assert abs(float(probs[0]) - expit(-d)) <= 1e-6 * expit(-d) + 1e-12
+        assert e == (1 if d > 0 else 0)
