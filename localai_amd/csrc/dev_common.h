@@ -109,4 +109,11 @@ __device__ __forceinline__ float silu(float g) {
     return g / (1.0f + expf(-c));
 }
 
+// silu with the hardware exponential and reciprocal (a few ulp), for
+// epilogues of the f16-operand GEMMs, whose own error is ~2^-12
+__device__ __forceinline__ float silu_fast(float g) {
+    const float c = fminf(fmaxf(g, -80.0f), 80.0f);
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-c));
+}
+
 }  // namespace lq

@@ -517,19 +517,128 @@ __device__ __forceinline__ void gt_half(const GtRaw<T> &w0, const GtRaw<T> &w1, 
     }
 }
 
+// The K loop and epilogue of one workgroup with NV 16-token MFMA tiles of
+// the BN holding tokens: expert tiles end partway, and each NV is its own
+// copy of the loop (no per-MFMA branches, which made the compiler copy the
+// accumulators around every conditional MFMA).
+template <int T, int BN, int MODE, int NW, int NV>
+__device__ __forceinline__ void gt_main(const GemmArgs &a, _Float16 (*Xs)[BN * GM_BK], float *tsc,
+                                        const uint8_t *w0p, const uint8_t *w1p, int64_t p0, int tn, int64_t t0,
+                                        int64_t t1, int64_t tiles, int64_t nsb) {
+    constexpr int XN = BN * 16 / (64 * NW);   // 16-byte x chunks per thread and step
+    constexpr int BB = mt_block_bytes(T);
+    const lq_geom &g = a.g;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+
+    // x loader: instruction i of wave w fills tile chunks (NW i + w) * 64 + lane,
+    // i.e. token row (NW i + w) * 4 + lane / 16, position lane % 16, from the
+    // row's chunk (lane % 16) ^ (row % 16); straight from global memory into
+    // LDS (no registers), waited for with vmcnt before the step's barrier.
+    // Rows of the MFMA tiles past NV are not read.
+    const _Float16 *xsrc[XN];
+#pragma unroll
+    for (int i = 0; i < XN; ++i) {
+        const int row = (NW * i + wave) * 4 + (lane >> 4), c = (lane & 15) ^ (row & 15);
+        xsrc[i] = a.Xh + gemm_xrow(a, p0 + (row < tn ? row : 0)) * a.ldh + 8 * c;
+    }
+    auto load_x = [&](int buf, int64_t step) {
+#pragma unroll
+        for (int i = 0; i < XN; ++i)
+            if ((NW * i + wave) * 4 < 16 * NV)   // uniform per wave
+                __builtin_amdgcn_global_load_lds(
+                    (const void *)(xsrc[i] + step * GM_BK),
+                    (__attribute__((address_space(3))) void *)&Xs[buf][(NW * i + wave) * 64 * 8], 16, 0, 0);
+    };
+
+    lq_f4 acc[NV][2];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        acc[i][0] = lq_f4{0.0f, 0.0f, 0.0f, 0.0f};
+        acc[i][1] = lq_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    // prologue: half 0 of block 0, and each token's output scale (one
+    // lookup per token rather than one per output value)
+    GtRaw<T> a0 = gt_load<T>(w0p, 0, lane), a1 = gt_load<T>(w1p, 0, lane);
+    load_x(0, 0);
+    if (tid < BN) tsc[tid] = a.inv[gemm_xrow(a, p0 + (tid < tn ? tid : 0))];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    // step loop over blocks: half 0 from Xs[0] / (a0, a1), half 1 from Xs[1] / (b0, b1);
+    // the next half's weights and x are requested before the current half's MFMAs
+    for (int64_t sb = 0; sb < nsb; ++sb) {
+        GtRaw<T> b0 = gt_load<T>(w0p + sb * BB, 1, lane), b1 = gt_load<T>(w1p + sb * BB, 1, lane);
+        if constexpr (T == LQ_Q4_K) {
+            b0.hd = a0.hd;
+            b1.hd = a1.hd;
+        }
+        load_x(1, 2 * sb + 1);
+        // nothing crosses: the loads stay ahead of the MFMAs, and the next
+        // half's decode stays behind them (it would wait on these loads)
+        __builtin_amdgcn_sched_barrier(0);
+        gt_half<T, 0, NV>(a0, a1, Xs[0], lane, acc);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // next block (the last block re-reads itself: Xs[0] is not read again)
+        const int64_t nx = sb + 1 < nsb ? sb + 1 : sb;
+        a0 = gt_load<T>(w0p + nx * BB, 0, lane);
+        a1 = gt_load<T>(w1p + nx * BB, 0, lane);
+        load_x(0, 2 * nx);
+        __builtin_amdgcn_sched_barrier(0);
+        gt_half<T, 1, NV>(b0, b1, Xs[1], lane, acc);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    // D[m][n]: lane holds tokens 4 (lane / 16) + v of token tile i, row lane % 16 of row tile j.
+    // Addresses advance from one base per row; 32-bit offsets (a tile spans
+    // at most BN rows of Y)
+    const int fr = lane & 15;
+    if constexpr (MODE == GM_MOE_GATE_UP) {
+        const int64_t r = t0 * MT_ROWS + fr;
+        float *yb = a.Y + p0 * a.y_ts + r;
+        const bool rok = r < a.inter;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int lt = 16 * i + 4 * (lane >> 4) + v;
+                if (lt >= tn || !rok) continue;
+                const float sc = tsc[lt];
+                yb[(uint32_t)lt * (uint32_t)a.y_ts] = silu_fast(acc[i][0][v] * sc) * (acc[i][1][v] * sc);
+            }
+        }
+    } else {
+        const int64_t r0 = t0 * MT_ROWS + fr, r1 = t1 * MT_ROWS + fr;
+        const bool ok0 = t0 < tiles && r0 < g.rows, ok1 = t1 < tiles && r1 < g.rows;
+        float *yb0 = a.Y + p0 * a.y_ts + r0 * a.y_rs, *yb1 = a.Y + p0 * a.y_ts + r1 * a.y_rs;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int lt = 16 * i + 4 * (lane >> 4) + v;
+                if (lt >= tn) continue;
+                const float sc = tsc[lt];
+                const uint32_t o = (uint32_t)lt * (uint32_t)a.y_ts;
+                if (ok0) yb0[o] = acc[i][0][v] * sc;
+                if (ok1) yb1[o] = acc[i][1][v] * sc;
+            }
+        }
+    }
+}
+
 // NW waves per workgroup (4 or 8): 32 NW weight rows (gate_up: 16 NW gate and
 // 16 NW up rows) share one staged x tile; 8 waves halve the x bytes each
 // weight byte brings along (the MoE expert tiles)
 template <int T, int BN, int MODE, int NW = 4>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_tile_kernel(GemmArgs a) {
     constexpr int NI = BN / 16;            // 16-token MFMA tiles per wave
-    constexpr int XN = BN * 16 / (64 * NW);   // 16-byte x chunks per thread and step
     constexpr int BB = mt_block_bytes(T);
     __shared__ __attribute__((aligned(16))) _Float16 Xs[2][BN * GM_BK];
+    __shared__ float tsc[BN];              // the output scale of each token of the tile
     const lq_geom &g = a.g;
     // wave index made wave-uniform: row-tile addresses go to scalar registers
     // (MoE Q4_K GEMMs 162 -> 128 VGPRs; gate_up 85 -> 81 us, down 55 -> 48 us)
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int wave = wave_id();
     const uint8_t *Wt = a.Wt;
     int64_t p0;
     int tn;
@@ -566,81 +675,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_tile_kernel(GemmArgs a) 
     }
     const uint8_t *w0p = Wt + (t0 < tiles ? t0 : tiles - 1) * nsb * BB;
     const uint8_t *w1p = Wt + (t1 < tiles ? t1 : tiles - 1) * nsb * BB;
-
-    // x loader: instruction i of wave w fills tile chunks (NW i + w) * 64 + lane,
-    // i.e. token row (NW i + w) * 4 + lane / 16, position lane % 16, from the
-    // row's chunk (lane % 16) ^ (row % 16); straight from global memory into
-    // LDS (no registers), waited for with vmcnt before the step's barrier
-    const _Float16 *xsrc[XN];
-#pragma unroll
-    for (int i = 0; i < XN; ++i) {
-        const int row = (NW * i + wave) * 4 + (lane >> 4), c = (lane & 15) ^ (row & 15);
-        xsrc[i] = a.Xh + gemm_xrow(a, p0 + (row < tn ? row : 0)) * a.ldh + 8 * c;
-    }
-    auto load_x = [&](int buf, int64_t step) {
-#pragma unroll
-        for (int i = 0; i < XN; ++i)
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(xsrc[i] + step * GM_BK),
-                (__attribute__((address_space(3))) void *)&Xs[buf][(NW * i + wave) * 64 * 8], 16, 0, 0);
-    };
-
-    lq_f4 acc[NI][2];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        acc[i][0] = lq_f4{0.0f, 0.0f, 0.0f, 0.0f};
-        acc[i][1] = lq_f4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-
-    // prologue: half 0 of block 0
-    GtRaw<T> a0 = gt_load<T>(w0p, 0, lane), a1 = gt_load<T>(w1p, 0, lane);
-    load_x(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    // step loop over blocks: half 0 from Xs[0] / (a0, a1), half 1 from Xs[1] / (b0, b1);
-    // the next half's weights and x are requested before the current half's MFMAs
-    for (int64_t sb = 0; sb < nsb; ++sb) {
-        GtRaw<T> b0 = gt_load<T>(w0p + sb * BB, 1, lane), b1 = gt_load<T>(w1p + sb * BB, 1, lane);
-        if constexpr (T == LQ_Q4_K) {
-            b0.hd = a0.hd;
-            b1.hd = a1.hd;
-        }
-        load_x(1, 2 * sb + 1);
-        // nothing crosses: the loads stay ahead of the MFMAs, and the next
-        // half's decode stays behind them (it would wait on these loads)
-        __builtin_amdgcn_sched_barrier(0);
-        gt_half<T, 0, NI>(a0, a1, Xs[0], lane, acc);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        // next block (the last block re-reads itself: Xs[0] is not read again)
-        const int64_t nx = sb + 1 < nsb ? sb + 1 : sb;
-        a0 = gt_load<T>(w0p + nx * BB, 0, lane);
-        a1 = gt_load<T>(w1p + nx * BB, 0, lane);
-        load_x(0, 2 * nx);
-        __builtin_amdgcn_sched_barrier(0);
-        gt_half<T, 1, NI>(b0, b1, Xs[1], lane, acc);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-    }
-    // D[m][n]: lane holds tokens 4 (lane / 16) + v of token tile i, row lane % 16 of row tile j
-    const int fr = lane & 15;
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int lt = 16 * i + 4 * (lane >> 4) + v;
-            if (lt >= tn) continue;
-            const int64_t p = p0 + lt;
-            const float sc = a.inv[gemm_xrow(a, p)];
-            if constexpr (MODE == GM_MOE_GATE_UP) {
-                const int64_t r = t0 * MT_ROWS + fr;
-                if (r < a.inter) a.Y[p * a.y_ts + r] = silu(acc[i][0][v] * sc) * (acc[i][1][v] * sc);
-            } else {
-                const int64_t r0 = t0 * MT_ROWS + fr, r1 = t1 * MT_ROWS + fr;
-                if (t0 < tiles && r0 < g.rows) a.Y[p * a.y_ts + r0 * a.y_rs] = acc[i][0][v] * sc;
-                if (t1 < tiles && r1 < g.rows) a.Y[p * a.y_ts + r1 * a.y_rs] = acc[i][1][v] * sc;
-            }
-        }
+    if constexpr (MODE == GM_DENSE || NI != 4) {
+        gt_main<T, BN, MODE, NW, NI>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
+    } else {
+        // expert tiles: one copy of the loop per count of 16-token tiles
+        const int nv = __builtin_amdgcn_readfirstlane((tn + 15) >> 4);
+        if (nv == 1) gt_main<T, BN, MODE, NW, 1>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
+        else if (nv == 2) gt_main<T, BN, MODE, NW, 2>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
+        else if (nv == 3) gt_main<T, BN, MODE, NW, 3>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
+        else gt_main<T, BN, MODE, NW, 4>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
     }
 }
 
