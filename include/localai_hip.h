@@ -63,13 +63,26 @@ int localai_hip_dequant(int ggml_type, const void *raw_dev, int64_t n_values,
                         float *out_dev, void *stream);
 
 /* y[t, r] = sum_c w[r, c] * x[t, c] for an fp32 matrix w [rows, cols] and
- * x [tokens, cols] -> y [tokens, rows] (all device, row-major). The device
- * path for GGUF matrices outside the packed types (F32, F16, Q4_1, Q5_0,
- * Q5_1), decoded once by localai_hip_dequant; it replaces the reference's
- * dequantize + NumPy `weights @ x` fallback (engine/gguf_parser.py:269-289,
- * :350-358). Results do not depend on the launch (fixed summation order). */
+ * x [tokens, cols] -> y [tokens, rows] (all device, row-major): the device
+ * path for F32 GGUF matrices (and any matrix already decoded to fp32 by
+ * localai_hip_dequant); it replaces the reference's NumPy `weights @ x`
+ * (engine/gguf_parser.py:269-289, :350-358). Results do not depend on the
+ * launch (fixed summation order). */
 int localai_hip_f32_matvec(const float *w_dev, int64_t rows, int64_t cols, const float *x_dev,
                            int64_t tokens, float *y_dev, void *stream);
+
+/* y[t, r] = sum_c W[r, c] * x[t, c] for t < tokens, straight from the GGML
+ * bytes of W [rows, cols] on the device (the file's bytes, no expansion):
+ * F16, Q4_1, Q5_0, Q5_1 -- the types without a packed kernel -- and F32,
+ * Q4_0, Q8_0. Each block is decoded in registers with the formulas of
+ * engine/dequant.py (bit-identical values) and multiplied in fp32 with a
+ * fixed summation order. Replaces the dequantize + NumPy `weights @ x`
+ * fallback of GGUFFile.matvec / .matmul (engine/gguf_parser.py:269-289,
+ * :350-358) and its fp32 / fp16 matrix caches (:65-69). cols a multiple of 8
+ * and of the block size; x 16-byte aligned (and W for F32 / F16); y is
+ * [tokens, rows]. LOCALAI_ETYPE for other types. */
+int localai_hip_ggml_matvec(int ggml_type, const void *w_dev, int64_t rows, int64_t cols, const float *x_dev,
+                            int64_t tokens, float *y_dev, void *stream);
 
 /* ---- device-resident weight matrices ------------------------------------ */
 

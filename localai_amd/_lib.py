@@ -26,6 +26,7 @@ SIGNATURES = {
     'localai_hip_block_layout': (_c_int, [_c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
     'localai_hip_dequant': (_c_int, [_c_int, _vp, _c_i64, _vp, _vp]),
     'localai_hip_f32_matvec': (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
+    'localai_hip_ggml_matvec': (_c_int, [_c_int, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
     'localai_hip_qmat_create': (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp,
                                          ctypes.POINTER(_vp)]),
     'localai_hip_qmat_destroy': (_c_int, [_vp]),

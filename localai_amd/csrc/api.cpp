@@ -169,6 +169,14 @@ int localai_hip_f32_matvec(const float *w, int64_t rows, int64_t cols, const flo
     return launch_f32_matvec(w, rows, cols, x, tokens, y, (hipStream_t)stream);
 }
 
+int localai_hip_ggml_matvec(int t, const void *w, int64_t rows, int64_t cols, const float *x, int64_t tokens,
+                            float *y, void *stream) {
+    clear_error();
+    if (!w || !x || !y) return fail(LOCALAI_EARG, "null pointer");
+    if (int st = ensure_device()) return st;
+    return launch_ggml_matvec(t, w, rows, cols, x, tokens, y, (hipStream_t)stream);
+}
+
 int localai_hip_zaya_router(const float *r0, const float *b_inp, const float *prev, const float *eda,
                             const float *norm_w, float eps, int64_t r, const float *w_gate, const float *b_gate,
                             int64_t r1, const float *w_mlp2, const float *b_mlp2, int64_t r2, const float *w_mlp4,
@@ -314,6 +322,11 @@ int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x, fl
     one.batch = 1;
     if (m->tiles && ntok == 1 && mt_matvec_ok(one))
         return launch_matvec_mfma(one, m->tiles + expert * m->tile_bytes, x, y, (hipStream_t)stream);
+    // several vectors of a tile-form handle: the weights in registers once,
+    // each vector through the one-vector arithmetic (no row planes needed)
+    if (m->tiles && mt_matvec_ok(one) && (reinterpret_cast<uintptr_t>(x) & 15) == 0)
+        return launch_matvec_mfma_tok(one, m->tiles + expert * m->tile_bytes, x, m->g.cols, y, m->g.rows, ntok,
+                                      (hipStream_t)stream);
     int st;
     const uint8_t *planes = qmat_planes(m, (hipStream_t)stream, &st);
     if (!planes) return st;

@@ -430,6 +430,83 @@ int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, floa
     return LOCALAI_OK;
 }
 
+// Several vectors, one matrix: y[t] = W x[t] for t < ntok. The workgroup's
+// row tiles are loaded into registers once (every block of the wave at
+// once) and each vector goes through the single-vector arithmetic of
+// mt_pass in turn (so y[t] is bit-identical to a one-vector call on x[t]);
+// the next vector's x is requested before the current one is summed. The
+// weights are read from HBM once per call however many vectors there are.
+template <int TYPE, int SPW, int RT, int MAXT>
+__global__ __launch_bounds__(MAXT) void gemv_mfma_tok(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
+                                                      int64_t tiles, const float *__restrict__ x, int64_t ldx,
+                                                      float *__restrict__ y, int64_t ldy, int ntok) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = lane_id(), wv = wave_id(), sb0 = wv * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    const int64_t blk = blockIdx.x;
+    const int i = threadIdx.x;
+    const int64_t tile = blk * RT + ((i >> 4) & (RT - 1)), row = tile * MT_ROWS + (i & 15);
+    const bool mine = i < RT * 16 && tile < tiles && row < rows;
+    float4 xv[1][SPW];
+    mt_load_x<SPW>(xv[0], x, nb, sb0, lane);
+    MtW<TYPE> w[RT][SPW];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        const int64_t tl = blk * RT + t < tiles ? blk * RT + t : tiles - 1;
+        mt_load_tile<TYPE, SPW>(w[t], Wt + tl * nb * mt_block_bytes(TYPE), nb, sb0, nsb, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    for (int t = 0; t < ntok; ++t) {
+        float4 xn[SPW];
+        mt_load_x<SPW>(xn, x + (int64_t)(t + 1 < ntok ? t + 1 : t) * ldx, nb, sb0, lane);
+        float *fin;
+        mt_pass<TYPE, SPW, RT, 1>(w, xv, nsb, smem, fin);
+        if (mine) y[(int64_t)t * ldy + row] = fin[i];
+#pragma unroll
+        for (int k = 0; k < SPW; ++k) xv[0][k] = xn[k];
+    }
+}
+
+int launch_matvec_mfma_tok(const lq_geom &g, const uint8_t *Wt, const float *x, int64_t ldx, float *y, int64_t ldy,
+                           int ntok, hipStream_t s) {
+    if (!mt_matvec_ok(g)) return fail(LOCALAI_ETYPE, "mfma matvec: Q4_K / Q6_K, or Q8_0 with cols % 256 == 0");
+    if ((reinterpret_cast<uintptr_t>(x) & 15) || ldx % 4)
+        return fail(LOCALAI_EARG, "mfma matvec: x rows must be 16-byte aligned");
+    if (ntok < 1) return LOCALAI_OK;
+    const int nb = (int)mt_nsb(g);
+    if (nb > 72) return fail(LOCALAI_EARG, "mfma matvec: K too large (more than 18432 values)");
+    const bool q6 = g.type == LQ_Q6_K, q8 = g.type == LQ_Q8_0;
+    const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
+    // up to 32 super-blocks: up to 16 waves (SPW = ceil(nb / 16)), two Q4_K
+    // tiles per workgroup where one super-block per wave leaves room, as in
+    // the one-vector plan; longer rows: 8 waves of ceil(nb / 8) blocks (up to
+    // 9 for K <= 18432), which fit in registers only below 16 waves
+    const int spw = nb <= 32 ? (nb + 15) / 16 : (nb + 7) / 8, waves = (nb + spw - 1) / spw;
+    const int rt = spw == 1 && tiles >= 768 && !q6 ? 2 : 1;
+    dim3 grid((unsigned)((tiles + rt - 1) / rt)), block(64 * waves);
+    const size_t lds = mt_lds_bytes(g.type, waves, spw, 1, rt);
+#define MT_T(S, R, M)                                                                                          \
+    do {                                                                                                       \
+        if (q6) hipLaunchKernelGGL((gemv_mfma_tok<LQ_Q6_K, S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, \
+                                   ldx, y, ldy, ntok);                                                         \
+        else if (q8) hipLaunchKernelGGL((gemv_mfma_tok<LQ_Q8_0, S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, \
+                                        x, ldx, y, ldy, ntok);                                                 \
+        else hipLaunchKernelGGL((gemv_mfma_tok<LQ_Q4_K, S, R, M>), grid, block, lds, s, Wt, g.rows, nb, tiles, x, ldx, \
+                                y, ldy, ntok);                                                                 \
+    } while (0)
+    switch (spw) {
+        case 1: if (rt == 2) MT_T(1, 2, 1024); else MT_T(1, 1, 1024); break;
+        case 2: MT_T(2, 1, 1024); break;
+        case 5: MT_T(5, 1, 512); break;
+        case 6: MT_T(6, 1, 512); break;
+        case 7: MT_T(7, 1, 512); break;
+        case 8: MT_T(8, 1, 512); break;
+        default: MT_T(9, 1, 512); break;
+    }
+#undef MT_T
+    LQ_HIP(hipGetLastError());
+    return LOCALAI_OK;
+}
+
 int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const *Wt, const float *x,
                             float *const *y, hipStream_t s) {
     if (n < 1 || n > MT_MAX_JOBS) return fail(LOCALAI_EARG, "mfma matvec: 1..8 matrices per fused launch");

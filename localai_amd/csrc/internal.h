@@ -40,6 +40,9 @@ int launch_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *packed, int di
 int launch_dequant_ggml(int t, const void *raw, int64_t n, float *out, hipStream_t s);
 int launch_f32_matvec(const float *W, int64_t rows, int64_t cols, const float *x, int64_t ntok, float *y,
                       hipStream_t s);
+// matvec from GGML bytes on the device (F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0; ggml_matvec.hip)
+int launch_ggml_matvec(int t, const void *W, int64_t rows, int64_t cols, const float *x, int64_t ntok, float *y,
+                       hipStream_t s);
 struct GemvPlan {
     int waves;        // waves per workgroup (split the K units)
     int slots;        // 64-value units per lane per wave
@@ -61,6 +64,9 @@ int launch_mt_unpack(const lq_geom &g, const uint8_t *tiles, int64_t tile_matrix
 const uint8_t *qmat_planes(const localai_qmat *m, hipStream_t s, int *status);
 bool mt_matvec_ok(const lq_geom &g);
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s);
+// several vectors x[t] (stride ldx) through the one-vector MFMA arithmetic, weights read once
+int launch_matvec_mfma_tok(const lq_geom &g, const uint8_t *Wt, const float *x, int64_t ldx, float *y, int64_t ldy,
+                           int ntok, hipStream_t s);
 int launch_matvec_mfma_many(int n, const lq_geom *const *g, const uint8_t *const *Wt, const float *x,
                             float *const *y, hipStream_t s);
 // the decode step's glue around a matvec (gemv_mfma.hip): prologue PRO / epilogue EPI

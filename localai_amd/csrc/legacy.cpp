@@ -140,6 +140,8 @@ int run(int t, const uint8_t *raw, const float *x, float *out, int rows, int col
     } else if (!st) {
         if (m->tiles && tokens == 1 && mt_matvec_ok(m->g)) {
             st = launch_matvec_mfma(m->g, m->tiles, g_x, g_y, s);
+        } else if (m->tiles && mt_matvec_ok(m->g)) {
+            st = launch_matvec_mfma_tok(m->g, m->tiles, g_x, cols, g_y, rows, tokens, s);
         } else {
             const uint8_t *planes = qmat_planes(m, s, &st);
             if (planes) st = launch_matvec(m->g, planes, g_x, cols, g_y, rows, tokens, s);

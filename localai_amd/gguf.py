@@ -125,6 +125,62 @@ class DenseMatrix:
         self.values = None
 
 
+class GgmlMatrix:
+    """GGML bytes of a [batch, rows, cols] matrix kept on the device as they are
+    in the file, with the QMat product interface (localai_hip_ggml_matvec:
+    blocks decoded in registers): F16, Q4_1, Q5_0 and Q5_1 matrices, which the
+    reference keeps as fp32 or fp16 caches (engine/gguf_parser.py:65-69)."""
+
+    def __init__(self, raw, ggml_type, batch, rows, cols):
+        t = device.torch()
+        block, bpb = block_layout(ggml_type)
+        self.ggml_type = int(ggml_type)
+        self.batch, self.rows, self.cols = int(batch), int(rows), int(cols)
+        self.matrix_bytes = self.rows * (self.cols // block) * bpb
+        host = np.frombuffer(raw, dtype=np.uint8)
+        if host.size != self.batch * self.matrix_bytes:
+            raise ValueError('tensor bytes do not match [batch, rows, cols]')
+        # each matrix starts 256-byte aligned (F16 rows need 16-byte alignment)
+        self.stride = -(-self.matrix_bytes // 256) * 256
+        self.bytes = t.empty(self.batch * self.stride, dtype=t.uint8, device=device.device())
+        for e in range(self.batch):
+            self.bytes[e * self.stride:e * self.stride + self.matrix_bytes].copy_(
+                t.from_numpy(host[e * self.matrix_bytes:(e + 1) * self.matrix_bytes].copy()))
+
+    @property
+    def device_bytes(self) -> int:
+        return self.bytes.numel()
+
+    def matvec(self, x, expert=0, out=None, stream=None):
+        t = device.torch()
+        squeeze = x.dim() == 1
+        x2 = x.reshape(1, -1) if squeeze else x
+        if x2.dtype != t.float32 or not x2.is_contiguous() or x2.data_ptr() % 16:
+            x2 = x2.to(t.float32).contiguous().clone()
+        if x2.shape[1] != self.cols:
+            raise ValueError(f'x has {x2.shape[1]} columns, matrix has {self.cols}')
+        if not 0 <= int(expert) < self.batch:
+            raise IndexError(f'expert {expert} outside [0, {self.batch})')
+        ntok = x2.shape[0]
+        if out is None:
+            out = t.empty((ntok, self.rows), dtype=t.float32, device=x2.device)
+        w = device.ptr(self.bytes) + int(expert) * self.stride
+        _lib.check(_lib.load().localai_hip_ggml_matvec(self.ggml_type, w, self.rows, self.cols, device.ptr(x2),
+                                                       ntok, device.ptr(out),
+                                                       ctypes.c_void_p(device.stream_ptr(stream))))
+        return out.reshape(-1) if squeeze else out
+
+    def matmul(self, x, expert=0, out=None, stream=None):
+        return self.matvec(x, expert=expert, out=out, stream=stream)
+
+    def close(self):
+        self.bytes = None
+
+
+# kept on the device as GGML bytes (GgmlMatrix) when rows are whole 8-value groups
+_RAW = (1, 3, 6, 7)
+
+
 class GGUFFile:
     def __init__(self, path):
         self.path = Path(path)
@@ -271,7 +327,9 @@ class GGUFFile:
 
     def device_matrix(self, name):
         """The device copy of matrix `name` ([out, in], or [experts, out, in]):
-        a QMat for the packed types, else a DenseMatrix; uploaded on first use."""
+        a QMat for the packed types, the GGML bytes (GgmlMatrix) for F16,
+        Q4_1, Q5_0 and Q5_1, an fp32 DenseMatrix for F32 (and rows that are
+        not whole 8-value groups); uploaded on first use."""
         hit = self._dev.get(name)
         if hit is not None:
             return hit
@@ -287,6 +345,8 @@ class GGUFFile:
         try:
             if info.ggml_type in _PACKED:
                 m = device.QMat.from_ggml(raw, info.ggml_type, rows, cols, batch)
+            elif info.ggml_type in _RAW and cols % 8 == 0:
+                m = GgmlMatrix(raw, info.ggml_type, batch, rows, cols)
             else:
                 from .dequant import dequantize_device
                 m = DenseMatrix(dequantize_device(raw, info.ggml_type, (batch * rows, cols)), batch, rows, cols)

@@ -143,3 +143,59 @@ def test_native_quant_cache_does_not_pin_the_mmap(model):
     # the entry of the closed map is dropped on the next use of the cache
     native_quant.matvec(raws[12], np.ones(COLS, np.float32), ROWS, COLS, 12)
     assert len(native_quant._cache) <= n_cached
+
+
+@pytest.mark.parametrize('t', (1, 3, 6, 7, 0, 2, 8))
+@pytest.mark.parametrize('rows,cols,tokens', [(1, 32 * 8, 1), (77, 512, 1), (257, 4096, 3), (33, 2048, 5)])
+def test_ggml_matvec_from_file_bytes(t, rows, cols, tokens):
+    """localai_hip_ggml_matvec on the GGML bytes as they are (F16, Q4_1,
+    Q5_0, Q5_1, and F32, Q4_0, Q8_0): against the fp64 product of the exact
+    decode, normwise 1e-5 (fp32 sums of exact products); repeated calls are
+    bit-identical."""
+    import ctypes
+    import torch
+    from localai_amd import _lib, device
+    if cols % 32 and t not in (0, 1):
+        pytest.skip('block types need cols % 32 == 0')
+    rng = np.random.default_rng(1000 * t + rows + tokens)
+    raw = random_ggml(rng, t, rows * cols)
+    x = rng.standard_normal((tokens, cols)).astype(np.float32)
+    w = torch.from_numpy(np.frombuffer(raw, np.uint8).copy()).to(device.device())
+    xd = device.to_device_f32(x)
+    lib = _lib.load()
+    outs = []
+    for _ in range(2):
+        y = torch.empty((tokens, rows), dtype=torch.float32, device=device.device())
+        _lib.check(lib.localai_hip_ggml_matvec(t, device.ptr(w), rows, cols, device.ptr(xd), tokens, device.ptr(y),
+                                               ctypes.c_void_p(device.stream_ptr())))
+        outs.append(y.cpu().numpy())
+    np.testing.assert_array_equal(bits(outs[0]), bits(outs[1]))
+    want = x.astype(np.float64) @ quant.dequantize(raw, t, (rows, cols)).astype(np.float64).T
+    assert normwise_rel(outs[0], want) < 1e-5
+
+
+def test_ggml_matvec_rejects_what_it_cannot_read():
+    import ctypes
+    import torch
+    from localai_amd import _lib, device
+    lib = _lib.load()
+    w = torch.zeros(4096, dtype=torch.uint8, device=device.device())
+    x = torch.zeros(64, dtype=torch.float32, device=device.device())
+    y = torch.empty(64, dtype=torch.float32, device=device.device())
+    p = device.ptr
+    assert lib.localai_hip_ggml_matvec(12, p(w), 1, 256, p(x), 1, p(y), None) == 2   # Q4_K: its own kernels
+    assert lib.localai_hip_ggml_matvec(3, p(w), 1, 48, p(x), 1, p(y), None) == 1     # not whole blocks
+    assert lib.localai_hip_ggml_matvec(1, p(w), 1, 12, p(x), 1, p(y), None) == 1     # not whole 8-value groups
+    assert lib.localai_hip_ggml_matvec(1, p(w) + 2, 1, 16, p(x), 1, p(y), None) == 1   # F16 rows unaligned
+
+
+def test_reader_keeps_f16_and_5bit_types_as_file_bytes(model):
+    """F16, Q4_1, Q5_0 and Q5_1 matrices stay on the device as their GGML
+    bytes (0.6 to 2 bytes per value instead of fp32's 4)."""
+    from localai_amd.gguf import GGUFFile, GgmlMatrix
+    path, raws, _ = model
+    with GGUFFile(path) as g:
+        for t in (1, 3, 6, 7):
+            m = g.device_matrix(f'blk.0.w{t}.weight')
+            assert isinstance(m, GgmlMatrix)
+            assert len(raws[t]) <= m.device_bytes < len(raws[t]) + 256

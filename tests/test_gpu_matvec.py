@@ -93,6 +93,35 @@ def test_multi_vector(t, ntok):
     assert normwise_rel(got, want) < 1e-5
 
 
+@pytest.mark.parametrize('t', (12, 14, 8))
+@pytest.mark.parametrize('rows,cols,ntok', [(200, 1024, 7), (14336, 4096, 3), (4096, 14336, 5), (300, 256 * 60, 2),
+                                            (48, 256 * 33, 4)])
+def test_multi_vector_on_the_tile_form(t, rows, cols, ntok):
+    """Several vectors through a Q4_K / Q6_K / Q8_0 handle run the tile-form
+    kernel: every y[t] equals the one-vector call on x[t] bit for bit, the
+    oracle within 1e-5 normwise, and the handle builds no row planes (its
+    device bytes do not change)."""
+    from localai_amd import _lib, device
+    rng = np.random.default_rng(rows + ntok + t)
+    raw = random_ggml(rng, t, rows * cols)
+    x = rng.standard_normal((ntok, cols)).astype(np.float32)
+    q = device.QMat.from_ggml(raw, t, rows, cols)
+    lib = _lib.load()
+    before = int(lib.localai_hip_qmat_device_bytes(q.handle))
+    xd = device.to_device_f32(x)
+    got = q.matvec(xd).cpu().numpy()
+    assert int(lib.localai_hip_qmat_device_bytes(q.handle)) == before
+    for i in range(ntok):
+        one = q.matvec(xd[i].contiguous()).cpu().numpy()
+        np.testing.assert_array_equal(got[i].view(np.uint32), one.view(np.uint32))
+    sel = np.arange(rows) if rows <= 4096 else np.unique(rng.choice(rows, 1500, replace=False))
+    rowb = len(raw) // rows
+    sub = np.frombuffer(raw, np.uint8).reshape(rows, rowb)[sel].tobytes()
+    want = quant.matmul_exact(sub, t, len(sel), cols, x)
+    assert normwise_rel(got[:, sel], want) < 1e-5
+    q.close()
+
+
 @pytest.mark.parametrize('name,t,rows,cols', [
     ('ffn_gate', 12, 14336, 4096), ('ffn_down', 14, 4096, 14336), ('attn_v', 14, 1024, 4096),
     ('attn_k', 12, 1024, 4096)])
