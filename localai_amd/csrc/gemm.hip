@@ -373,9 +373,8 @@ __device__ __forceinline__ GtRaw<T> gt_load(const uint8_t *blk, int half, int la
     const int n = lane & 15;
     if constexpr (T == LQ_Q4_K) {
         r.qs = ld16(blk + half * 1024 + 16 * lane);
-        // half 1 takes half 0's scales (the loop copies them): a second load
-        // of the same bytes made the register allocator split the loaded
-        // registers and wait for the load right after issuing it
+        // the scales once per block, with half 0 (the loop derives half 1's
+        // scale pairs from them too)
         if (half == 0) r.hd = ld16(blk + 2048 + 16 * n);
     } else if constexpr (T == LQ_Q6_K) {
         r.ql = ld16(blk + half * 1024 + 16 * lane);
@@ -479,15 +478,12 @@ __device__ __forceinline__ lq_h8 gt_b(const GtRaw<T> &r, int q, uint32_t pair_ab
 // that holds ready MFMAs keeps the matrix core of its SIMD (the waves of a
 // SIMD come from different workgroups). Dense 14336 x 4096 x 512 Q8_0: 88 us
 // against 97 us; the expert GEMMs gain about 1 %.
+// Q4_K: pr0 / pr1 are the scale pairs of this half (gt_q4k_pair), computed
+// by the caller while half 0's scale registers are live
 template <int T, int HALF, int NI>
 __device__ __forceinline__ void gt_half(const GtRaw<T> &w0, const GtRaw<T> &w1, const _Float16 *xs, int lane,
-                                        lq_f4 (&acc)[NI][2]) {
+                                        lq_f4 (&acc)[NI][2], uint32_t pr0 = 0, uint32_t pr1 = 0) {
     const int fr = lane & 15, q = lane >> 4;
-    uint32_t pr0 = 0, pr1 = 0;
-    if constexpr (T == LQ_Q4_K) {
-        pr0 = gt_q4k_pair<HALF>(w0.hd, q);
-        pr1 = gt_q4k_pair<HALF>(w1.hd, q);
-    }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
         // all A reads of the slice in flight while the B operands are decoded
@@ -567,16 +563,31 @@ __device__ __forceinline__ void gt_main(const GemmArgs &a, _Float16 (*Xs)[BN * G
     // step loop over blocks: half 0 from Xs[0] / (a0, a1), half 1 from Xs[1] / (b0, b1);
     // the next half's weights and x are requested before the current half's MFMAs
     for (int64_t sb = 0; sb < nsb; ++sb) {
-        GtRaw<T> b0 = gt_load<T>(w0p + sb * BB, 1, lane), b1 = gt_load<T>(w1p + sb * BB, 1, lane);
-        if constexpr (T == LQ_Q4_K) {
-            b0.hd = a0.hd;
-            b1.hd = a1.hd;
-        }
+        const GtRaw<T> b0 = gt_load<T>(w0p + sb * BB, 1, lane), b1 = gt_load<T>(w1p + sb * BB, 1, lane);
         load_x(1, 2 * sb + 1);
+        // Q4_K: both halves' scale pairs now, so the block's scale registers
+        // die in half 0 and the next block's scales load straight into them
+        // (kept live into half 1, the compiler copied each freshly loaded
+        // scale register and waited for the load right after issuing it)
+        uint32_t p00 = 0, p01 = 0, p10 = 0, p11 = 0;
+        if constexpr (T == LQ_Q4_K) {
+            // whole 128-bit tuples here: the loop-carried scales stay in the
+            // registers their load wrote
+            typedef unsigned u4v __attribute__((ext_vector_type(4)));
+            u4v h0 = __builtin_bit_cast(u4v, a0.hd), h1 = __builtin_bit_cast(u4v, a1.hd);
+            asm volatile("" : "+v"(h0), "+v"(h1));
+            a0.hd = __builtin_bit_cast(uint4, h0);
+            a1.hd = __builtin_bit_cast(uint4, h1);
+            const int q = lane >> 4;
+            p00 = gt_q4k_pair<0>(a0.hd, q);
+            p01 = gt_q4k_pair<0>(a1.hd, q);
+            p10 = gt_q4k_pair<1>(a0.hd, q);
+            p11 = gt_q4k_pair<1>(a1.hd, q);
+        }
         // nothing crosses: the loads stay ahead of the MFMAs, and the next
         // half's decode stays behind them (it would wait on these loads)
         __builtin_amdgcn_sched_barrier(0);
-        gt_half<T, 0, NV>(a0, a1, Xs[0], lane, acc);
+        gt_half<T, 0, NV>(a0, a1, Xs[0], lane, acc, p00, p01);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         // next block (the last block re-reads itself: Xs[0] is not read again)
@@ -585,7 +596,7 @@ __device__ __forceinline__ void gt_main(const GemmArgs &a, _Float16 (*Xs)[BN * G
         a1 = gt_load<T>(w1p + nx * BB, 0, lane);
         load_x(0, 2 * nx);
         __builtin_amdgcn_sched_barrier(0);
-        gt_half<T, 1, NV>(b0, b1, Xs[1], lane, acc);
+        gt_half<T, 1, NV>(b0, b1, Xs[1], lane, acc, p10, p11);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
