@@ -596,7 +596,8 @@ static inline size_t perm_lds_bytes(int64_t E, int64_t N, bool match, bool stage
 //      lanes per expert, two waves each);
 //   3. wave 0 scans the expert totals (lane l owns a contiguous run of
 //      experts): offsets, counts, the active list and, for the expert GEMMs,
-//      the tile list (tiles of tile_w consecutive perm positions per expert);
+//      the tile list (tiles of tile_w consecutive perm positions per expert:
+//      every expert's full tiles, then every expert's partial last tile);
 //   4. every assignment lands at offset[e] + wave base + rank -- STAGE: in
 //      LDS, copied out to perm[] in order afterwards (the scattered stores stay
 //      off the one CU's address path).
@@ -687,36 +688,50 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__rest
         const int tw = tb.tile_w;
         const int pe = (E + 63) / 64;
         const int e0 = min(E, lane * pe), e1 = min(E, e0 + pe);
-        int so = 0, sa = 0, st = 0;
+        int so = 0, sa = 0, sf = 0, sp = 0;
         for (int e = e0; e < e1; ++e) {
             const int c = off[e];
             so += c;
             sa += c > 0;
-            if (tw > 0) st += (c + tw - 1) / tw;
+            if (tw > 0) {
+                sf += c / tw;
+                sp += c % tw != 0;
+            }
         }
-        // inclusive sums over the lanes, then exclusive starts of this lane's run
+        // inclusive sums over the lanes, then exclusive starts of this lane's run;
+        // the full tiles of every expert come first, the partial last tiles after
+        // them: the expert GEMM grid starts the long tiles first and its last
+        // workgroups are the short ones
         const int io = wave_incl_sum(so, lane), ia = wave_incl_sum(sa, lane);
-        const int it = tw > 0 ? wave_incl_sum(st, lane) : 0;
-        int o = io - so, na = ia - sa, nt = it - st;
+        const int iff = tw > 0 ? wave_incl_sum(sf, lane) : 0, ip = tw > 0 ? wave_incl_sum(sp, lane) : 0;
+        const int nfull = __builtin_amdgcn_readlane(iff, 63);
+        int o = io - so, na = ia - sa, nf = iff - sf, np = nfull + ip - sp;
         for (int e = e0; e < e1; ++e) {
             const int c = off[e];
             off[e] = o;
             tb.offsets[e] = o;
             tb.counts[e] = c;
             if (c > 0) tb.active[na++] = e;
-            if (tw > 0)
-                for (int p = 0; p < c; p += tw, ++nt) {
-                    tb.tile_e[nt] = e;
-                    tb.tile_p0[nt] = o + p;
-                    tb.tile_n[nt] = min(tw, c - p);
+            if (tw > 0) {
+                for (int p = 0; p + tw <= c; p += tw, ++nf) {
+                    tb.tile_e[nf] = e;
+                    tb.tile_p0[nf] = o + p;
+                    tb.tile_n[nf] = tw;
                 }
+                if (c % tw) {
+                    tb.tile_e[np] = e;
+                    tb.tile_p0[np] = o + c - c % tw;
+                    tb.tile_n[np] = c % tw;
+                    ++np;
+                }
+            }
             o += c;
         }
         if (lane == 63) {
             off[E] = io;
             tb.offsets[E] = io;
             tb.n_active[0] = ia;
-            if (tw > 0) tb.n_tiles[0] = it;
+            if (tw > 0) tb.n_tiles[0] = iff + ip;
         }
     }
     __syncthreads();

@@ -327,7 +327,8 @@ def test_fused_wait_that_runs_out_is_reported():
 def expected_tables(idx, E, tile_w):
     """Stable counting sort of the flat assignments a = t * k + s by expert,
     its inverse, per-expert counts / offsets / active list and the expert GEMM
-    tiles (runs of tile_w perm positions per expert)."""
+    tiles (runs of tile_w perm positions per expert: the full runs of every
+    expert in expert order, then the partial last runs in expert order)."""
     flat = idx.reshape(-1).astype(np.int64)
     perm = np.argsort(flat, kind='stable').astype(np.int32)
     pos = np.empty_like(perm)
@@ -339,10 +340,14 @@ def expected_tables(idx, E, tile_w):
     if tile_w:
         te, tp, tn = [], [], []
         for e in np.flatnonzero(counts):
-            for p in range(0, counts[e], tile_w):
+            for p in range(0, counts[e] - tile_w + 1, tile_w):
                 te.append(e)
                 tp.append(offsets[e] + p)
-                tn.append(min(tile_w, counts[e] - p))
+                tn.append(tile_w)
+        for e in np.flatnonzero(counts % tile_w):
+            te.append(e)
+            tp.append(offsets[e] + counts[e] - counts[e] % tile_w)
+            tn.append(counts[e] % tile_w)
         want.update(tile_e=np.array(te, np.int32), tile_p0=np.array(tp, np.int32), tile_n=np.array(tn, np.int32))
     return want
 
