@@ -46,8 +46,11 @@ def _compile(src: Path) -> Path:
 
 # kernels whose global loads are asm with hand-counted waits (isa_check.py):
 # (source, kernel, None) for register loads, (source, kernel, n) for a ring of
-# LDS stages filled by global_load_lds, n copies per stage and wave
-COUNTED_LOADS = [('gemm.hip', 'gemm_cu_q80_kernel', None), ('moe.hip', 'moe_route_logits_kernel', 4)]
+# LDS stages filled by global_load_lds, n copies per stage and wave (n = 0: a
+# double buffer, whose every copy from before the last barrier has landed by
+# the LDS reads after it)
+COUNTED_LOADS = [('gemm.hip', 'gemm_cu_q80_kernel', None), ('moe.hip', 'moe_route_logits_kernel', 4),
+                 ('gemm.hip', 'gemm_tile_kernel', 0)]
 
 
 def _check(item) -> None:

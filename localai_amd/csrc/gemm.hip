@@ -358,6 +358,25 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 // Workgroup: 4 waves x 2 row tiles (128 weight rows; for gate_up 64 gate rows
 // and the 64 matching up rows) x BN tokens, 128 K values per step.
 
+// Workgroup barrier without the fence of __syncthreads, whose wait for every
+// outstanding LDS read would stall on the next step's operand prefetch. What
+// crosses it is ordered by hand: each wave waits (vmcnt) for its own copies
+// into the ring before arriving, and every read of a ring slot has been
+// consumed by an MFMA (lgkmcnt wait) before the barrier that precedes the
+// slot's refill. The memory clobber keeps the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void cu_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// 1 KB from global memory (16 bytes per lane) into LDS at the wave-uniform
+// byte address lds (lane i's bytes at lds + 16 i), through M0, which it saves
+// and restores
+__device__ __forceinline__ void cu_dma(const void *src, uint32_t lds) {
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep)
+                 : "v"(src), "s"(lds)
+                 : "memory");
+}
 constexpr int GT_WROWS = 128;          // weight rows per workgroup (dense, 4 waves)
 constexpr int GM_MOE_NW = 8;           // waves per workgroup of the expert tile GEMMs
 
@@ -513,6 +532,38 @@ __device__ __forceinline__ void gt_half(const GtRaw<T> &w0, const GtRaw<T> &w1, 
     }
 }
 
+// Waits for the loads of gt_load<T>(.., HALF, ..) into r (the compiler places
+// the wait before these empty asm statements, which read and rewrite the
+// loaded registers)
+__device__ __forceinline__ void gt_touch(uint4 &v) {
+    typedef unsigned u4v __attribute__((ext_vector_type(4)));
+    u4v t = __builtin_bit_cast(u4v, v);
+    asm volatile("" : "+v"(t));
+    v = __builtin_bit_cast(uint4, t);
+}
+template <int T, int HALF>
+__device__ __forceinline__ void gt_ready(GtRaw<T> &r) {
+    if constexpr (T == LQ_Q4_K) {
+        gt_touch(r.qs);
+        if constexpr (HALF == 0) gt_touch(r.hd);
+    } else if constexpr (T == LQ_Q6_K) {
+        gt_touch(r.ql);
+        gt_touch(r.qh);
+        gt_touch(r.sc);
+        asm volatile("" : "+v"(r.d));
+    } else {
+        gt_touch(r.p0);
+        gt_touch(r.p1);
+        gt_touch(r.dd);
+    }
+}
+
+// Global loads gt_load<T> issues for one row tile's half HALF
+template <int T, int HALF>
+constexpr int gt_loads() {
+    return T == LQ_Q4_K ? (HALF == 0 ? 2 : 1) : T == LQ_Q6_K ? 4 : 3;
+}
+
 // The K loop and epilogue of one workgroup with NV 16-token MFMA tiles of
 // the BN holding tokens: expert tiles end partway, and each NV is its own
 // copy of the loop (no per-MFMA branches, which made the compiler copy the
@@ -537,13 +588,17 @@ __device__ __forceinline__ void gt_main(const GemmArgs &a, _Float16 (*Xs)[BN * G
         const int row = (NW * i + wave) * 4 + (lane >> 4), c = (lane & 15) ^ (row & 15);
         xsrc[i] = a.Xh + gemm_xrow(a, p0 + (row < tn ? row : 0)) * a.ldh + 8 * c;
     }
+    // The copies are asm (cu_dma): the compiler, which sees a builtin copy as
+    // an LDS write it cannot place, waited for every load (vmcnt(0)) before
+    // the first LDS read after one, the weight loads just issued included.
+    // Their completion before the LDS reads is the kernel's own wait before
+    // each barrier.
+    const uint32_t xs0 = (uint32_t)(uintptr_t)&Xs[0][0];
     auto load_x = [&](int buf, int64_t step) {
 #pragma unroll
         for (int i = 0; i < XN; ++i)
             if ((NW * i + wave) * 4 < 16 * NV)   // uniform per wave
-                __builtin_amdgcn_global_load_lds(
-                    (const void *)(xsrc[i] + step * GM_BK),
-                    (__attribute__((address_space(3))) void *)&Xs[buf][(NW * i + wave) * 64 * 8], 16, 0, 0);
+                cu_dma(xsrc[i] + step * GM_BK, xs0 + (uint32_t)(buf * BN * GM_BK * 2 + (NW * i + wave) * 64 * 16));
     };
 
     lq_f4 acc[NV][2];
@@ -560,44 +615,43 @@ __device__ __forceinline__ void gt_main(const GemmArgs &a, _Float16 (*Xs)[BN * G
     if (tid < BN) tsc[tid] = a.inv[gemm_xrow(a, p0 + (tid < tn ? tid : 0))];
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    // step loop over blocks: half 0 from Xs[0] / (a0, a1), half 1 from Xs[1] / (b0, b1);
-    // the next half's weights and x are requested before the current half's MFMAs
+    // step loop over blocks: half 0 from Xs[0] / (a0, a1), half 1 from Xs[1] /
+    // (b0, b1). Each half waits for its own weights (requested one half
+    // earlier), then requests the next half's x copy and, after it, the next
+    // half's weights, so the wait before the barrier (vmcnt = those weight
+    // loads) retires only the copy: the weights stay in flight across it.
     for (int64_t sb = 0; sb < nsb; ++sb) {
-        const GtRaw<T> b0 = gt_load<T>(w0p + sb * BB, 1, lane), b1 = gt_load<T>(w1p + sb * BB, 1, lane);
-        load_x(1, 2 * sb + 1);
+        gt_ready<T, 0>(a0);
+        gt_ready<T, 0>(a1);
         // Q4_K: both halves' scale pairs now, so the block's scale registers
         // die in half 0 and the next block's scales load straight into them
         // (kept live into half 1, the compiler copied each freshly loaded
         // scale register and waited for the load right after issuing it)
         uint32_t p00 = 0, p01 = 0, p10 = 0, p11 = 0;
         if constexpr (T == LQ_Q4_K) {
-            // whole 128-bit tuples here: the loop-carried scales stay in the
-            // registers their load wrote
-            typedef unsigned u4v __attribute__((ext_vector_type(4)));
-            u4v h0 = __builtin_bit_cast(u4v, a0.hd), h1 = __builtin_bit_cast(u4v, a1.hd);
-            asm volatile("" : "+v"(h0), "+v"(h1));
-            a0.hd = __builtin_bit_cast(uint4, h0);
-            a1.hd = __builtin_bit_cast(uint4, h1);
             const int q = lane >> 4;
             p00 = gt_q4k_pair<0>(a0.hd, q);
             p01 = gt_q4k_pair<0>(a1.hd, q);
             p10 = gt_q4k_pair<1>(a0.hd, q);
             p11 = gt_q4k_pair<1>(a1.hd, q);
         }
-        // nothing crosses: the loads stay ahead of the MFMAs, and the next
-        // half's decode stays behind them (it would wait on these loads)
+        load_x(1, 2 * sb + 1);
+        GtRaw<T> b0 = gt_load<T>(w0p + sb * BB, 1, lane), b1 = gt_load<T>(w1p + sb * BB, 1, lane);
+        // nothing crosses: the loads stay ahead of the MFMAs
         __builtin_amdgcn_sched_barrier(0);
         gt_half<T, 0, NV>(a0, a1, Xs[0], lane, acc, p00, p01);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * gt_loads<T, 1>()) : "memory");
         __syncthreads();
+        gt_ready<T, 1>(b0);
+        gt_ready<T, 1>(b1);
         // next block (the last block re-reads itself: Xs[0] is not read again)
         const int64_t nx = sb + 1 < nsb ? sb + 1 : sb;
+        load_x(0, 2 * nx);
         a0 = gt_load<T>(w0p + nx * BB, 0, lane);
         a1 = gt_load<T>(w1p + nx * BB, 0, lane);
-        load_x(0, 2 * nx);
         __builtin_amdgcn_sched_barrier(0);
         gt_half<T, 1, NV>(b0, b1, Xs[1], lane, acc, p10, p11);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * gt_loads<T, 0>()) : "memory");
         __syncthreads();
     }
     // D[m][n]: lane holds tokens 4 (lane / 16) + v of token tile i, row lane % 16 of row tile j.
@@ -749,25 +803,6 @@ __device__ __forceinline__ void cu_load(mt_i4 &v, const void *base, uint32_t off
 }
 __device__ __forceinline__ void cu_load(int &v, const void *base, uint32_t off) {
     asm volatile("global_load_dword %0, %1, %2" : "=v"(v) : "v"(off), "s"(base) : "memory");
-}
-// Workgroup barrier without the fence of __syncthreads, whose wait for every
-// outstanding LDS read would stall on the next step's operand prefetch. What
-// crosses it is ordered by hand: each wave waits (vmcnt) for its own copies
-// into the ring before arriving, and every read of a ring slot has been
-// consumed by an MFMA (lgkmcnt wait) before the barrier that precedes the
-// slot's refill. The memory clobber keeps the compiler from moving memory
-// accesses across it.
-__device__ __forceinline__ void cu_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-// 1 KB from global memory (16 bytes per lane) into LDS at the wave-uniform
-// byte address lds (lane i's bytes at lds + 16 i), through M0, which it saves
-// and restores
-__device__ __forceinline__ void cu_dma(const void *src, uint32_t lds) {
-    uint32_t keep;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(keep)
-                 : "v"(src), "s"(lds)
-                 : "memory");
 }
 template <int N, class W>
 __device__ __forceinline__ void cu_wait_w(W &w) {
