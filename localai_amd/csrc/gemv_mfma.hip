@@ -408,6 +408,77 @@ static MtPlan mt_plan(int nb, int64_t tiles, bool q6) {
         }                                                      \
     }
 
+// One vector, many row tiles (the vocabulary head): one workgroup per CU
+// (a wave per super-block, rows of up to 16 super-blocks) loops over groups
+// of RT tiles, blk, blk + grid, ... . x is staged into LDS and its A operands
+// loaded into registers once per workgroup rather than once per tile, and
+// the next group's weights are requested before the current group's dot
+// products, so each CU streams weights without the gaps between the
+// one-tile workgroups of the plain kernel, whose waves each staged x for
+// four MFMAs. Dot products and the cross-wave sum are mt_pass's (results
+// bit-identical to gemv_mfma's); the wave partials go through two
+// alternating LDS buffers, one barrier per group.
+template <int TYPE, int RT>
+__global__ __launch_bounds__(1024) void gemv_mfma_loop(const uint8_t *__restrict__ Wt, int64_t rows, int nb,
+                                                       int64_t tiles, const float *__restrict__ x,
+                                                       float *__restrict__ y) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int XB = mt_xbytes(TYPE);
+    const int lane = lane_id(), wv = wave_id(), nw = blockDim.x >> 6;   // nw == nb
+    const int64_t tile_bytes = (int64_t)nb * mt_block_bytes(TYPE), step = (int64_t)gridDim.x * RT;
+    uint8_t *wl = smem + wv * XB;
+    float *red = reinterpret_cast<float *>(smem + nw * XB);   // [2][nw][RT][64]
+    const uint8_t *wsb = Wt + (int64_t)wv * mt_block_bytes(TYPE);   // the wave's super-block of tile 0
+    auto load = [&](MtW<TYPE>(&w)[RT], int64_t t0) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const int64_t tl = t0 + t < tiles ? t0 + t : tiles - 1;
+            w[t] = mt_load_w<TYPE>(wsb + tl * tile_bytes, lane);
+        }
+    };
+    const float4 xv = *reinterpret_cast<const float4 *>(x + 256 * wv + 4 * lane);
+    MtW<TYPE> wa[RT], wb[RT];
+    int64_t t0 = (int64_t)blockIdx.x * RT;
+    load(wa, t0);
+    __builtin_amdgcn_sched_barrier(0);
+    mt_stage<TYPE>(xv, wl, lane);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const MtLane<TYPE> L = mt_lane<TYPE>(lane);
+    const MtA<TYPE> a = mt_load_a<TYPE>(wl, L);
+    auto group = [&](const MtW<TYPE>(&w)[RT], MtW<TYPE>(&next)[RT], int64_t t0, int buf) {
+        if (t0 + step < tiles) load(next, t0 + step);   // uniform
+        __builtin_amdgcn_sched_barrier(0);
+        float *r = red + buf * nw * RT * 64;
+#pragma unroll
+        for (int t = 0; t < RT; ++t) r[(wv * RT + t) * 64 + lane] = mt_dot<TYPE>(w[t], a, L, 0.0f);
+        __syncthreads();
+        const int i = threadIdx.x;
+        if (i < RT * 16) {
+            const int t = i >> 4, n = i & 15;
+            float v = 0.0f;
+            for (int kk = 0; kk < nw; ++kk) {
+                const float *q = r + (kk * RT + t) * 64 + n;
+                v += (q[0] + q[16]) + (q[32] + q[48]);
+            }
+            const int64_t row = (t0 + t) * MT_ROWS + n;
+            if (t0 + t < tiles && row < rows) y[row] = v;
+        }
+    };
+    // two copies of the group body, one per register set (the sets alternate)
+    while (t0 < tiles) {
+        group(wa, wb, t0, 0);
+        t0 += step;
+        if (t0 >= tiles) break;
+        group(wb, wa, t0, 1);
+        t0 += step;
+    }
+}
+
+// Row tiles from which a one-vector matvec of up to 16 super-blocks per row
+// runs gemv_mfma_loop (a few groups per CU and more)
+constexpr int64_t MT_LOOP_TILES = 2048;
+constexpr int MT_LOOP_RT = 2;
+
 int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, float *y, hipStream_t s) {
     if (!mt_matvec_ok(g)) return fail(LOCALAI_ETYPE, "mfma matvec: Q4_K / Q6_K, or Q8_0 with cols % 256 == 0");
     if (reinterpret_cast<uintptr_t>(x) & 15) return fail(LOCALAI_EARG, "mfma matvec: x must be 16-byte aligned");
@@ -415,6 +486,21 @@ int launch_matvec_mfma(const lq_geom &g, const uint8_t *Wt, const float *x, floa
     if (nb > 72) return fail(LOCALAI_EARG, "mfma matvec: K too large (more than 18432 values)");
     const bool q6 = g.type == LQ_Q6_K, q8 = g.type == LQ_Q8_0;
     const int64_t tiles = (g.rows + MT_ROWS - 1) / MT_ROWS;
+    if (nb <= 16 && tiles >= MT_LOOP_TILES) {
+        int dev = 0, cus = 0;
+        LQ_HIP(hipGetDevice(&dev));
+        LQ_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        // as many workgroups as CUs, or fewer so that each runs the same count of groups
+        const int64_t groups = (tiles + MT_LOOP_RT - 1) / MT_LOOP_RT;
+        const int64_t per = (groups + cus - 1) / cus;
+        const dim3 lgrid((unsigned)((groups + per - 1) / per)), lblock(64 * nb);
+        const size_t llds = (size_t)nb * mt_xbytes(g.type) + (size_t)2 * nb * MT_LOOP_RT * 64 * 4;
+        if (q6) hipLaunchKernelGGL((gemv_mfma_loop<LQ_Q6_K, MT_LOOP_RT>), lgrid, lblock, llds, s, Wt, g.rows, nb, tiles, x, y);
+        else if (q8) hipLaunchKernelGGL((gemv_mfma_loop<LQ_Q8_0, MT_LOOP_RT>), lgrid, lblock, llds, s, Wt, g.rows, nb, tiles, x, y);
+        else hipLaunchKernelGGL((gemv_mfma_loop<LQ_Q4_K, MT_LOOP_RT>), lgrid, lblock, llds, s, Wt, g.rows, nb, tiles, x, y);
+        LQ_HIP(hipGetLastError());
+        return LOCALAI_OK;
+    }
     const MtPlan p = mt_plan(nb, tiles, q6 || q8);   // one tile per workgroup for the larger blocks
     dim3 grid((unsigned)((tiles + p.rt - 1) / p.rt)), block(64 * p.waves);
     const size_t lds = mt_lds_bytes(g.type, p.waves, p.spw, 1, p.rt);

@@ -165,6 +165,37 @@ def test_vocab_head_128256x4096(t):
     assert err < 1e-5
 
 
+@pytest.mark.parametrize('t', (12, 14, 8))
+def test_many_tile_loop_kernel(t):
+    """From 2048 row tiles a one-vector matvec runs the tile-looping kernel:
+    2049 tiles (an odd count, the last one 5 rows deep) at K = 2048 (eight
+    waves). Sampled rows and the last tile against the oracle, and the first
+    and last 64 rows bit for bit equal to the one-tile-per-workgroup kernel
+    run on those rows alone (same products, same summation order; the last
+    64 start mid-tile in the big matrix)."""
+    from localai_amd import device, synth
+    rows, cols = 2048 * 16 + 5, 2048
+    rng = np.random.default_rng(40 + t)
+    raw = synth.quant_tensor(rng, t, rows, cols)
+    x = synth.activations(rng, cols)
+    xd = device.to_device_f32(x)
+    q = device.QMat.from_ggml(raw, t, rows, cols)
+    y = q.matvec(xd).cpu().numpy()
+    q.close()
+    assert np.isfinite(y).all()
+    rowb = len(raw) // rows
+    buf = np.frombuffer(raw, np.uint8).reshape(rows, rowb)
+    sel = np.unique(np.concatenate([np.arange(rows - 21, rows), rng.choice(rows, 1500, replace=False)]))
+    want = quant.matvec_exact(buf[sel].tobytes(), t, len(sel), cols, x)
+    assert normwise_rel(y[sel], want) < 1e-5
+    for lo, hi in ((0, 64), (rows - 64, rows)):
+        small = device.QMat.from_ggml(buf[lo:hi].tobytes(), t, hi - lo, cols)
+        ys = small.matvec(xd).cpu().numpy()
+        small.close()
+        # a row's arithmetic does not depend on which rows share its tile
+        np.testing.assert_array_equal(y[lo:hi].view(np.uint32), ys.view(np.uint32))
+
+
 def test_expert_slices_of_a_3d_tensor():
     """[E, rows, cols] tensor; expert e is the byte slice of engine/zaya.py:144-150."""
     from localai_amd import device
