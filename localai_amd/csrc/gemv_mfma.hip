@@ -446,7 +446,10 @@ __global__ __launch_bounds__(1024) void gemv_mfma_loop(const uint8_t *__restrict
     const MtLane<TYPE> L = mt_lane<TYPE>(lane);
     const MtA<TYPE> a = mt_load_a<TYPE>(wl, L);
     auto group = [&](const MtW<TYPE>(&w)[RT], MtW<TYPE>(&next)[RT], int64_t t0, int buf) {
-        if (t0 + step < tiles) load(next, t0 + step);   // uniform
+        // unconditional (past the end: the last tile again, from L2): a
+        // conditional request made the compiler's waits for the current set
+        // count as if it had not been issued, and wait for it too
+        load(next, t0 + step);
         __builtin_amdgcn_sched_barrier(0);
         float *r = red + buf * nw * RT * 64;
 #pragma unroll
