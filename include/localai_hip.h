@@ -118,9 +118,12 @@ int localai_hip_qmat_dequant(const localai_qmat *m, int64_t expert, float *out_d
  * 256-value super-blocks: int8 MFMA over the raw quants, x split exactly
  * into three int8 pieces per scale group (21 bits of each value against the
  * group maximum), the integer dot products exact, recombined and scaled in
- * fp32 (normwise error about 1e-6). Other types and several vectors: fp32
- * products of exactly decoded weights, fp32 accumulation (the vectors two
- * per launch while cols <= 8192, one otherwise). */
+ * fp32 (normwise error about 1e-6); from 2048 row tiles one workgroup per CU
+ * loops over the tiles (same arithmetic, same bits). 2..31 vectors of such
+ * a handle: the same arithmetic per vector over the tile form, the weights
+ * read once per call (each y[t] equal to the one-vector call on x[t]). Other
+ * types: fp32 products of exactly decoded weights, fp32 accumulation (the
+ * vectors two per launch while cols <= 8192, one otherwise). */
 int localai_hip_matvec(const localai_qmat *m, int64_t expert, const float *x_dev,
                        float *y_dev, int ntok, void *stream);
 

@@ -1,7 +1,9 @@
-"""The reference-side binding of INTEGRATION.md, run as written.
+"""The reference-side binding in the maintainers' integration notes at the
+repository root, run as written.
 
 The two residency blocks (register the GGUF map in GGUFFile.__init__,
-unregister it in close()) are read out of INTEGRATION.md and executed against
+unregister it in close()) are read out of those notes (the fenced python
+blocks marked `<!-- snippet: NAME -->`) and executed against
 an object that opens a GGUF file exactly as engine/gguf_parser.py:50-53 does
 (`open('rb')`, `mmap.mmap(fileno, 0, access=mmap.ACCESS_READ)`). The CPU test
 checks that registration works on that read-only map and that the map can
@@ -27,7 +29,7 @@ ROOT = Path(__file__).resolve().parents[1]
 def snippet(name):
     text = (ROOT / 'INTEGRATION.md').read_text()
     m = re.search(r'<!-- snippet: ' + re.escape(name) + r' -->\s*```python\n(.*?)```', text, re.S)
-    assert m, f'snippet {name} not found in INTEGRATION.md'
+    assert m, f'snippet {name} not found in the integration notes'
     lines = m.group(1).splitlines()
     indent = min(len(s) - len(s.lstrip()) for s in lines if s.strip())
     return '\n'.join(s[indent:] for s in lines)
