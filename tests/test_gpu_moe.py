@@ -354,6 +354,9 @@ def expected_tables(idx, E, tile_w):
 
 @pytest.mark.parametrize('E,T,k', [
     (16, 1, 2),        # one token: the router writes the tables
+    (16, 8, 2),        # few assignments over few experts (one wave's worth)
+    (64, 16, 4),       # 64 assignments over 64 experts
+    (2, 5, 1),         # two experts, one expert per token
     (1, 40, 1),        # one expert: every assignment matches
     (16, 31, 4),       # matvec path (no tiles), sixteen waves of eight assignments or fewer
     (128, 512, 8),     # lane masks in LDS, ranks in registers, perm staged in LDS
