@@ -714,9 +714,10 @@ def expert_gemm_roofline(args, torch, device, E, H, I, k, T, distinct):
     """The prefill layer's dominant kernel, the gate_up expert GEMM (with
     SiLU*up), run alone (localai_hip_moe_expert_gemm) on the routing tables
     each rotated layer copy's last forward left in its workspace. Its bytes:
-    the gate_up weights of the touched experts, the f16 rows of h and the
-    fp32 act rows it writes; its flops 2 * T * k * H * 2I. The binding roof is
-    HBM (about 175 flop per byte against a ridge of about 315)."""
+    the gate_up weights of the touched experts, the f16 rows of h and the f16
+    SiLU*up rows it writes for the down GEMM; its flops 2 * T * k * H * 2I.
+    The binding roof is HBM (about 180 flop per byte against a ridge of about
+    315)."""
     import ctypes
     from localai_amd import _lib
     layers, hd, stream = _moe_gpu.last
@@ -729,7 +730,7 @@ def expert_gemm_roofline(args, torch, device, E, H, I, k, T, distinct):
                                                    ws.numel(), 0, sp))
     kms = time_steps(torch, [lambda L=L: run(L) for L in layers], stream, args.steps, args.warmup)
     gu_bytes = 2 * I * (H // 256) * 144
-    nbytes = distinct * gu_bytes + T * H * 2 + T * k * I * 4
+    nbytes = distinct * gu_bytes + T * H * 2 + T * k * I * 2
     flops = 2 * T * k * H * 2 * I
     gbs = nbytes / (kms * 1e-3) / 1e9
     tfs = flops / (kms * 1e-3) / 1e12

@@ -96,7 +96,10 @@ int localai_hip_ggml_matvec(int ggml_type, const void *w_dev, int64_t rows, int6
  * the Q8_0 matvec of rows that are not whole 256-value super-blocks and the
  * fallback MoE paths read is built from it on the first such call (which
  * allocates and waits for the stream, so not under graph capture:
- * LOCALAI_ESTATE there) and then kept. Other types hold the row planes. */
+ * LOCALAI_ESTATE there) and then kept. Other types hold the row planes.
+ * With the tile form a handle also keeps, per matrix, the largest row L2
+ * norm of its first and of its second half of rows (8 bytes per matrix;
+ * the prefill MoE gate_up GEMM scales its f16 outputs from them). */
 int localai_hip_qmat_create(int ggml_type, int64_t rows, int64_t cols, int64_t batch,
                             const void *ggml_bytes, int src_is_device, void *stream,
                             localai_qmat **out);

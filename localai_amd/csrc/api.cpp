@@ -218,6 +218,7 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
     m->data = nullptr;
     m->tiles = nullptr;
     m->tile_bytes = 0;
+    m->row_norm = nullptr;
     hipGetDevice(&m->device);
     // Q4_K / Q6_K / Q8_0 keep only the tile form, which their one-vector
     // matvec, GEMM and MoE kernels read; the row planes are built on first
@@ -251,6 +252,15 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
         } else {
             st = launch_mt_repack(g, dsrc, m->tiles, m->tile_bytes, s);
         }
+        if (st == LOCALAI_OK) {
+            e = hipMalloc(&m->row_norm, (size_t)(2 * batch) * sizeof(float));
+            if (e != hipSuccess) {
+                m->row_norm = nullptr;
+                st = hip_fail(e, "hipMalloc(qmat row norms)");
+            } else {
+                st = launch_row_norms(g, dsrc, m->row_norm, s);
+            }
+        }
     }
     if (staging) {
         hipError_t e2 = hipStreamSynchronize(s);
@@ -260,6 +270,7 @@ int localai_hip_qmat_create(int t, int64_t rows, int64_t cols, int64_t batch, co
     if (st != LOCALAI_OK) {
         hipFree(m->data);
         if (m->tiles) hipFree(m->tiles);
+        if (m->row_norm) hipFree(m->row_norm);
         delete m;
         return st;
     }
@@ -272,6 +283,7 @@ int localai_hip_qmat_destroy(localai_qmat *m) {
     if (!m) return LOCALAI_OK;
     if (m->data) hipFree(m->data);
     if (m->tiles) hipFree(m->tiles);
+    if (m->row_norm) hipFree(m->row_norm);
     delete m;
     return LOCALAI_OK;
 }

@@ -73,4 +73,56 @@ int launch_dequant_ggml(int t, const void *raw, int64_t n, float *out, hipStream
     return LOCALAI_OK;
 }
 
+// Largest row L2 norm of each row half of every matrix: one wave per row
+// sums the squares of its exact decoded values in fp64; lane 0 rounds the
+// norm up to a float and raises the matrix's half (out[2 b + (row >=
+// rows / 2)]) to it with an unsigned atomic max (non-negative floats order
+// like their bits; NaN, bits above inf, wins). The MoE gate_up GEMM bounds
+// its SiLU * up outputs with these.
+template <int T>
+__global__ __launch_bounds__(256) void row_norm_kernel(const uint8_t *__restrict__ raw, int64_t rows, int64_t cols,
+                                                       int64_t nrows, float *__restrict__ out) {
+    constexpr int BV = T == LQ_Q4_K || T == LQ_Q5_K || T == LQ_Q6_K ? 256 : 32;
+    constexpr int BPB = T == LQ_Q4_0 ? 18 : T == LQ_Q4_1 ? 20 : T == LQ_Q5_0 ? 22 : T == LQ_Q5_1 ? 24
+                      : T == LQ_Q8_0 ? 34 : T == LQ_Q4_K ? 144 : T == LQ_Q5_K ? 176 : 210;
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= nrows) return;
+    const int lane = threadIdx.x & 63;
+    const uint8_t *row = raw + r * (cols / BV) * BPB;
+    double ss = 0.0;
+    for (int64_t e = 8 * lane; e < cols; e += 512) {
+        float v[8];
+        decode8<T>(row + (e / BV) * BPB, (int)(e % BV), v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += (double)v[i] * (double)v[i];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) {
+        const float f = (float)sqrt(ss);   // >= 0 or NaN
+        // the next float up (one more in the bits of a non-negative float)
+        const unsigned up = __builtin_bit_cast(unsigned, f) + (f < __builtin_inff() ? 1u : 0u);
+        const int64_t rr = r % rows;
+        atomicMax(reinterpret_cast<unsigned *>(out) + 2 * (r / rows) + (rr >= rows / 2 ? 1 : 0),
+                  up);
+    }
+}
+
+int launch_row_norms(const lq_geom &g, const uint8_t *ggml, float *out, hipStream_t s) {
+    LQ_HIP(hipMemsetAsync(out, 0, (size_t)(2 * g.batch) * sizeof(float), s));
+    const int64_t nrows = g.rows * g.batch;
+    const dim3 grid((unsigned)((nrows + 3) / 4));
+    switch (g.type) {
+#define LQ_RN(T)                                                                                                 \
+    case T:                                                                                                      \
+        hipLaunchKernelGGL(row_norm_kernel<T>, grid, dim3(256), 0, s, ggml, g.rows, g.cols, nrows, out);         \
+        break;
+        LQ_RN(LQ_Q4_0) LQ_RN(LQ_Q8_0) LQ_RN(LQ_Q4_K) LQ_RN(LQ_Q5_K) LQ_RN(LQ_Q6_K)
+#undef LQ_RN
+        default: return fail(LOCALAI_ETYPE, "row norms: unsupported type");
+    }
+    LQ_HIP(hipGetLastError());
+    return LOCALAI_OK;
+}
+
 }  // namespace lq

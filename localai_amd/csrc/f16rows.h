@@ -17,11 +17,13 @@ namespace lq {
 // 32 q + 8 c .. + 7 (c < 4) go to 16-byte slot ((t / 16) * (ldh / 32) + q) * 64
 // + (t % 16) + 16 c, so that one 32-value slice of 16 tokens is 1 KB
 // contiguous in lane order; tokens ntok .. ntok_pad - 1 are written as zeros.
+// nrm2 (not null): nrm2[t] = the row's sum of squares (fp32; NaN or inf
+// where the row holds one).
 template <int NG>
 __device__ __forceinline__ void x_to_f16_row(int64_t t, const float *__restrict__ X, int64_t ldx, int cols,
                                              const int32_t *__restrict__ rows_map, int k, int64_t ntok,
                                              _Float16 *__restrict__ Xh, int ldh, float *__restrict__ inv, int vec,
-                                             int tiled, int64_t ntok_pad) {
+                                             int tiled, int64_t ntok_pad, float *__restrict__ nrm2 = nullptr) {
     const int lane = lane_id();
     if (t >= ntok_pad) return;
     if (t >= ntok) {
@@ -57,9 +59,11 @@ __device__ __forceinline__ void x_to_f16_row(int64_t t, const float *__restrict_
         }
         return m;
     };
+    auto sq = [](const lq_f4 &v) { return v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]; };
     constexpr int NR = NG > 0 ? NG : 1;
     lq_f4 lo[NR], hi[NR];
     uint32_t mb = 0;
+    float ss = 0.0f;
     if (NG > 0) {
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
@@ -69,12 +73,21 @@ __device__ __forceinline__ void x_to_f16_row(int64_t t, const float *__restrict_
         }
 #pragma unroll
         for (int i = 0; i < NR; ++i) mb = max(mb, max(mag(lo[i]), mag(hi[i])));
+        if (nrm2)
+#pragma unroll
+            for (int i = 0; i < NR; ++i) ss += sq(lo[i]) + sq(hi[i]);
     } else {
         for (int gi = lane; gi < ngx; gi += 64) {
             lq_f4 l, h;
             load(gi, l, h);
             mb = max(mb, max(mag(l), mag(h)));
+            if (nrm2) ss += sq(l) + sq(h);
         }
+    }
+    if (nrm2) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (lane == 0) nrm2[t] = ss;
     }
     const float m = __builtin_bit_cast(float, wave_max_u32(mb));
     int s = 0;

@@ -50,9 +50,10 @@ template <int NG>
 __global__ __launch_bounds__(256) void x_to_f16_kernel(const float *__restrict__ X, int64_t ldx, int cols,
                                                        const int32_t *__restrict__ rows_map, int k, int64_t ntok,
                                                        _Float16 *__restrict__ Xh, int ldh,
-                                                       float *__restrict__ inv, int vec, int tiled, int64_t ntok_pad) {
+                                                       float *__restrict__ inv, int vec, int tiled, int64_t ntok_pad,
+                                                       float *__restrict__ nrm2) {
     const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave_id();
-    x_to_f16_row<NG>(t, X, ldx, cols, rows_map, k, ntok, Xh, ldh, inv, vec, tiled, ntok_pad);
+    x_to_f16_row<NG>(t, X, ldx, cols, rows_map, k, ntok, Xh, ldh, inv, vec, tiled, ntok_pad, nrm2);
 }
 
 // ---------------------------------------------------------------- weights
@@ -174,6 +175,14 @@ struct GemmArgs {
     int64_t wt_bytes;          // tile-form bytes per matrix
     const int32_t *rows_map;   // null, or: token p reads Xh / inv row rows_map[p] / rows_k
     int rows_k;
+    // MoE gate_up on the tile form, f16 output (Yh not null): SiLU * up of
+    // token p goes to Yh row p (stride ldy) times 2^s, inv_out[p] = 2^-s, s
+    // from the bound 4 |gate rows| |up rows| |h row|^2 (wnorm: the expert
+    // handle's row_norm, xnorm2: sum of squares per Xh row)
+    _Float16 *Yh;
+    int64_t ldy;
+    float *inv_out;
+    const float *wnorm, *xnorm2;
 };
 
 // Xh / inv row of token position p
@@ -569,9 +578,9 @@ constexpr int gt_loads() {
 // copy of the loop (no per-MFMA branches, which made the compiler copy the
 // accumulators around every conditional MFMA).
 template <int T, int BN, int MODE, int NW, int NV>
-__device__ __forceinline__ void gt_main(const GemmArgs &a, _Float16 (*Xs)[BN * GM_BK], float *tsc,
-                                        const uint8_t *w0p, const uint8_t *w1p, int64_t p0, int tn, int64_t t0,
-                                        int64_t t1, int64_t tiles, int64_t nsb) {
+__device__ __forceinline__ void gt_main(const GemmArgs &a, _Float16 (*Xs)[BN * GM_BK], float *tsc, float *asc,
+                                        const float *wn, const uint8_t *w0p, const uint8_t *w1p, int64_t p0, int tn,
+                                        int64_t t0, int64_t t1, int64_t tiles, int64_t nsb) {
     constexpr int XN = BN * 16 / (64 * NW);   // 16-byte x chunks per thread and step
     constexpr int BB = mt_block_bytes(T);
     const lq_geom &g = a.g;
@@ -612,7 +621,29 @@ __device__ __forceinline__ void gt_main(const GemmArgs &a, _Float16 (*Xs)[BN * G
     // lookup per token rather than one per output value)
     GtRaw<T> a0 = gt_load<T>(w0p, 0, lane), a1 = gt_load<T>(w1p, 0, lane);
     load_x(0, 0);
-    if (tid < BN) tsc[tid] = a.inv[gemm_xrow(a, p0 + (tid < tn ? tid : 0))];
+    if (tid < BN) {
+        const int64_t xr = gemm_xrow(a, p0 + (tid < tn ? tid : 0));
+        tsc[tid] = a.inv[xr];
+        if constexpr (MODE == GM_MOE_GATE_UP) {
+            if (a.Yh) {
+                // |silu(g) u| <= |g| |u| <= |gate row| |up row| |h|^2 (Cauchy-
+                // Schwarz), times 4 for the rounding of the f16 operands, the
+                // sums and the fast SiLU; 2^s brings the bound into [2^14,
+                // 2^15), so no output overflows f16 (s = 0 for a zero or
+                // non-finite bound, x_to_f16_row's rule)
+                const double b = 4.0 * (double)wn[0] * (double)wn[1] * (double)a.xnorm2[xr];
+                int s = 0;
+                if (b > 0.0 && b <= 1.0e300) {
+                    int e;
+                    frexp(b, &e);
+                    s = 15 - e;
+                    s = s > 120 ? 120 : s < -120 ? -120 : s;
+                }
+                asc[tid] = ldexpf(1.0f, s);
+                if (blockIdx.x == 0 && tid < tn) a.inv_out[p0 + tid] = ldexpf(1.0f, -s);
+            }
+        }
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     // step loop over blocks: half 0 from Xs[0] / (a0, a1), half 1 from Xs[1] /
@@ -660,16 +691,33 @@ __device__ __forceinline__ void gt_main(const GemmArgs &a, _Float16 (*Xs)[BN * G
     const int fr = lane & 15;
     if constexpr (MODE == GM_MOE_GATE_UP) {
         const int64_t r = t0 * MT_ROWS + fr;
-        float *yb = a.Y + p0 * a.y_ts + r;
         const bool rok = r < a.inter;
+        if (a.Yh) {
+            // the f16 rows the down GEMM reads: the same f32 value times
+            // 2^s, rounded once (as x_to_f16_row rounds it)
+            _Float16 *hb = a.Yh + p0 * a.ldy + r;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
+            for (int i = 0; i < NV; ++i) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int lt = 16 * i + 4 * (lane >> 4) + v;
-                if (lt >= tn || !rok) continue;
-                const float sc = tsc[lt];
-                yb[(uint32_t)lt * (uint32_t)a.y_ts] = silu_fast(acc[i][0][v] * sc) * (acc[i][1][v] * sc);
+                for (int v = 0; v < 4; ++v) {
+                    const int lt = 16 * i + 4 * (lane >> 4) + v;
+                    if (lt >= tn || !rok) continue;
+                    const float sc = tsc[lt];
+                    const float y = silu_fast(acc[i][0][v] * sc) * (acc[i][1][v] * sc);
+                    hb[(uint32_t)lt * (uint32_t)a.ldy] = (_Float16)(y * asc[lt]);
+                }
+            }
+        } else {
+            float *yb = a.Y + p0 * a.y_ts + r;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int lt = 16 * i + 4 * (lane >> 4) + v;
+                    if (lt >= tn || !rok) continue;
+                    const float sc = tsc[lt];
+                    yb[(uint32_t)lt * (uint32_t)a.y_ts] = silu_fast(acc[i][0][v] * sc) * (acc[i][1][v] * sc);
+                }
             }
         }
     } else {
@@ -700,6 +748,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_tile_kernel(GemmArgs a) 
     constexpr int BB = mt_block_bytes(T);
     __shared__ __attribute__((aligned(16))) _Float16 Xs[2][BN * GM_BK];
     __shared__ float tsc[BN];              // the output scale of each token of the tile
+    __shared__ float asc[MODE == GM_MOE_GATE_UP ? BN : 1];   // gate_up with f16 output: its scale per token
     const lq_geom &g = a.g;
     // wave index made wave-uniform: row-tile addresses go to scalar registers
     // (MoE Q4_K GEMMs 162 -> 128 VGPRs; gate_up 85 -> 81 us, down 55 -> 48 us)
@@ -708,6 +757,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_tile_kernel(GemmArgs a) 
     int64_t p0;
     int tn;
     int64_t blk;
+    const float *wn = nullptr;   // the expert's row norms (gate_up with f16 output)
     if constexpr (MODE == GM_DENSE) {
         // 1-D grid, padded to a multiple of 8; workgroup id -> logical index
         // xcd * per + id / 8 walks the row blocks of one token tile per XCD
@@ -724,6 +774,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_tile_kernel(GemmArgs a) 
         const int tile = blockIdx.y;
         if (tile >= a.n_tiles[0]) return;
         Wt += (int64_t)a.tile_e[tile] * a.wt_bytes;
+        if (a.wnorm) wn = a.wnorm + 2 * (int64_t)a.tile_e[tile];
         p0 = a.tile_p0[tile];
         tn = a.tile_n[tile];
     }
@@ -741,14 +792,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_tile_kernel(GemmArgs a) 
     const uint8_t *w0p = Wt + (t0 < tiles ? t0 : tiles - 1) * nsb * BB;
     const uint8_t *w1p = Wt + (t1 < tiles ? t1 : tiles - 1) * nsb * BB;
     if constexpr (MODE == GM_DENSE || NI != 4) {
-        gt_main<T, BN, MODE, NW, NI>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
+        gt_main<T, BN, MODE, NW, NI>(a, Xs, tsc, asc, wn, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
     } else {
         // expert tiles: one copy of the loop per count of 16-token tiles
         const int nv = __builtin_amdgcn_readfirstlane((tn + 15) >> 4);
-        if (nv == 1) gt_main<T, BN, MODE, NW, 1>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
-        else if (nv == 2) gt_main<T, BN, MODE, NW, 2>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
-        else if (nv == 3) gt_main<T, BN, MODE, NW, 3>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
-        else gt_main<T, BN, MODE, NW, 4>(a, Xs, tsc, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
+        if (nv == 1) gt_main<T, BN, MODE, NW, 1>(a, Xs, tsc, asc, wn, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
+        else if (nv == 2) gt_main<T, BN, MODE, NW, 2>(a, Xs, tsc, asc, wn, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
+        else if (nv == 3) gt_main<T, BN, MODE, NW, 3>(a, Xs, tsc, asc, wn, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
+        else gt_main<T, BN, MODE, NW, 4>(a, Xs, tsc, asc, wn, w0p, w1p, p0, tn, t0, t1, tiles, nsb);
     }
 }
 
@@ -1124,8 +1175,9 @@ __global__ __launch_bounds__(512) void x_to_f16_tiles_kernel(const float *__rest
 }
 
 int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *rows_map, int k, int64_t ntok,
-                    _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s, int tiled) {
+                    _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s, int tiled, float *nrm2) {
     if (ntok <= 0) return LOCALAI_OK;
+    if (tiled && nrm2) return fail(LOCALAI_EARG, "f16 tiles: no row norms");
     if (cols % 8 || ldh % 8 || ldh < cols) return fail(LOCALAI_EARG, "f16 rows: cols % 8 != 0");
     if (tiled && ldh % 32) return fail(LOCALAI_EARG, "f16 tiles: row length % 32 != 0");
     const int vec = (uintptr_t)X % 16 == 0 && ldx % 4 == 0;
@@ -1152,7 +1204,7 @@ int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *ro
     const dim3 grid((unsigned)((npad + wpg - 1) / wpg));
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, dim3(64 * wpg), 0, s, X, ldx, (int)cols, rows_map, k, ntok, Xh, (int)ldh, inv,
-                           vec, tiled, npad);
+                           vec, tiled, npad, nrm2);
     };
     if (per <= 1)
         go(x_to_f16_kernel<1>);
@@ -1233,7 +1285,8 @@ int moe_gemm_tile() { return GM_MOE_BN; }
 int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, const uint8_t *Wt_all, int64_t wt_bytes, bool gate_up,
                     const _Float16 *Xh, int64_t ldh, const float *inv, const int32_t *rows_map, int rows_k,
                     float *Y, int64_t y_ts, int64_t inter, const int32_t *tile_e, const int32_t *tile_p0,
-                    const int32_t *tile_n, const int32_t *n_tiles, int max_tiles, hipStream_t s) {
+                    const int32_t *tile_n, const int32_t *n_tiles, int max_tiles, hipStream_t s,
+                    const MoeF16Out *f16_out) {
     GemmArgs a{};
     a.g = g; a.W = Wall; a.Xh = Xh; a.ldh = (int)ldh; a.inv = inv; a.Y = Y; a.y_ts = y_ts; a.y_rs = 1;
     a.rows_map = rows_map; a.rows_k = rows_k;
@@ -1241,6 +1294,12 @@ int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, const uint8_t *Wt_all
     a.Wt = Wt_all; a.wt_bytes = wt_bytes;
     if (max_tiles <= 0) return LOCALAI_OK;
     if (max_tiles > 65535) return fail(LOCALAI_EARG, "moe: too many token tiles");
+    if (f16_out) {
+        if (!gate_up || !Wt_all || inter % MT_ROWS || !f16_out->wnorm || !f16_out->xnorm2)
+            return fail(LOCALAI_EARG, "moe: f16 gate_up output needs the tile form, inter % 16 == 0 and the norms");
+        a.Yh = f16_out->Yh; a.ldy = f16_out->ldy; a.inv_out = f16_out->inv_out;
+        a.wnorm = f16_out->wnorm; a.xnorm2 = f16_out->xnorm2;
+    }
     if (Wt_all && (!gate_up || inter % MT_ROWS == 0)) {
         constexpr int NW = GM_MOE_NW;
         if (gate_up)

@@ -14,6 +14,8 @@ struct localai_qmat {
     int device;
     uint8_t *tiles;     // device, MFMA tile form (gemv_mfma.hip) or null
     int64_t tile_bytes; // per matrix of the tile form
+    float *row_norm;    // device, with the tile form: per matrix, the largest row L2 norm of rows
+                        // [0, rows / 2) and of rows [rows / 2, rows) (gate_up: gate and up), rounded up
 };
 
 namespace lq {
@@ -56,6 +58,9 @@ int launch_matvec(const lq_geom &g, const uint8_t *packed, const float *x, int64
 
 int64_t mt_matrix_bytes(const lq_geom &g);
 int launch_mt_repack(const lq_geom &g, const uint8_t *ggml, uint8_t *dst, int64_t dst_matrix_bytes, hipStream_t s);
+// largest row L2 norms of the two row halves of every matrix of GGML bytes
+// (localai_qmat::row_norm; out: 2 * batch floats, cleared here)
+int launch_row_norms(const lq_geom &g, const uint8_t *ggml, float *out, hipStream_t s);
 // tile form -> GGML bytes (the inverse of launch_mt_repack)
 int launch_mt_unpack(const lq_geom &g, const uint8_t *tiles, int64_t tile_matrix_bytes, uint8_t *ggml,
                      hipStream_t s);
@@ -99,12 +104,22 @@ int64_t gemm_workspace_bytes(const lq_geom &g, int64_t ntok);
 int launch_gemm(const lq_geom &g, const uint8_t *packed, const uint8_t *Wt, const float *x, int64_t ntok, float *y,
                 int64_t y_ts, int64_t y_rs, void *ws, int64_t ws_bytes, hipStream_t s);
 
+// nrm2 (not null, row layout only): each row's sum of squares
 int launch_x_to_f16(const float *X, int64_t ldx, int64_t cols, const int32_t *rows_map, int k, int64_t ntok,
-                    _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s, int tiled = 0);
+                    _Float16 *Xh, int64_t ldh, float *inv, hipStream_t s, int tiled = 0, float *nrm2 = nullptr);
+// The gate_up expert GEMM's f16 output (GemmArgs::Yh): the down GEMM's input
+// rows and their scales written directly.
+struct MoeF16Out {
+    _Float16 *Yh;
+    int64_t ldy;
+    float *inv_out;
+    const float *wnorm, *xnorm2;
+};
 int launch_moe_gemm(const lq_geom &g, const uint8_t *Wall, const uint8_t *Wt_all, int64_t wt_bytes, bool gate_up,
                     const _Float16 *Xh, int64_t ldh, const float *inv, const int32_t *rows_map, int rows_k,
                     float *Y, int64_t y_ts, int64_t inter, const int32_t *tile_e, const int32_t *tile_p0,
-                    const int32_t *tile_n, const int32_t *n_tiles, int max_tiles, hipStream_t s);
+                    const int32_t *tile_n, const int32_t *n_tiles, int max_tiles, hipStream_t s,
+                    const MoeF16Out *f16_out = nullptr);
 int moe_gemm_tile();   // tokens per expert GEMM tile
 
 int launch_zaya_router_tail(const float *r0, const float *b0, const float *prev, const float *eda,
@@ -116,7 +131,7 @@ int launch_zaya_scale(const float *gu, const float *x, int64_t n, const float *s
 
 struct MoeLayout {
     int64_t logits, sync, counts, offsets, active, n_active, perm, pos, act, ysl;
-    int64_t tile_e, tile_p0, tile_n, n_tiles, xh_gu, inv_gu, xh_dn, inv_dn;
+    int64_t tile_e, tile_p0, tile_n, n_tiles, xh_gu, inv_gu, hn2, xh_dn, inv_dn;
     int64_t max_tiles, bytes;
 };
 MoeLayout moe_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I);

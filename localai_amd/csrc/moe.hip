@@ -58,6 +58,7 @@ struct MoeTables {
     int32_t *n_tiles;   // [1]
     _Float16 *xh_gu;    // [T, ldh(H)] f16 token rows of h
     float *inv_gu;      // [T]
+    float *hn2;         // [T] sum of squares of each token row of h
     _Float16 *xh_dn;    // [N, ldh(I)] f16 act rows
     float *inv_dn;      // [N]
     int max_tiles;
@@ -533,6 +534,7 @@ struct F16Rows {
     _Float16 *Xh;
     float *inv;
     int cols, ldh, vec;
+    float *nrm2;   // each row's sum of squares (x_to_f16_row)
 };
 template <int CONV>
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float *__restrict__ logits, int T, int E, int k,
@@ -541,7 +543,7 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *__restrict__
     const int t = blockIdx.x * 4 + wave_id();
     if (t >= T) return;
     if constexpr (CONV >= 0)
-        x_to_f16_row<CONV>(t, cv.X, cv.cols, cv.cols, nullptr, 1, T, cv.Xh, cv.ldh, cv.inv, cv.vec, 0, T);
+        x_to_f16_row<CONV>(t, cv.X, cv.cols, cv.cols, nullptr, 1, T, cv.Xh, cv.ldh, cv.inv, cv.vec, 0, T, cv.nrm2);
     route_select_any(logits + (int64_t)t * E, E, k, t, topk_idx, topk_w, MoeTables{}, 0);
 }
 
@@ -1111,6 +1113,13 @@ static int64_t moe_max_tiles(int64_t N, int64_t E, int tile_w) {
 // f16 token rows, zero-padded to a multiple of 256 values (gemm.hip)
 static int64_t f16_stride(int64_t cols) { return 256 * ((cols + 255) / 256); }
 
+// Whether the prefill gate_up GEMM writes the down GEMM's f16 rows itself
+// (on the tile form, with the handle's row norms, rows without padding);
+// else it writes fp32 SiLU * up rows and x_to_f16 converts them.
+static bool moe_gate_up_f16_out(const localai_qmat *gu, int64_t I) {
+    return gu->tiles && gu->row_norm && I % MT_ROWS == 0 && f16_stride(I) == I;
+}
+
 // Byte offsets of the workspace's tables, each 256-byte aligned (the expert
 // GEMM tables only from MOE_GEMM_TOKENS tokens on; -1 otherwise).
 MoeLayout moe_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
@@ -1129,7 +1138,7 @@ MoeLayout moe_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
     L.act = take(N * I * 4);
     L.ysl = take(N * H * 4);
     L.max_tiles = 0;
-    L.tile_e = L.tile_p0 = L.tile_n = L.n_tiles = L.xh_gu = L.inv_gu = L.xh_dn = L.inv_dn = -1;
+    L.tile_e = L.tile_p0 = L.tile_n = L.n_tiles = L.xh_gu = L.inv_gu = L.hn2 = L.xh_dn = L.inv_dn = -1;
     if (T >= MOE_GEMM_TOKENS) {
         L.max_tiles = moe_max_tiles(N, E, moe_gemm_tile());
         L.tile_e = take(L.max_tiles * 4);
@@ -1138,6 +1147,7 @@ MoeLayout moe_layout(int64_t T, int64_t E, int64_t k, int64_t H, int64_t I) {
         L.n_tiles = take(4);
         L.xh_gu = take(T * f16_stride(H) * 2);
         L.inv_gu = take(T * 4);
+        L.hn2 = take(T * 4);
         L.xh_dn = take(N * f16_stride(I) * 2);
         L.inv_dn = take(N * 4);
     }
@@ -1173,6 +1183,7 @@ static MoeTables carve(void *ws, int64_t T, int64_t E, int64_t k, int64_t H, int
         tb.n_tiles = (int32_t *)(p + L.n_tiles);
         tb.xh_gu = (_Float16 *)(p + L.xh_gu);
         tb.inv_gu = (float *)(p + L.inv_gu);
+        tb.hn2 = (float *)(p + L.hn2);
         tb.xh_dn = (_Float16 *)(p + L.xh_dn);
         tb.inv_dn = (float *)(p + L.inv_dn);
     }
@@ -1392,7 +1403,8 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
         const dim3 tgrid((unsigned)((T + 3) / 4));
         if (tb.tile_w > 0 && gu->g.cols == H && H % 8 == 0 && f16_stride(H) <= 8 * 64 * 8) {
             // prefill: the f16 rows of h that gate_up reads come with the selection
-            const F16Rows cv{h, tb.xh_gu, tb.inv_gu, (int)H, (int)f16_stride(H), (int)((uintptr_t)h % 16 == 0 && H % 4 == 0)};
+            const F16Rows cv{h,   tb.xh_gu, tb.inv_gu, (int)H, (int)f16_stride(H), (int)((uintptr_t)h % 16 == 0 && H % 4 == 0),
+                             tb.hn2};
             const int per = (int)((f16_stride(H) / 8 + 63) / 64);
             auto go = [&](auto kern) {
                 hipLaunchKernelGGL(kern, tgrid, dim3(256), 0, s, tb.logits, (int)T, (int)E, k, topk_idx, topk_w, cv);
@@ -1442,19 +1454,25 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
         if (gu->g.cols != H || dn->g.cols != I) return fail(LOCALAI_EARG, "moe: expert shapes");
         // gate_up reads the f16 rows of h through the permutation (perm[p] / k)
         if (!h_f16_done)
-            if (int st = launch_x_to_f16(h, H, H, nullptr, 1, T, tb.xh_gu, f16_stride(H), tb.inv_gu, s)) return st;
+            if (int st = launch_x_to_f16(h, H, H, nullptr, 1, T, tb.xh_gu, f16_stride(H), tb.inv_gu, s, 0, tb.hn2))
+                return st;
         // the expert GEMMs read the tile form where there is one (gate_up
         // with inter a multiple of 16), else the row planes
         int st = LOCALAI_OK;
-        const uint8_t *wgu = gu->tiles && I % MT_ROWS == 0 ? nullptr : qmat_planes(gu, s, &st);
+        const bool gu_tiled = gu->tiles && I % MT_ROWS == 0;
+        const uint8_t *wgu = gu_tiled ? nullptr : qmat_planes(gu, s, &st);
         if (st) return st;
         const uint8_t *wdn = dn->tiles ? nullptr : qmat_planes(dn, s, &st);
         if (st) return st;
-        if (int st = launch_moe_gemm(gu->g, wgu, gu->tiles && I % MT_ROWS == 0 ? gu->tiles : nullptr, gu->tile_bytes, true, tb.xh_gu, f16_stride(H),
-                                     tb.inv_gu, tb.perm, k, tb.act, I, I, tb.tile_e, tb.tile_p0, tb.tile_n,
-                                     tb.n_tiles, tb.max_tiles, s))
+        // on the tile form, gate_up writes the down GEMM's f16 rows itself
+        const MoeF16Out direct{tb.xh_dn, f16_stride(I), tb.inv_dn, gu->row_norm, tb.hn2};
+        const bool f16_out = moe_gate_up_f16_out(gu, I);
+        if (int st = launch_moe_gemm(gu->g, wgu, gu_tiled ? gu->tiles : nullptr, gu->tile_bytes, true, tb.xh_gu,
+                                     f16_stride(H), tb.inv_gu, tb.perm, k, tb.act, I, I, tb.tile_e, tb.tile_p0,
+                                     tb.tile_n, tb.n_tiles, tb.max_tiles, s, f16_out ? &direct : nullptr))
             return st;
-        if (int st = launch_x_to_f16(tb.act, I, I, nullptr, 1, N, tb.xh_dn, f16_stride(I), tb.inv_dn, s)) return st;
+        if (!f16_out)
+            if (int st = launch_x_to_f16(tb.act, I, I, nullptr, 1, N, tb.xh_dn, f16_stride(I), tb.inv_dn, s)) return st;
         if (int st = launch_moe_gemm(dn->g, wdn, dn->tiles, dn->tile_bytes, false, tb.xh_dn, f16_stride(I),
                                      tb.inv_dn, nullptr, 1, tb.ysl, H, I, tb.tile_e, tb.tile_p0, tb.tile_n,
                                      tb.n_tiles, tb.max_tiles, s))
@@ -1505,9 +1523,10 @@ int launch_moe_expert_gemm(const localai_qmat *gu, const localai_qmat *dn, int64
     if (which == 0) {
         const bool tiled = gu->tiles && I % MT_ROWS == 0;
         if (!tiled && !gu->data) return fail(LOCALAI_ESTATE, "moe expert gemm: run the layer once first");
+        const MoeF16Out direct{tb.xh_dn, f16_stride(I), tb.inv_dn, gu->row_norm, tb.hn2};
         return launch_moe_gemm(gu->g, tiled ? nullptr : gu->data, tiled ? gu->tiles : nullptr, gu->tile_bytes, true,
                                tb.xh_gu, f16_stride(H), tb.inv_gu, tb.perm, k, tb.act, I, I, tb.tile_e, tb.tile_p0,
-                               tb.tile_n, tb.n_tiles, tb.max_tiles, s);
+                               tb.tile_n, tb.n_tiles, tb.max_tiles, s, moe_gate_up_f16_out(gu, I) ? &direct : nullptr);
     }
     if (!dn->tiles && !dn->data) return fail(LOCALAI_ESTATE, "moe expert gemm: run the layer once first");
     return launch_moe_gemm(dn->g, dn->tiles ? nullptr : dn->data, dn->tiles, dn->tile_bytes, false, tb.xh_dn,

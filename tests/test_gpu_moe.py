@@ -60,6 +60,27 @@ def test_qwen3_moe_style_small_prefill():
     assert normwise_rel(out, rout) < 1e-3
 
 
+@pytest.mark.parametrize('scale', (2.0 ** -30, 1.0, 2.0 ** 30))
+@pytest.mark.parametrize('t,I', [(12, 256), (8, 256), (8, 320)])
+def test_prefill_act_rows_at_extreme_scales(scale, t, I):
+    """The gate_up GEMM scales its f16 SiLU*up rows by a power of two taken
+    from a bound (expert row norms times |h|^2) when inter is a multiple of
+    256; otherwise (Q8_0, I = 320) it writes fp32 rows that a conversion
+    kernel scales by their maximum. Both keep the layer within 1e-3 of the
+    oracle for activations 2^30 times smaller or larger than usual, and for a
+    token whose row of h is all zero."""
+    from localai_amd import synth
+    rng = np.random.default_rng(int(np.log2(scale)) + 100 + I + t)
+    E, H, k, T = 8, 512, 2, 40
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    h = synth.activations(rng, T, H) * np.float32(scale)
+    h[5] = 0.0
+    (out, idx, g), (rout, ridx, rg) = run_both(rw, gu, dn, t, E, H, I, k, h)
+    np.testing.assert_array_equal(idx, ridx)
+    assert np.isfinite(out).all()
+    assert normwise_rel(out, rout) < 1e-3
+
+
 @pytest.mark.parametrize('t', (12, 14, 8))
 @pytest.mark.parametrize('T', (31, 32, 67, 200))
 def test_gemm_path_threshold_and_ragged_tiles(t, T):
