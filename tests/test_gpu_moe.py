@@ -61,7 +61,7 @@ def test_qwen3_moe_style_small_prefill():
 
 
 @pytest.mark.parametrize('scale', (2.0 ** -30, 1.0, 2.0 ** 30))
-@pytest.mark.parametrize('t,I', [(12, 256), (8, 256), (8, 320)])
+@pytest.mark.parametrize('t,I', [(12, 256), (14, 256), (8, 256), (8, 320)])
 def test_prefill_act_rows_at_extreme_scales(scale, t, I):
     """The gate_up GEMM scales its f16 SiLU*up rows by a power of two taken
     from a bound (expert row norms times |h|^2) when inter is a multiple of
