@@ -1006,7 +1006,9 @@ __global__ void moe_combine_vec_kernel(const float *__restrict__ ysl, const int3
 // LDS: the mt_pass regions.
 // sel_logits (not null; E <= 64): the router wrote only the logits
 // (moe_route1_kernel) and each workgroup selects the experts itself, before
-// anything else; topk_idx / topk_w then receive the selection.
+// anything else; topk_idx / topk_w then receive the selection, and the
+// routing tables (counts, offsets, active, perm, pos) come from the first
+// down tile.
 // SKIP: skip is the route index that stands for "no expert" (ZAYA's skip
 // route, engine/zaya.py:297-301): its slot adds gate * h instead of an
 // expert output; its gate_up tiles read no weights but still clear and
@@ -1036,7 +1038,8 @@ __global__ __launch_bounds__(512) void moe_decode1_kernel(
         // workgroup selects them itself (route_select, the router's own
         // rule); workgroup 0 also writes them out
         if (w == 0) {
-            route_select<1>(sel_logits, E, k, 0, sel_idx, sel_w, tb, 0);
+            // the first down tile (which waits anyway) also writes the routing tables
+            route_select<1>(sel_logits, E, k, 0, sel_idx, sel_w, tb, r == n_gu);
             if (r == 0 && lane < k) {
                 const_cast<int32_t *>(topk_idx)[lane] = sel_idx[lane];
                 const_cast<float *>(topk_w)[lane] = sel_w[lane];
@@ -1375,7 +1378,9 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
     const int64_t I = gu->g.rows / 2;
     MoeTables tb = carve(ws, T, E, k, H, I);
     const int one = T == 1 && tb.tile_w == 0;   // single token: the router writes the tables
-    if (one && k <= 2 && E <= 64 && moe_mfma_ok(gu, dn, h, H, I)) {
+    // the fused expert kernel clears out while other workgroups still read h
+    const bool apart = out + T * H <= h || h + T * H <= out;
+    if (one && k <= 2 && E <= 64 && apart && moe_mfma_ok(gu, dn, h, H, I)) {
         // one token through the fused expert kernel: the router writes only
         // the logits and the expert kernel selects
         if (H % (256 * ROUTE_CH))
@@ -1478,15 +1483,15 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
                                      tb.n_tiles, tb.max_tiles, s))
             return st;
     } else if (moe_mfma_ok(gu, dn, h, H, I)) {
-        // decode on MFMA; one token with k <= 2: gate_up and down in one
-        // launch, the combine folded into down
-        if (T == 1 && k <= 2)
+        // decode on MFMA; one token with k <= 2 (out apart from h): gate_up
+        // and down in one launch, the combine folded into down
+        if (T == 1 && k <= 2 && apart)
             return gu->g.type == LQ_Q6_K
                        ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s)
                        : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
         // k <= 2: down adds gate * y onto out (cleared by gate_up) itself,
         // unless out overlaps h (gate_up still reads h)
-        float *fold = k <= 2 && (out + T * H <= h || h + T * H <= out) ? out : nullptr;
+        float *fold = k <= 2 && apart ? out : nullptr;
         const int st = gu->g.type == LQ_Q6_K
                            ? launch_moe_mfma_t<LQ_Q6_K>(gu, dn, tb, h, H, I, k, slots, fold, topk_w, T, s)
                            : launch_moe_mfma_t<LQ_Q4_K>(gu, dn, tb, h, H, I, k, slots, fold, topk_w, T, s);

@@ -404,3 +404,116 @@ def test_routing_tables_are_a_stable_sort(E, T, k):
     assert ('tile_e' in got) == (T >= 32)
     for name, w in want.items():
         np.testing.assert_array_equal(got[name], w, err_msg=name)
+
+
+@pytest.mark.parametrize('t,E,T,k,H,I', [
+    (14, 16, 8, 2, 1024, 512),     # ZAYA-like, one workgroup tile of down rows per 16
+    (12, 16, 2, 2, 512, 256),      # two tokens
+    (12, 64, 31, 2, 512, 256),     # 62 assignments over 64 experts (one wave's worth)
+    (14, 4, 31, 2, 256, 256),      # few experts, many assignments each
+    (12, 8, 5, 1, 2048, 4096),     # top-1, K = 8 / 16 super-blocks (ZAYA's row widths)
+    (14, 2, 3, 2, 256, 256),       # both experts for every token
+])
+def test_few_token_layer_and_tables(t, E, T, k, H, I):
+    """2 .. 31 tokens on Q4_K / Q6_K experts (route and permute kernels, then
+    the grouped i8 MFMA kernels): routing, gates and output against the
+    oracle, and the routing tables against a stable sort."""
+    from localai_amd import synth
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(T * 13 + E + t)
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    h = synth.activations(rng, T, H)
+    layer = MoELayer(rw, gu, dn, t, E, H, I, k)
+    out, idx, g = layer.forward(h)
+    rout, ridx, rg, _ = omoe.moe_forward(h, rw, gu, dn, t, E, k, I)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
+    assert normwise_rel(out, rout) < 1e-5
+    got = layer.last_tables(T)
+    for name, w in expected_tables(idx, E, 0).items():
+        np.testing.assert_array_equal(got[name], w, err_msg=name)
+
+
+@pytest.mark.parametrize('T', (1, 8))
+def test_routing_tables_on_the_mfma_decode_path(T):
+    """One token (the fused kernel's first workgroup writes the tables) and
+    eight (route and permute kernels), Q6_K experts: the tables against a
+    stable sort."""
+    from localai_amd import synth
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(5 + T)
+    E, H, I, k, t = 16, 512, 256, 2, 14
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    h = synth.activations(rng, T, H)
+    layer = MoELayer(rw, gu, dn, t, E, H, I, k)
+    _, idx, _ = layer.forward(h)
+    got = layer.last_tables(T)
+    for name, w in expected_tables(idx, E, 0).items():
+        np.testing.assert_array_equal(got[name], w, err_msg=name)
+
+
+@pytest.mark.parametrize('T', (1, 8))
+def test_output_in_place_of_h(T):
+    """out given as h's own buffer: the fused kernels (which clear out while
+    other workgroups still read h) are not taken; the separate kernels and
+    the combine give the oracle's result."""
+    import torch
+    from localai_amd import synth, device
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(71 + T)
+    E, H, I, k, t = 16, 512, 256, 2, 14
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    h = synth.activations(rng, T, H)
+    layer = MoELayer(rw, gu, dn, t, E, H, I, k)
+    hd = device.to_device_f32(h)
+    out, idx, g = layer.forward_device(hd, out=hd)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == hd.data_ptr()
+    rout, ridx, rg, _ = omoe.moe_forward(h, rw, gu, dn, t, E, k, I)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    assert normwise_rel(out.cpu().numpy(), rout) < 1e-5
+
+
+def test_few_token_layer_repeated_and_graph_replayed():
+    """The few-token path (route, permute, grouped gate_up and down):
+    back-to-back calls of 8 tokens, a call of 3 and one of 1 in between, and
+    replays of a captured graph all match the oracle."""
+    import torch
+    from localai_amd import synth, device
+    from localai_amd.moe import MoELayer
+    rng = np.random.default_rng(78)
+    E, H, I, k, t, T = 16, 1024, 512, 2, 14, 8
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    layer = MoELayer(rw, gu, dn, t, E, H, I, k)
+
+    def check(h, out, idx, g):
+        rout, ridx, rg, _ = omoe.moe_forward(h, rw, gu, dn, t, E, k, I)
+        np.testing.assert_array_equal(idx, ridx)
+        np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
+        assert normwise_rel(out, rout) < 1e-5
+
+    for n in (T, T, 3, 1, T):
+        h = synth.activations(rng, n, H)
+        check(h, *layer.forward(h))
+    stream = torch.cuda.Stream()
+    hd = device.to_device_f32(synth.activations(rng, T, H))
+    out = torch.empty((T, H), dtype=torch.float32, device=hd.device)
+    idx = torch.empty((T, k), dtype=torch.int32, device=hd.device)
+    gates = torch.empty((T, k), dtype=torch.float32, device=hd.device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        layer.forward_device(hd, out=out, idx=idx, gates=gates, stream=stream)
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            layer.forward_device(hd, out=out, idx=idx, gates=gates, stream=stream)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        h = synth.activations(rng, T, H)
+        hd.copy_(torch.from_numpy(h).to(hd.device))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        check(h, out.cpu().numpy(), idx.cpu().numpy(), gates.cpu().numpy())
+        h3 = synth.activations(rng, 3, H)
+        check(h3, *layer.forward(h3))
+
