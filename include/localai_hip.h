@@ -330,9 +330,10 @@ int localai_hip_moe_forward(const float *h_dev, int64_t tokens, int64_t hidden,
  * [0, experts) that is not skip makes that slot's rows of out NaN and is
  * reported by localai_hip_moe_error. One launch for gate_up and down
  * (plus a counter clear); the sum is the same whatever order the slots land.
- * Experts must be Q4_K or Q6_K handles with the tile form, at most 32
- * super-blocks a row and inter % 64 == 0 (ETYPE otherwise: the caller then
- * runs the matvec path). Workspace: as
+ * Experts must be Q4_K, Q6_K or Q8_0 handles with the tile form (Q8_0:
+ * hidden and inter multiples of 256), at most 32 blocks of 256 values a row
+ * and inter % 64 == 0 (ETYPE otherwise: the caller then runs the matvec
+ * path). Workspace: as
  * localai_hip_moe_workspace_size(1, experts, top_k, hidden, inter); h_dev
  * 16-byte and the workspace 256-byte aligned; out must not overlap h. */
 int localai_hip_moe_experts1(const float *h_dev, int64_t hidden, const localai_qmat *gate_up,
@@ -351,7 +352,10 @@ int64_t localai_hip_static_workspace_bytes(void);
  * serving loops that forbid allocation -- can run the MoE layer. Same
  * arguments, limits and results as localai_hip_moe_forward; sizes whose
  * workspace (localai_hip_moe_workspace_size) exceeds the static one are
- * LOCALAI_EARG. All calls on one device share its array: calls that overlap
+ * LOCALAI_EARG; experts and sizes whose path would first build a handle's
+ * row planes (below 32 tokens: Q8_0 rows of partial 256-value blocks, rows
+ * over 64 blocks of 256; the ordinary entry builds them) are LOCALAI_ETYPE.
+ * All calls on one device share its array: calls that overlap
  * in time on one device race, and the router logits the workspace holds
  * after a call are overwritten by the next. No counterpart in the reference. */
 int localai_hip_moe_forward_static(const float *h_dev, int64_t tokens, int64_t hidden,

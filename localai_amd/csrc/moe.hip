@@ -947,6 +947,75 @@ __global__ __launch_bounds__(MAXT) void moe_mfma_down(const uint8_t *__restrict_
     }
 }
 
+// Rows of more than 32 blocks of 256 (up to 64): each wave's eight blocks
+// stream through two register sets (mt_pass_pipe) for every token instead
+// of being held, x is read for each token after the previous pass, and
+// gate_up runs its gate and up tiles as two passes; otherwise as
+// moe_mfma_gate_up / moe_mfma_down with one row tile per workgroup.
+template <int TYPE, int SPW>
+__global__ __launch_bounds__(512) void moe_mfma_gate_up_pipe(const uint8_t *__restrict__ Wt, int64_t mat_bytes,
+                                                              int nb, int64_t inter, MoeTables tb,
+                                                              const float *__restrict__ h, int64_t H, int k,
+                                                              float *__restrict__ zero, int64_t nzero) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int slot = blockIdx.y;
+    if (zero && slot == 0) {
+        const int64_t per = (nzero + gridDim.x - 1) / gridDim.x, c0 = blockIdx.x * per;
+        for (int64_t c = c0 + threadIdx.x; c < c0 + per && c < nzero; c += blockDim.x) zero[c] = 0.0f;
+    }
+    if (slot >= tb.n_active[0]) return;
+    const int e = tb.active[slot];
+    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    const int64_t i = blockIdx.x, tile_bytes = (int64_t)nb * mt_block_bytes(TYPE);
+    const uint8_t *We = Wt + (int64_t)e * mat_bytes;
+    const int64_t gtiles = inter / MT_ROWS;
+    const uint8_t *const tg[1] = {We + i * tile_bytes}, *const tu[1] = {We + (gtiles + i) * tile_bytes};
+    const int n = tb.counts[e], base = tb.offsets[e];
+    const int r = threadIdx.x;
+    for (int j = 0; j < n; ++j) {
+        const int p = base + j;
+        float4 xv[SPW];
+        mt_load_x<SPW>(xv, h + (int64_t)(tb.perm[p] / k) * H, nb, sb0, lane);
+        float *fin;
+        mt_pass_pipe<TYPE, SPW, 1>(tg, nb, sb0, nsb, xv, smem, fin);
+        const float gv = r < MT_ROWS ? fin[r] : 0.0f;
+        mt_pass_pipe<TYPE, SPW, 1>(tu, nb, sb0, nsb, xv, smem, fin);
+        if (r < MT_ROWS) tb.act[(int64_t)p * inter + i * MT_ROWS + r] = silu(gv) * fin[r];
+    }
+}
+
+template <int TYPE, int SPW>
+__global__ __launch_bounds__(512) void moe_mfma_down_pipe(const uint8_t *__restrict__ Wt, int64_t mat_bytes, int nb,
+                                                           int64_t hidden, MoeTables tb, int64_t inter,
+                                                           float *__restrict__ out, const float *__restrict__ topk_w,
+                                                           int k) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int slot = blockIdx.y;
+    if (slot >= tb.n_active[0]) return;
+    const int e = tb.active[slot];
+    const int n = tb.counts[e], base = tb.offsets[e];
+    const int lane = lane_id(), sb0 = wave_id() * SPW, nsb = mt_nsb(nb, sb0, SPW);
+    const int64_t i = blockIdx.x;
+    const uint8_t *const tl[1] = {Wt + (int64_t)e * mat_bytes + i * nb * mt_block_bytes(TYPE)};
+    const int r = threadIdx.x;
+    const int64_t row = i * MT_ROWS + r;
+    for (int j = 0; j < n; ++j) {
+        const int p = base + j;
+        float4 xv[SPW];
+        mt_load_x<SPW>(xv, tb.act + (int64_t)p * inter, nb, sb0, lane);
+        float *fin;
+        mt_pass_pipe<TYPE, SPW, 1>(tl, nb, sb0, nsb, xv, smem, fin);
+        if (r < MT_ROWS && row < hidden) {
+            if (out) {
+                const int a = tb.perm[p];
+                atomicAdd(out + (int64_t)(a / k) * hidden + row, topk_w[a] * fin[r]);
+            } else {
+                tb.ysl[(int64_t)p * hidden + row] = fin[r];
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- combine
 
 // out[t, :] = sum_j topk_w[t, j] * ysl[pos[t*k + j], :], slots in top-k order
@@ -1244,13 +1313,26 @@ static int launch_grouped(const localai_qmat *m, const MoeTables &tb, const floa
     return LOCALAI_OK;
 }
 
-// MFMA decode path: both expert tensors in the tile form with K <= 32
-// super-blocks: one super-block per wave (up to 16 waves) for K <= 16
-// super-blocks, else four per wave (up to 8 waves, room for the registers).
+// MFMA decode path: both expert tensors in the tile form (Q4_K, Q6_K, or
+// Q8_0 with rows of whole 256-value blocks, since the kernels read x 256
+// values a block) with K <= 64 blocks of 256: one block per wave (up to 16
+// waves) for K <= 16, four per wave for K <= 32 (up to 8 waves, room for
+// the registers), four per wave streamed through two register sets for
+// K <= 64 (16 waves).
 static bool moe_mfma_ok(const localai_qmat *gu, const localai_qmat *dn, const float *h, int64_t H, int64_t I) {
-    return gu->tiles && dn->tiles && gu->g.type == dn->g.type && gu->g.type != LQ_Q8_0 && gu->g.nb <= 32 &&
-           dn->g.nb <= 32 &&
-           (reinterpret_cast<uintptr_t>(h) & 15) == 0 && I % MT_ROWS == 0 && gu->g.cols == H && dn->g.cols == I;
+    const bool q80 = gu->g.type == LQ_Q8_0;
+    // the streamed kernels' LDS (8 waves of eight staged blocks, ~76 KB)
+    const bool lds = (mt_nsb(gu->g) <= 32 && mt_nsb(dn->g) <= 32) ||
+                     mt_lds_bytes(gu->g.type, 8, 8, 1, 1) <= max_lds_per_block();
+    return gu->tiles && dn->tiles && gu->g.type == dn->g.type && mt_nsb(gu->g) <= 64 && mt_nsb(dn->g) <= 64 && lds &&
+           (!q80 || (H % 256 == 0 && I % 256 == 0)) && (reinterpret_cast<uintptr_t>(h) & 15) == 0 &&
+           I % MT_ROWS == 0 && gu->g.cols == H && dn->g.cols == I;
+}
+
+// The fused one-token kernel: at most 32 blocks of 256 per row (four per
+// wave of its 8 waves)
+static bool moe_decode1_ok(const localai_qmat *gu, const localai_qmat *dn) {
+    return mt_nsb(gu->g) <= 32 && mt_nsb(dn->g) <= 32;
 }
 
 // Whether launch_moe would have to build the row planes of gu or dn (a
@@ -1283,13 +1365,13 @@ static void launch_moe_mfma_st(const localai_qmat *gu, const localai_qmat *dn, c
                                int64_t H, int64_t I, int k, int slots, float *out, const float *topk_w, int64_t T,
                                bool gate_up, hipStream_t s) {
     if (gate_up) {
-        const int nb = (int)gu->g.nb, waves = (nb + SPW - 1) / SPW;
+        const int nb = (int)mt_nsb(gu->g), waves = (nb + SPW - 1) / SPW;
         const int64_t groups = (I / MT_ROWS + RT - 1) / RT;
         hipLaunchKernelGGL((moe_mfma_gate_up<TYPE, SPW, MAXT, RT>), dim3((unsigned)groups, slots), dim3(64 * waves),
                            mt_lds_bytes(TYPE, waves, SPW, 1, 2 * RT), s, gu->tiles, gu->tile_bytes, nb, I, tb, h, H, k,
                            out, T * H);
     } else {
-        const int nb = (int)dn->g.nb, waves = (nb + SPW - 1) / SPW;
+        const int nb = (int)mt_nsb(dn->g), waves = (nb + SPW - 1) / SPW;
         const int64_t groups = ((H + MT_ROWS - 1) / MT_ROWS + RT - 1) / RT;
         hipLaunchKernelGGL((moe_mfma_down<TYPE, SPW, MAXT, RT>), dim3((unsigned)groups, slots), dim3(64 * waves),
                            mt_lds_bytes(TYPE, waves, SPW, 1, RT), s, dn->tiles, dn->tile_bytes, nb, H, tb, I, out,
@@ -1297,22 +1379,46 @@ static void launch_moe_mfma_st(const localai_qmat *gu, const localai_qmat *dn, c
     }
 }
 
+// rows of 33 .. 64 blocks: moe_mfma_gate_up_pipe / moe_mfma_down_pipe, 8 waves
+// of eight blocks
+template <int TYPE>
+static void launch_moe_mfma_pipe(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
+                                 int64_t H, int64_t I, int k, int slots, float *out, const float *topk_w, int64_t T,
+                                 bool gate_up, hipStream_t s) {
+    if (gate_up) {
+        const int nb = (int)mt_nsb(gu->g), waves = (nb + 7) / 8;
+        hipLaunchKernelGGL((moe_mfma_gate_up_pipe<TYPE, 8>), dim3((unsigned)(I / MT_ROWS), slots), dim3(64 * waves),
+                           mt_lds_bytes(TYPE, waves, 8, 1, 1), s, gu->tiles, gu->tile_bytes, nb, I, tb, h, H, k, out,
+                           T * H);
+    } else {
+        const int nb = (int)mt_nsb(dn->g), waves = (nb + 7) / 8;
+        hipLaunchKernelGGL((moe_mfma_down_pipe<TYPE, 8>), dim3((unsigned)((H + MT_ROWS - 1) / MT_ROWS), slots),
+                           dim3(64 * waves), mt_lds_bytes(TYPE, waves, 8, 1, 1), s, dn->tiles, dn->tile_bytes, nb, H,
+                           tb, I, out, topk_w, k);
+    }
+}
+
 template <int TYPE>
 static int launch_moe_mfma_t(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
                              int64_t H, int64_t I, int k, int slots, float *out, const float *topk_w, int64_t T,
                              hipStream_t s) {
-    // nb <= 32 for both (moe_mfma_ok)
-    if (gu->g.nb <= 16)
+    // at most 64 blocks of 256 per row for both (moe_mfma_ok)
+    const int64_t ng = mt_nsb(gu->g), nd = mt_nsb(dn->g);
+    if (ng <= 16)
         launch_moe_mfma_st<TYPE, 1, 1024, 1>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, true, s);
-    else
+    else if (ng <= 32)
         launch_moe_mfma_st<TYPE, 4, 512, 1>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, true, s);
-    LQ_HIP(hipGetLastError());
-    if (dn->g.nb <= 8)
-        launch_moe_mfma_st<TYPE, 1, 512, 2>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, false, s);
-    else if (dn->g.nb <= 16)
-        launch_moe_mfma_st<TYPE, 2, 512, 2>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, false, s);
     else
+        launch_moe_mfma_pipe<TYPE>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, true, s);
+    LQ_HIP(hipGetLastError());
+    if (nd <= 8)
+        launch_moe_mfma_st<TYPE, 1, 512, 2>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, false, s);
+    else if (nd <= 16)
+        launch_moe_mfma_st<TYPE, 2, 512, 2>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, false, s);
+    else if (nd <= 32)
         launch_moe_mfma_st<TYPE, 4, 512, 1>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, false, s);
+    else
+        launch_moe_mfma_pipe<TYPE>(gu, dn, tb, h, H, I, k, slots, out, topk_w, T, false, s);
     LQ_HIP(hipGetLastError());
     return LOCALAI_OK;
 }
@@ -1348,7 +1454,7 @@ static void launch_decode1_k(const localai_qmat *gu, const localai_qmat *dn, con
     const unsigned grid = (unsigned)(k * (I / MT_ROWS) + k * ((H + MT_ROWS - 1) / MT_ROWS));
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(grid), dim3(512), a > b ? a : b, s, h, (int)H, (int)E, k, gu->tiles,
-                           gu->tile_bytes, (int)gu->g.nb, I, dn->tiles, dn->tile_bytes, (int)dn->g.nb, topk_idx,
+                           gu->tile_bytes, (int)mt_nsb(gu->g), I, dn->tiles, dn->tile_bytes, (int)mt_nsb(dn->g), topk_idx,
                            topk_w, out, tb, tb.sync, skip, g_d1_spin.load(), g_d1_count.load(), sel_logits);
     };
     if (skip >= 0)
@@ -1361,7 +1467,7 @@ template <int TYPE>
 static int launch_decode1_t(const localai_qmat *gu, const localai_qmat *dn, const MoeTables &tb, const float *h,
                             int64_t H, int64_t E, int k, int64_t I, const int32_t *topk_idx, const float *topk_w,
                             float *out, hipStream_t s, int skip = -1, const float *sel_logits = nullptr) {
-    const int sg = d1_spw(gu->g.nb), sd = d1_spw(dn->g.nb);
+    const int sg = d1_spw(mt_nsb(gu->g)), sd = d1_spw(mt_nsb(dn->g));
 #define LQ_D1(SG, SD)                                                                                       \
     if (sg == SG && sd == SD)                                                                               \
         launch_decode1_k<TYPE, SG, SD>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, skip, s, sel_logits);
@@ -1380,7 +1486,7 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
     const int one = T == 1 && tb.tile_w == 0;   // single token: the router writes the tables
     // the fused expert kernel clears out while other workgroups still read h
     const bool apart = out + T * H <= h || h + T * H <= out;
-    if (one && k <= 2 && E <= 64 && apart && moe_mfma_ok(gu, dn, h, H, I)) {
+    if (one && k <= 2 && E <= 64 && apart && moe_mfma_ok(gu, dn, h, H, I) && moe_decode1_ok(gu, dn)) {
         // one token through the fused expert kernel: the router writes only
         // the logits and the expert kernel selects
         if (H % (256 * ROUTE_CH))
@@ -1390,9 +1496,14 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
             hipLaunchKernelGGL(moe_route1_kernel<false>, dim3((unsigned)E), dim3(64), 0, s, h, (int)H, rw, rb,
                                tb.logits, tb.sync);
         LQ_HIP(hipGetLastError());
-        return gu->g.type == LQ_Q6_K
-                   ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, -1, tb.logits)
-                   : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, -1, tb.logits);
+        switch (gu->g.type) {
+            case LQ_Q6_K:
+                return launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, -1, tb.logits);
+            case LQ_Q8_0:
+                return launch_decode1_t<LQ_Q8_0>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, -1, tb.logits);
+            default:
+                return launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, -1, tb.logits);
+        }
     }
     bool h_f16_done = false;   // the f16 rows of h for the expert GEMMs written
     if (T >= ROUTE_TILE_TOKENS) {
@@ -1485,16 +1596,18 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
     } else if (moe_mfma_ok(gu, dn, h, H, I)) {
         // decode on MFMA; one token with k <= 2 (out apart from h): gate_up
         // and down in one launch, the combine folded into down
-        if (T == 1 && k <= 2 && apart)
-            return gu->g.type == LQ_Q6_K
-                       ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s)
-                       : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
+        if (T == 1 && k <= 2 && apart && moe_decode1_ok(gu, dn)) switch (gu->g.type) {
+                case LQ_Q6_K: return launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
+                case LQ_Q8_0: return launch_decode1_t<LQ_Q8_0>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
+                default: return launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s);
+            }
         // k <= 2: down adds gate * y onto out (cleared by gate_up) itself,
         // unless out overlaps h (gate_up still reads h)
         float *fold = k <= 2 && apart ? out : nullptr;
-        const int st = gu->g.type == LQ_Q6_K
-                           ? launch_moe_mfma_t<LQ_Q6_K>(gu, dn, tb, h, H, I, k, slots, fold, topk_w, T, s)
-                           : launch_moe_mfma_t<LQ_Q4_K>(gu, dn, tb, h, H, I, k, slots, fold, topk_w, T, s);
+        const int st =
+            gu->g.type == LQ_Q6_K   ? launch_moe_mfma_t<LQ_Q6_K>(gu, dn, tb, h, H, I, k, slots, fold, topk_w, T, s)
+            : gu->g.type == LQ_Q8_0 ? launch_moe_mfma_t<LQ_Q8_0>(gu, dn, tb, h, H, I, k, slots, fold, topk_w, T, s)
+                                    : launch_moe_mfma_t<LQ_Q4_K>(gu, dn, tb, h, H, I, k, slots, fold, topk_w, T, s);
         if (st) return st;
         if (fold) return LOCALAI_OK;
     } else {
@@ -1552,15 +1665,18 @@ int launch_moe_experts1(const float *h, int64_t H, const localai_qmat *gu, const
                         const int32_t *topk_idx, const float *topk_w, int skip, float *out, void *ws,
                         hipStream_t s) {
     const int64_t I = gu->g.rows / 2, E = gu->g.batch;
-    if (!moe_mfma_ok(gu, dn, h, H, I) || (gu->g.type != LQ_Q4_K && gu->g.type != LQ_Q6_K))
-        return fail(LOCALAI_ETYPE, "moe experts: Q4_K or Q6_K experts in the tile form, at most 32 blocks a row");
+    if (!moe_mfma_ok(gu, dn, h, H, I) || !moe_decode1_ok(gu, dn))
+        return fail(LOCALAI_ETYPE,
+                    "moe experts: Q4_K, Q6_K or Q8_0 experts in the tile form, at most 32 blocks of 256 a row");
     if (out < h + H && h < out + H) return fail(LOCALAI_EARG, "moe experts: out overlaps h");
     MoeTables tb = carve(ws, 1, E, k, H, I);
     hipLaunchKernelGGL(d1_clear_kernel, dim3(1), dim3(256), 0, s, tb.sync);
     LQ_HIP(hipGetLastError());
-    return gu->g.type == LQ_Q6_K
-               ? launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, skip)
-               : launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, skip);
+    switch (gu->g.type) {
+        case LQ_Q6_K: return launch_decode1_t<LQ_Q6_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, skip);
+        case LQ_Q8_0: return launch_decode1_t<LQ_Q8_0>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, skip);
+        default: return launch_decode1_t<LQ_Q4_K>(gu, dn, tb, h, H, E, k, I, topk_idx, topk_w, out, s, skip);
+    }
 }
 
 }  // namespace lq

@@ -77,8 +77,9 @@ int localai_hip_moe_forward_static(const float *h, int64_t T, int64_t H, const f
                                       " bytes of workspace, more than the library's " +
                                       std::to_string(STATIC_WS_BYTES));
     // Paths that read the row planes of a handle holding only the tile form
-    // (Q8_0 experts below 32 tokens, rows over 32 super-blocks, ...) would
-    // build them with hipMalloc: refused before any launch.
+    // (below 32 tokens: Q8_0 rows of partial 256-value blocks, rows over 64
+    // blocks of 256, ...) would build them with hipMalloc: refused before
+    // any launch.
     if (gu->g.rows % 2 == 0 && moe_would_build_planes(h, T, H, gu, dn))
         return fail(LOCALAI_ETYPE, "moe (static workspace): these experts and sizes take a path that reads row "
                                    "planes the handles do not hold yet; this entry point allocates nothing");

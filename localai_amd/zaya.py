@@ -13,7 +13,7 @@ Per MoE layer:
   expert e < E                        gate_up[e] h, SiLU * up, down[e] act,
                                       times probs[e] (engine/zaya.py:303-306)
   e == E (skip)                       h * probs[E] (:297-301)
-Q4_K / Q6_K experts run as one launch that reads the chosen index and its
+Q4_K / Q6_K / Q8_0 experts run as one launch that reads the chosen index and its
 probability on the device (localai_hip_moe_experts1, the skip route
 included), so the host waits only for the outputs. Other expert types take
 the matvec path: the host reads the index (four bytes) to pick the expert
@@ -163,7 +163,7 @@ class ZayaMoEMixin(ZayaExpertsMixin):
         ptr = device.ptr
         st = lib.localai_hip_moe_experts1(ptr(h_d), H, gu.handle, dn.handle, 1, ptr(expert), ptr(expert_w),
                                           self.n_experts, ptr(out), ptr(ws), ws.numel(), s)
-        if st == 2:   # ETYPE: not Q4_K / Q6_K on the tile form
+        if st == 2:   # ETYPE: not Q4_K / Q6_K / Q8_0 on the tile form
             cache[('experts1', p)] = False
             return False
         _lib.check(st)

@@ -168,23 +168,25 @@ def test_skip_route_and_forced_expert(tmp_path, forced, xt):
     assert normwise_rel(moe, w_moe) < (5e-6 if forced == E else 1e-5)
 
 
+@pytest.mark.parametrize('xt', [8, 13])
 @pytest.mark.parametrize('forced', [E, 3])
-def test_matvec_path_for_q8_0_experts(tmp_path, forced):
-    """Q8_0 experts have no one-launch kernel: the block reads the index on the
-    host and runs the matvecs; the skip route and an expert both checked."""
+def test_q8_0_and_matvec_path_experts(tmp_path, forced, xt):
+    """Q8_0 experts (tile form) take the one-launch kernel like Q4_K / Q6_K;
+    Q5_K experts have none: the block reads the index on the host and runs
+    the matvecs. The skip route and an expert both checked."""
     from localai_amd.gguf import GGUFFile
-    rng = np.random.default_rng(40 + forced)
+    rng = np.random.default_rng(40 + forced + xt)
     bias = np.zeros(E + 1)
     bias[forced] = 10.0
-    raw = layer_tensors(rng, bias, xt=8)
-    path = tmp_path / 'q8.gguf'
+    raw = layer_tensors(rng, bias, xt=xt)
+    path = tmp_path / f'x{xt}.gguf'
     write_layer(path, raw)
     t = oracle_tensors(raw)
     h = rng.standard_normal(H).astype(np.float32)
     with GGUFFile(path) as g:
         m = model_class()(g)
         moe, state = m._moe(1, h, None)
-        assert m._zaya_cache().get(('experts1', 'blk.1.')) is False
+        assert (m._zaya_cache().get(('experts1', 'blk.1.')) is False) == (xt == 13)
     w_moe, w_state, _, w_e, _ = zm.moe_block(t, E, EPS, h, None)
     assert w_e == forced
     assert normwise_rel(state, w_state) < 5e-6

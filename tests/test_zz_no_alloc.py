@@ -49,12 +49,15 @@ def _static(layer, hd):
     return outs
 
 
-@pytest.mark.parametrize('case', ['zaya_decode', 'qwen3_prefill'])
+@pytest.mark.parametrize('case', ['zaya_decode', 'q8_0_decode', 'qwen3_prefill'])
 def test_static_workspace_matches_caller_workspace(case):
     from localai_amd import device, synth
     if case == 'zaya_decode':   # hidden 2048, 16 Q6_K experts, top-2, intermediate 4096: 8 tokens, then 1
         layer, (rw, gu, dn), rng = _layer(71, 16, 2048, 4096, 2, 14)
         sizes = (8, 1)
+    elif case == 'q8_0_decode':   # 8 Q8_0 experts on the tile form (no row planes): 4 tokens, then 1
+        layer, (rw, gu, dn), rng = _layer(73, 8, 1024, 512, 2, 8)
+        sizes = (4, 1)
     else:                       # 64 Q4_K experts, top-8, intermediate 768: 96 tokens (GEMM path), then 8
         layer, (rw, gu, dn), rng = _layer(72, 64, 2048, 768, 8, 12)
         sizes = (96, 8)
@@ -67,23 +70,24 @@ def test_static_workspace_matches_caller_workspace(case):
         np.testing.assert_array_equal(sg.view(np.uint32), wg.view(np.uint32))
         np.testing.assert_array_equal(so.view(np.uint32), wo.view(np.uint32))
         if T <= 8:
-            ref, ridx, _, _ = omoe.moe_forward(h, rw, gu, dn, 14 if case == 'zaya_decode' else 12, layer.E,
-                                               layer.k, layer.I)
+            t = {'zaya_decode': 14, 'q8_0_decode': 8}.get(case, 12)
+            ref, ridx, _, _ = omoe.moe_forward(h, rw, gu, dn, t, layer.E, layer.k, layer.I)
             np.testing.assert_array_equal(si, ridx)
             assert normwise_rel(so, ref) < 1e-5
 
 
 def test_static_refuses_paths_that_would_build_row_planes():
-    """Q8_0 experts below 32 tokens run the grouped kernels over the row
-    planes, which a Q8_0 handle builds on first use (an allocation): the
-    static entry refuses with LOCALAI_ETYPE before any launch, and the free
-    device memory does not move. Once the ordinary entry has built the planes,
-    the static entry takes that path, allocates nothing and matches it bit for
-    bit (two calls, the second smaller)."""
+    """Q8_0 experts whose rows are not whole 256-value blocks (inter 320)
+    below 32 tokens run the grouped kernels over the row planes, which a
+    Q8_0 handle builds on first use (an allocation): the static entry
+    refuses with LOCALAI_ETYPE before any launch, and the free device memory
+    does not move. Once the ordinary entry has built the planes, the static
+    entry takes that path, allocates nothing and matches it bit for bit (two
+    calls, the second smaller)."""
     from localai_amd import _lib, device, synth
     lib = _lib.load()
     tt = device.torch()
-    layer, (rw, gu, dn), rng = _layer(74, 8, 1024, 512, 2, 8)
+    layer, (rw, gu, dn), rng = _layer(74, 8, 1024, 320, 2, 8)
     hd = device.to_device_f32(synth.activations(rng, 4, layer.H))
     outs = _outputs(layer, 4, hd.device)
     tt.cuda.synchronize()
