@@ -10,13 +10,13 @@
 //   silu(g)      = g / (1 + exp(-clip(g, -80, 80)))  (engine/zaya.py:305)
 //
 // Kernels (one stream, in order):
-//   route     few tokens: one workgroup per token: router logits, top-k,
-//             gates (for a single token also the permutation tables below);
-//             many tokens: register-tiled logits over LDS-streamed rows,
-//             then one wave per token for top-k and gates
-//   permute   one workgroup: ballot-matched ranks per wave, per-expert
-//             scan, stable expert-major permutation of the T*k assignments
-//             and the expert GEMM tile list
+//   route     few tokens: the router logits, one one-wave workgroup per
+//             (expert, token); many tokens: register-tiled logits over
+//             LDS-streamed rows, then one wave per token for top-k and gates
+//   permute   one workgroup (few tokens: first top-k and gates, one wave per
+//             token): ballot-matched ranks per wave, per-expert scan, stable
+//             expert-major permutation of the T*k assignments and the expert
+//             GEMM tile list
 //   gate_up   grouped matvec over the active experts, one workgroup per
 //             (64-row gate tile + matching up tile, expert); SiLU*up fused
 //   down      grouped matvec over the active experts
@@ -168,161 +168,33 @@ __device__ __forceinline__ void route_select_any(const float *lg, int E, int k, 
         route_select<16>(lg, E, k, t, topk_idx, topk_w, tb, tables);
 }
 
-// LDS of moe_route_kernel: h is staged as fp64 when it fits with the logits;
-// wider rows convert h in registers in every wave.
-constexpr size_t ROUTE_LDS_BYTES = 65536;
 // From this many tokens on, the logits come from moe_route_logits_kernel and
-// the selection from moe_topk_kernel.
+// the selection from moe_topk_kernel; below, from moe_route1_kernel and the
+// permutation.
 constexpr int ROUTE_TILE_TOKENS = 16;
-// 16-byte chunks per lane and pass of moe_route_kernel: rows of up to 2048
+// 16-byte chunks per lane and pass of moe_route1_kernel: rows of up to 2048
 // elements in one pass.
 constexpr int ROUTE_CH = 8;
 
-// Router of one token t by a whole workgroup (route_token; moe_route_kernel
-// runs one workgroup per token for a few tokens). h is converted to fp64
-// once (in LDS) and shared by the waves, each of which computes whole expert
-// logits from one read of the expert's router row (the next row is requested
-// before the current one is summed); wave 0 then selects the experts. LDS: E
-// logits, then the row of h as fp64. PART: H is not a
-// multiple of 256 * ROUTE_CH, so the last pass over a row has chunks past
-// its end.
-// Phase marks of the router (entry, h staged, logits summed, selection
-// done); empty unless a profiling build defines it.
-#ifndef ROUTE_MARK
-#define ROUTE_MARK(phase)
-#endif
-
-template <bool LDS_H, bool PART, bool LEAN = false>
-__device__ __forceinline__ void route_token(const float *__restrict__ h, int H, const float *__restrict__ rw,
-                                            const float *__restrict__ rb, int E, int k, float *__restrict__ logits,
-                                            int32_t *__restrict__ topk_idx, float *__restrict__ topk_w,
-                                            const MoeTables &tb, int tables, int t, float *lds_f) {
-    const int lane = lane_id(), w = wave_id(), nw = blockDim.x >> 6;
-    double *h64 = reinterpret_cast<double *>(lds_f + ((E + 3) & ~3));
-    const float *ht = h + (int64_t)t * H;
-    constexpr int CH = ROUTE_CH;
-    // one pass per expert (H <= 256 CH) with the next expert's row requested
-    // before the current one is summed; LEAN (fewer registers) or longer
-    // rows: passes of 256 CH elements, one row at a time
-    const bool onepass = !LEAN && H <= 256 * CH;
-    auto load = [&](float4 (&v)[CH], const float *row, int i0) {
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-            const int i = i0 + 256 * j + 4 * lane;
-            v[j] = *reinterpret_cast<const float4 *>(row + (i < H ? i : H - 4));   // unconditional
-        }
-    };
-    ROUTE_MARK(0);
-    float4 wv[CH];
-    if (onepass && w < E) load(wv, rw + (int64_t)w * H, 0);   // in flight while h is staged
-    if (LDS_H) {
-        for (int i = threadIdx.x * 4; i < H; i += blockDim.x * 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(ht + i);
-            *reinterpret_cast<double2 *>(h64 + i) = make_double2(v.x, v.y);
-            *reinterpret_cast<double2 *>(h64 + i + 2) = make_double2(v.z, v.w);
-        }
-        __syncthreads();
-    }
-    ROUTE_MARK(1);
-    // lane l sums elements 256j + 4l + c (j = 0, 1, ..., c = 0..3) in that
-    // order (exact fp64 products); H is a multiple of 4, so a chunk is either
-    // wholly inside the row or wholly past its end
-    auto dot = [&](const float4 (&wv)[CH], const float4 (&hv)[CH], int i0, double &s) {
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-            const int i = i0 + 256 * j + 4 * lane;
-            const bool in = !PART || i < H;      // chunks past H add exact zero products
-            double2 a, b;
-            if (LDS_H) {
-                const int ic = in ? i : 0;
-                a = *reinterpret_cast<const double2 *>(h64 + ic);
-                b = *reinterpret_cast<const double2 *>(h64 + ic + 2);
-            } else {
-                a = make_double2(hv[j].x, hv[j].y);
-                b = make_double2(hv[j].z, hv[j].w);
-            }
-            s = __builtin_fma(in ? a.x : 0.0, (double)wv[j].x, s);
-            s = __builtin_fma(in ? a.y : 0.0, (double)wv[j].y, s);
-            s = __builtin_fma(in ? b.x : 0.0, (double)wv[j].z, s);
-            s = __builtin_fma(in ? b.y : 0.0, (double)wv[j].w, s);
-        }
-    };
-    auto finish = [&](int e, double s) {
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-        if (lane == 0) {
-            float f = (float)s;
-            if (rb) f = f + rb[e];
-            lds_f[e] = f;
-            logits[(int64_t)t * E + e] = f;
-        }
-    };
-    float4 hv[CH];
-    if (onepass) {
-        if (!LDS_H) load(hv, ht, 0);
-        for (int e = w; e < E; e += nw) {
-            if (e + nw < E) {   // the next expert's row goes out before this one is summed
-                float4 wn[CH];
-                load(wn, rw + (int64_t)(e + nw) * H, 0);
-                double s = 0.0;
-                dot(wv, hv, 0, s);
-                finish(e, s);
-#pragma unroll
-                for (int j = 0; j < CH; ++j) wv[j] = wn[j];
-            } else {
-                double s = 0.0;
-                dot(wv, hv, 0, s);
-                finish(e, s);
-            }
-        }
-    } else {
-        for (int e = w; e < E; e += nw) {
-            double s = 0.0;
-            for (int i0 = 0; i0 < H; i0 += 256 * CH) {
-                load(wv, rw + (int64_t)e * H, i0);
-                if (!LDS_H) load(hv, ht, i0);
-                __builtin_amdgcn_sched_barrier(0);   // every load issued before the first sum
-                dot(wv, hv, i0, s);
-            }
-            finish(e, s);
-        }
-    }
-    ROUTE_MARK(2);
-    __syncthreads();
-    ROUTE_MARK(3);
-    if (w == 0) route_select_any(lds_f, E, k, t, topk_idx, topk_w, tb, tables);
-    ROUTE_MARK(4);
-}
-
-template <bool LDS_H, bool PART>
-__global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ h, int H,
-                                                         const float *__restrict__ rw,
-                                                         const float *__restrict__ rb, int E, int k,
-                                                         float *__restrict__ logits,
-                                                         int32_t *__restrict__ topk_idx,
-                                                         float *__restrict__ topk_w, MoeTables tb, int tables) {
-    extern __shared__ __attribute__((aligned(16))) float lds_f[];
-    if (tables)   // one token: the counter block of the fused expert kernel that follows
-        for (int i = threadIdx.x; i < D1_WORDS; i += blockDim.x) tb.sync[i] = 0u;
-    route_token<LDS_H, PART>(h, H, rw, rb, E, k, logits, topk_idx, topk_w, tb, tables, blockIdx.x, lds_f);
-}
-
-// Router logits of one token spread over E one-wave workgroups: workgroup e
-// computes logit e exactly as a wave of route_token does (lane l sums
-// elements 256 j + 4 l + c in (j, c) order as exact fp64 products, chunks
-// past H adding exact zero products, then the butterfly), so the logits are
-// equal bit for bit. One workgroup read the whole 16 x 2048 router matrix in
-// about 6.5 us; 16 workgroups read one row each at the same time. Workgroup
-// 0 also clears the counter block of moe_decode1_kernel, which then selects
-// the experts itself. PART: H is not a multiple of 256 * ROUTE_CH.
+// Router logits of a few tokens spread over E x T one-wave workgroups:
+// workgroup (e, t) computes logit e of token t as the canonical sum (lane l
+// sums elements 256 j + 4 l + c in (j, c) order as exact fp64 products,
+// chunks past H adding exact zero products, then the butterfly), rounded to
+// fp32 once. One workgroup per token (each wave one expert row at a time)
+// took 5.5 us at 8 tokens x 16 experts and 20 us for one token of 128
+// experts; E x T workgroups read the rows at the same time. Workgroup (0, 0) also clears the counter block of
+// moe_decode1_kernel, which then selects the experts itself (else the
+// permutation selects them). PART: H is not a multiple of 256 * ROUTE_CH.
 template <bool PART>
 __global__ __launch_bounds__(64) void moe_route1_kernel(const float *__restrict__ h, int H,
                                                         const float *__restrict__ rw,
                                                         const float *__restrict__ rb, float *__restrict__ logits,
                                                         uint32_t *__restrict__ sync) {
     const int lane = threadIdx.x, e = blockIdx.x;
-    if (e == 0)
+    if (e == 0 && blockIdx.y == 0)
         for (int i = lane; i < D1_WORDS; i += 64) sync[i] = 0u;
+    h += (int64_t)blockIdx.y * H;
+    logits += (int64_t)blockIdx.y * gridDim.x;
     constexpr int CH = ROUTE_CH;
     const float *row = rw + (int64_t)e * H;
     double s = 0.0;
@@ -368,7 +240,7 @@ constexpr int RL_LD = 68;                  // LDS row of a pair: 64 lane partial
 static_assert(RL_ROWS % RL_NW == 0 && RL_RPW == 4, "the chunk wait below counts 4 copies per wave");
 static_assert(RL_NW * RL_PAIRS * RL_LD * 8 <= RL_STAGES * RL_ROWS * 1024, "reduction fits the chunk stages");
 
-// Router logits for many tokens, equal bit for bit to moe_route_kernel's:
+// Router logits for many tokens, equal bit for bit to moe_route1_kernel's:
 // lane l of each wave accumulates, for each (token, expert) pair of its
 // RL_T x RL_E tile, the exact fp64 products of elements 256 j + 4 l + c in
 // (j, c) order. The workgroup's RL_ROWS rows stream through LDS one 256-
@@ -604,12 +476,22 @@ static inline size_t perm_lds_bytes(int64_t E, int64_t N, bool match, bool stage
 //      LDS, copied out to perm[] in order afterwards (the scattered stores stay
 //      off the one CU's address path).
 // The result lists the assignments in (expert, a) order.
+// sel_logits (not null; fewer than ROUTE_TILE_TOKENS tokens): the router
+// wrote only the logits [N / k, E] (moe_route1_kernel); the waves first
+// select each token's experts and gates (route_select, one wave per token)
+// into idx / topk_w, then sort them.
 template <bool MATCH, bool STAGE>
-__global__ __launch_bounds__(1024) void moe_permute_kernel(const int32_t *__restrict__ idx, int N, int E,
-                                                           MoeTables tb) {
+__global__ __launch_bounds__(1024) void moe_permute_kernel(int32_t *__restrict__ idx, int N, int E, MoeTables tb,
+                                                           const float *__restrict__ sel_logits, int k,
+                                                           float *__restrict__ topk_w) {
     extern __shared__ __align__(16) int ws[];
     constexpr int U = 8;                   // assignments per lane per batch of loads
     const int lane = lane_id(), w = wave_id();
+    if (sel_logits) {
+        for (int t = w; t < N / k; t += PERM_WAVES)
+            route_select_any(sel_logits + (int64_t)t * E, E, k, t, idx, topk_w, tb, 0);
+        __syncthreads();   // idx is read below by every wave
+    }
     int *cnt = ws;
     int *off = ws + PERM_WAVES * E;
     const int head = (17 * E + 2) & ~1;
@@ -1060,8 +942,9 @@ __global__ void moe_combine_vec_kernel(const float *__restrict__ ysl, const int3
 // ------------------------------------------------- one-token decode, fused
 
 // The expert part of the MoE layer for one token with k <= 2 in one launch,
-// after the router (moe_route_kernel, which wrote topk_idx / topk_w and
-// zeroed the counter block). Workgroup r:
+// after topk_idx / topk_w were written (by the permutation's selection, or by
+// the caller: localai_hip_moe_experts1) and the counter block zeroed.
+// Workgroup r:
 //   r < n_gu          gate_up tile i of slot s (n_gu = k * inter / 16): the
 //                     expert's weights, act[s] rows; clears its share of out;
 //                     counts itself done
@@ -1483,7 +1366,7 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
                void *ws, hipStream_t s) {
     const int64_t I = gu->g.rows / 2;
     MoeTables tb = carve(ws, T, E, k, H, I);
-    const int one = T == 1 && tb.tile_w == 0;   // single token: the router writes the tables
+    const bool one = T == 1 && tb.tile_w == 0;
     // the fused expert kernel clears out while other workgroups still read h
     const bool apart = out + T * H <= h || h + T * H <= out;
     if (one && k <= 2 && E <= 64 && apart && moe_mfma_ok(gu, dn, h, H, I) && moe_decode1_ok(gu, dn)) {
@@ -1535,27 +1418,23 @@ int launch_moe(const float *h, int64_t T, int64_t H, const float *rw, const floa
                                topk_w, F16Rows{});
         }
     } else {
-        const size_t head = (size_t)((E + 3) & ~3) * 4;   // logits
-        const bool lds_h = head + (size_t)H * 8 <= ROUTE_LDS_BYTES;
-        const size_t sh = head + (lds_h ? (size_t)H * 8 : 0);
-        const bool part = H % (256 * ROUTE_CH) != 0;
-        auto go = [&](auto kern) {
-            hipLaunchKernelGGL(kern, dim3((unsigned)T), dim3(1024), sh, s, h, (int)H, rw, rb, (int)E, k, tb.logits,
-                               topk_idx, topk_w, tb, one);
-        };
-        if (lds_h)
-            part ? go(moe_route_kernel<true, true>) : go(moe_route_kernel<true, false>);
+        // few tokens: the logits over (expert, token) one-wave workgroups; the
+        // permutation selects the experts
+        const dim3 rgrid((unsigned)E, (unsigned)T);
+        if (H % (256 * ROUTE_CH))
+            hipLaunchKernelGGL(moe_route1_kernel<true>, rgrid, dim3(64), 0, s, h, (int)H, rw, rb, tb.logits, tb.sync);
         else
-            part ? go(moe_route_kernel<false, true>) : go(moe_route_kernel<false, false>);
+            hipLaunchKernelGGL(moe_route1_kernel<false>, rgrid, dim3(64), 0, s, h, (int)H, rw, rb, tb.logits, tb.sync);
     }
     LQ_HIP(hipGetLastError());
-    if (!one) {
+    {
         const int64_t N = T * k;
         const bool match = perm_lds_bytes(E, N, true, false) <= PERM_LDS_MAX;
         const bool stage = perm_lds_bytes(E, N, match, true) <= PERM_LDS_MAX;
         const size_t sh2 = perm_lds_bytes(E, N, match, stage);
+        const float *sel = T < ROUTE_TILE_TOKENS ? tb.logits : nullptr;
         auto go = [&](auto kern) {
-            hipLaunchKernelGGL(kern, dim3(1), dim3(1024), sh2, s, topk_idx, (int)N, (int)E, tb);
+            hipLaunchKernelGGL(kern, dim3(1), dim3(1024), sh2, s, topk_idx, (int)N, (int)E, tb, sel, k, topk_w);
         };
         if (match)
             stage ? go(moe_permute_kernel<true, true>) : go(moe_permute_kernel<true, false>);
