@@ -222,17 +222,19 @@ def test_router_logits_bit_exact(T, E, H, k):
     assert np.isfinite(out).all()
 
 
-def test_one_token_layer_repeated_and_graph_replayed():
+@pytest.mark.parametrize('k', (2, 8))
+def test_one_token_layer_repeated_and_graph_replayed(k):
     """The one-token layer runs as one launch whose workgroups hand work to
     each other through counters in the workspace; every call must leave them
     ready for the next: back-to-back calls with new tokens, a call of another
     size in between, and replays of a captured HIP graph (the token copied in
-    between replays) all match the oracle."""
+    between replays) all match the oracle. k = 8 takes the route, permute
+    and grouped kernels, whose tables must be rebuilt every call."""
     import torch
     from localai_amd import synth, device
     from localai_amd.moe import MoELayer
-    rng = np.random.default_rng(77)
-    E, H, I, k, t = 16, 1024, 512, 2, 14
+    rng = np.random.default_rng(77 + k)
+    E, H, I, t = 16, 1024, 512, 14
     rw, gu, dn = make_layer(rng, E, H, I, t)
     layer = MoELayer(rw, gu, dn, t, E, H, I, k)
 
@@ -555,6 +557,24 @@ def test_q8_0_experts_decode(T, k, I):
     rw, gu, dn = make_layer(rng, E, H, I, 8)
     h = synth.activations(rng, T, H)
     (out, idx, g), (rout, ridx, rg) = run_both(rw, gu, dn, 8, E, H, I, k, h)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
+    assert normwise_rel(out, rout) < 1e-5
+
+
+@pytest.mark.parametrize('t', (12, 14, 8))
+@pytest.mark.parametrize('E,k', [(16, 3), (128, 8), (64, 4), (8, 8)])
+def test_one_token_top_k(t, E, k):
+    """One token with top-3 .. top-8 (Qwen3-MoE decode: 128 experts, top-8):
+    the router over (expert, token) workgroups, the selection inside the
+    permutation, the grouped kernels and the combine. Routing, gates and
+    output against the oracle."""
+    from localai_amd import synth
+    rng = np.random.default_rng(E * 7 + k + t)
+    H, I = 1024, 512
+    rw, gu, dn = make_layer(rng, E, H, I, t)
+    h = synth.activations(rng, 1, H)
+    (out, idx, g), (rout, ridx, rg) = run_both(rw, gu, dn, t, E, H, I, k, h, bias=synth.zipf_bias(E))
     np.testing.assert_array_equal(idx, ridx)
     np.testing.assert_allclose(g, rg, rtol=1e-5, atol=1e-6)
     assert normwise_rel(out, rout) < 1e-5
