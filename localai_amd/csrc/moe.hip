@@ -182,9 +182,10 @@ constexpr int ROUTE_CH = 8;
 // chunks past H adding exact zero products, then the butterfly), rounded to
 // fp32 once. One workgroup per token (each wave one expert row at a time)
 // took 5.5 us at 8 tokens x 16 experts and 20 us for one token of 128
-// experts; E x T workgroups read the rows at the same time. Workgroup (0, 0) also clears the counter block of
-// moe_decode1_kernel, which then selects the experts itself (else the
-// permutation selects them). PART: H is not a multiple of 256 * ROUTE_CH.
+// experts; E x T workgroups read the rows at the same time. Workgroup
+// (0, 0) also clears the counter block of moe_decode1_kernel, which then
+// selects the experts itself (else the permutation selects them). PART: H
+// is not a multiple of 256 * ROUTE_CH.
 template <bool PART>
 __global__ __launch_bounds__(64) void moe_route1_kernel(const float *__restrict__ h, int H,
                                                         const float *__restrict__ rw,
@@ -1200,8 +1201,8 @@ static int launch_grouped(const localai_qmat *m, const MoeTables &tb, const floa
 // Q8_0 with rows of whole 256-value blocks, since the kernels read x 256
 // values a block) with K <= 64 blocks of 256: one block per wave (up to 16
 // waves) for K <= 16, four per wave for K <= 32 (up to 8 waves, room for
-// the registers), four per wave streamed through two register sets for
-// K <= 64 (16 waves).
+// the registers), eight per wave streamed through two register sets for
+// K <= 64 (8 waves; moe_mfma_gate_up_pipe / moe_mfma_down_pipe).
 static bool moe_mfma_ok(const localai_qmat *gu, const localai_qmat *dn, const float *h, int64_t H, int64_t I) {
     const bool q80 = gu->g.type == LQ_Q8_0;
     // the streamed kernels' LDS (8 waves of eight staged blocks, ~76 KB)
