@@ -9,9 +9,12 @@
 // upload into a temporary copy. Calls are serialised by one mutex, as the
 // reference serialises its pool (engine/native_quant.cpp:361-363).
 //
-// x and the result travel through pinned host staging buffers (hipHostMalloc,
-// grown on demand) with asynchronous copies on the library's legacy stream,
-// so a call waits once, after the download, rather than once per copy.
+// x goes up through a pinned host staging buffer (hipHostMalloc, grown on
+// demand) with an asynchronous copy on the library's legacy stream; the
+// matvecs store the result straight into a second pinned buffer (host memory
+// the device addresses: 30.0 -> 22.1 us per Q4_K 14336 x 4096 call against a
+// download copy; a copy kernel for x instead of the DMA copy gained nothing),
+// the GEMM through an asynchronous download; a call waits once, at the end.
 //
 // The exports return void like the reference; a failure leaves NaN in `out`
 // and the status in localai_hip_last_status().
@@ -138,17 +141,19 @@ int run(int t, const uint8_t *raw, const float *x, float *out, int rows, int col
         if (!st) st = launch_gemm(m->g, m->tiles ? nullptr : m->data, m->tiles, g_x, tokens, g_y, 1, tokens, g_ws, wsb,
                                   s);
     } else if (!st) {
+        // the matvecs store y straight into the pinned staging buffer (host
+        // memory the device can address): no download copy
         if (m->tiles && tokens == 1 && mt_matvec_ok(m->g)) {
-            st = launch_matvec_mfma(m->g, m->tiles, g_x, g_y, s);
+            st = launch_matvec_mfma(m->g, m->tiles, g_x, g_hy, s);
         } else if (m->tiles && mt_matvec_ok(m->g)) {
-            st = launch_matvec_mfma_tok(m->g, m->tiles, g_x, cols, g_y, rows, tokens, s);
+            st = launch_matvec_mfma_tok(m->g, m->tiles, g_x, cols, g_hy, rows, tokens, s);
         } else {
             const uint8_t *planes = qmat_planes(m, s, &st);
-            if (planes) st = launch_matvec(m->g, planes, g_x, cols, g_y, rows, tokens, s);
+            if (planes) st = launch_matvec(m->g, planes, g_x, cols, g_hy, rows, tokens, s);
         }
     }
     if (!st) {
-        hipError_t e = hipMemcpyAsync(g_hy, g_y, ny * 4, hipMemcpyDeviceToHost, s);
+        hipError_t e = gemm ? hipMemcpyAsync(g_hy, g_y, ny * 4, hipMemcpyDeviceToHost, s) : hipSuccess;
         if (e == hipSuccess) e = hipStreamSynchronize(s);
         if (e != hipSuccess) st = hip_fail(e, "download y");
     }
