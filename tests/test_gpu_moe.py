@@ -184,7 +184,9 @@ def test_mfma_decode_path_shapes(t, k, H, I, T):
 
 
 @pytest.mark.parametrize('T,E,H,k', [
-    (1, 8, 288, 2),       # one token: the per-token router; H ends in a partial 256-chunk
+    (1, 8, 288, 2),       # one token: the one-wave router, fused expert kernel; H ends in a partial chunk
+    (1, 130, 256, 8),     # one token, 130 experts, top-8: one-wave router, selection in the permutation
+    (5, 200, 288, 3),     # a few tokens, partial 256-chunk, more experts than a wave's lanes
     (15, 20, 256, 3),     # just below the tiled router
     (16, 20, 288, 3),     # tiled router, partial chunk, experts not a multiple of 16
     (37, 80, 320, 5),     # E > 64: DPP top-k; tokens not a multiple of 8
@@ -387,6 +389,9 @@ def expected_tables(idx, E, tile_w):
     (64, 2200, 8),     # perm too large to stage: scattered stores
     (512, 200, 8),     # too many experts for the LDS lane masks: ballots
     (1024, 40, 2),     # the largest expert count
+    (1024, 3, 16),     # the largest expert count and top-k below the tiled router
+    (130, 1, 8),       # one token over more than 64 experts: selected in the permutation
+    (16, 15, 4),       # the most tokens of the one-wave router
 ])
 def test_routing_tables_are_a_stable_sort(E, T, k):
     """perm lists the assignments in (expert, a) order, pos inverts it, and
