@@ -378,7 +378,7 @@ def expected_tables(idx, E, tile_w):
 
 
 @pytest.mark.parametrize('E,T,k', [
-    (16, 1, 2),        # one token: the router writes the tables
+    (16, 1, 2),        # one token (Q8_0 experts of inter 128: route, permute, grouped kernels)
     (16, 8, 2),        # few assignments over few experts (one wave's worth)
     (64, 16, 4),       # 64 assignments over 64 experts
     (2, 5, 1),         # two experts, one expert per token
