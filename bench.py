@@ -82,7 +82,7 @@ MALL_BYTES = 256 << 20
 METRIC = 'µs/layer + achieved HBM GB/s (% of peak) for Q4_K/Q6_K matvec & MoE layer'
 WORKLOADS = ['llama3_8b_decode_layer', 'q4k_matvec', 'q8_0_matvec', 'vocab_head', 'legacy_host_matvec', 'q8_0_prefill',
              'zaya_moe_decode', 'qwen3_moe_prefill', 'llama3_8b_layer_chain', 'llama3_8b_attention_decode',
-             'qwen35_delta_net_step', 'hbm_read_floor', 'hbm_copy']
+             'qwen35_delta_net_step', 'hbm_read_floor', 'hbm_copy', 'moe_decode_shapes']
 # the default run: the headline, then these under "workloads"
 DEFAULT_SUITE = ['q4k_matvec', 'q8_0_prefill', 'zaya_moe_decode', 'qwen3_moe_prefill', 'q8_0_matvec', 'vocab_head',
                  'legacy_host_matvec', 'llama3_8b_layer_chain', 'llama3_8b_attention_decode', 'qwen35_delta_net_step',
@@ -808,6 +808,33 @@ def wl_zaya(args, torch, device, synth):
             'roofline': roof, 'cpu_baseline': cpu}
 
 
+def wl_moe_decode_shapes(args, torch, device, synth):
+    """Decode (fewer than 32 tokens) of two more MoE shapes, not in the default
+    run: Qwen3-MoE-like (hidden 2048, 128 Q4_K experts, top-8, intermediate
+    768, Zipf router bias) at 1 and 4 tokens -- the router over (expert,
+    token) one-wave workgroups, the top-k inside the permutation, the grouped
+    i8 MFMA kernels and the combine -- and Mixtral-like (hidden 4096, 8 Q4_K
+    experts, top-2, intermediate 14336: down rows of 56 blocks of 256, the
+    streamed kernels) at 1 and 8 tokens."""
+    per_q4 = lambda H, I: (2 * I * (H // 256) + H * (I // 256)) * 144   # noqa: E731
+    cases = {}
+    for name, (E, H, I, k, bias), Ts in (('qwen3_like', (128, 2048, 768, 8, synth.zipf_bias(128)), (1, 4)),
+                                         ('mixtral_like', (8, 4096, 14336, 2, None), (1, 8))):
+        for T in Ts:
+            ms, nbytes, distinct, copies, _ = _moe_gpu(args, torch, device, synth, E, H, I, k, 12, T, bias,
+                                                       per_q4(H, I), name)
+            _moe_gpu.last = None
+            cases[f'{name}_t{T}'] = {'us_per_layer': round(ms * 1e3, 3), 'distinct_experts': distinct,
+                                     'algorithmic_bytes': nbytes, 'GB/s': round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                     'layer_copies_rotated': copies}
+    first = cases['qwen3_like_t1']
+    return {'value': first['GB/s'], 'unit': 'GB/s', 'ms_per_step': first['us_per_layer'] * 1e-3,
+            'us_per_layer': first['us_per_layer'], 'hbm_frac': round(first['GB/s'] / HBM_PEAK_GBS, 4),
+            'dtype': 'fp32', 'data': 'synthetic (seeded Q4_K experts, router N(0,0.02), h N(0,1))',
+            'config': {'workload': 'moe_decode_qwen3_like_and_mixtral_like', 'cases': cases},
+            'roofline': None, 'cpu_baseline': None}
+
+
 def wl_qwen3(args, torch, device, synth):
     E, H, I, k, t, T = 128, 2048, 768, 8, 12, 512
     per_expert = 2 * I * (H // 256) * 144 + H * (I // 256) * 144
@@ -1118,7 +1145,7 @@ FUNCS = {'llama3_8b_decode_layer': 'wl_layer', 'q4k_matvec': 'wl_q4k', 'q8_0_mat
          'q8_0_prefill': 'wl_q8_prefill',
          'zaya_moe_decode': 'wl_zaya', 'qwen3_moe_prefill': 'wl_qwen3', 'llama3_8b_layer_chain': 'wl_chain',
          'hbm_read_floor': 'wl_floor', 'hbm_copy': 'wl_copy', 'llama3_8b_attention_decode': 'wl_attention',
-         'qwen35_delta_net_step': 'wl_delta_net'}
+         'qwen35_delta_net_step': 'wl_delta_net', 'moe_decode_shapes': 'wl_moe_decode_shapes'}
 
 
 def run_workload(name, args, torch, device, synth):
