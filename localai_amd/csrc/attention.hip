@@ -404,12 +404,16 @@ int launch_attention_decode(const float *q, const float *k_new, const float *v_n
 // here is the fp64 exponential rounded once to fp32 (correctly rounded); the
 // reference's np.exp on float32 can differ from it in the last bit or two.
 //
-// delta_net_kernel (key_dim == KF, 64 or 128): a workgroup of 4 waves owns 64
-// value columns of one head. The waves copy the [KF, 64] slab into LDS
-// together (every load in flight at once), wave 0 runs the two ordered chains
-// (lane = column; the scaled column in registers between them) and writes the
-// updated slab to LDS, and the 4 waves store it. delta_net_any_kernel: any
-// key_dim, one wave per 64 columns straight from global memory.
+// delta_net_kernel (key_dim KF, 64 or 128): a workgroup of 4 waves owns 64
+// value columns of one head; lane = column. Only the two sums are serial, so
+// only they stay on one wave: each wave scales its own rows of the slab (rows
+// 4 at a time, interleaved over the waves), keeps them in registers, and
+// writes the products keep * k to LDS; wave 0 adds them in ki order (128
+// dependent adds, the products read 4 at a time); then each wave forms its
+// rows' updated values, stores them and writes val * q; wave 0 adds those.
+// Every product and sum is the reference loop's own fp32 operation.
+// delta_net_any_kernel: any key_dim, one wave per 64 columns straight from
+// global memory.
 template <int KF>
 __global__ __launch_bounds__(256) void delta_net_kernel(float *__restrict__ state, const float *__restrict__ q,
                                                         const float *__restrict__ k, const float *__restrict__ v,
@@ -417,46 +421,74 @@ __global__ __launch_bounds__(256) void delta_net_kernel(float *__restrict__ stat
                                                         const float *__restrict__ beta, float *__restrict__ core,
                                                         int VD) {
 #pragma clang fp contract(off)
-    __shared__ float S_s[KF][64];
-    __shared__ float k_s[KF], q_s[KF];
-    const int h = blockIdx.y, c0 = blockIdx.x * 64, tid = (int)threadIdx.x, col = tid & 63, w = tid >> 6;
+    constexpr int RW = KF / 4, LD = KF + 4;  // rows per wave; padded column stride of the product table
+    __shared__ __align__(16) float prod[64 * LD];
+    __shared__ float delta_s[64];
+    const int h = blockIdx.y, c0 = blockIdx.x * 64, tid = (int)threadIdx.x, col = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: k and q by scalar loads
     const bool in = c0 + col < VD;
+    // columns past VD read column c0 and store nothing
     float *hs = state + (int64_t)h * KF * VD + c0 + (in ? col : 0);
-    // every load requested before any is used (columns past VD read column c0)
-    float t[KF / 4];
+    const float *kh = k + (int64_t)h * KF, *qh = q + (int64_t)h * KF;
+    float keep[RW];
 #pragma unroll
-    for (int i = 0; i < KF / 4; ++i) t[i] = hs[(int64_t)(w + 4 * i) * VD];
+    for (int i = 0; i < RW; ++i) keep[i] = hs[(int64_t)(16 * (i >> 2) + 4 * w + (i & 3)) * VD];
+    const float factor = (float)exp((double)decay[h]);
+    float *mine = prod + col * LD + 4 * w;
 #pragma unroll
-    for (int i = 0; i < KF / 4; ++i) S_s[w + 4 * i][col] = in ? t[i] : 0.0f;
-    if (tid < KF) {
-        k_s[tid] = k[(int64_t)h * KF + tid];
-        q_s[tid] = q[(int64_t)h * KF + tid];
+    for (int i = 0; i < RW; i += 4) {
+        float4 pr;
+        float *pp = &pr.x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            keep[i + j] = keep[i + j] * factor;
+            pp[j] = keep[i + j] * kh[16 * (i >> 2) + 4 * w + j];
+        }
+        *reinterpret_cast<float4 *>(mine + 16 * (i >> 2)) = pr;
     }
     __syncthreads();
     if (w == 0) {
-        const float factor = (float)exp((double)decay[h]);
-        float keep[KF], pred = 0.0f, acc = 0.0f;
+        float pred = 0.0f;
 #pragma unroll
-        for (int ki = 0; ki < KF; ++ki) {
-            keep[ki] = S_s[ki][col] * factor;
-            pred = pred + keep[ki] * k_s[ki];
+        for (int ki = 0; ki < KF; ki += 4) {
+            const float4 pr = *reinterpret_cast<const float4 *>(prod + col * LD + ki);
+            pred = pred + pr.x;
+            pred = pred + pr.y;
+            pred = pred + pr.z;
+            pred = pred + pr.w;
         }
-        const float delta = in ? (v[(int64_t)h * VD + c0 + col] - pred) * beta[h] : 0.0f;
-#pragma unroll
-        for (int ki = 0; ki < KF; ++ki) {
-            const float val = keep[ki] + k_s[ki] * delta;
-            S_s[ki][col] = val;
-            acc = acc + val * q_s[ki];
-        }
-        if (in) core[(int64_t)h * VD + c0 + col] = acc;
+        delta_s[col] = in ? (v[(int64_t)h * VD + c0 + col] - pred) * beta[h] : 0.0f;
     }
     __syncthreads();
+    const float delta = delta_s[col];
+#pragma unroll
+    for (int i = 0; i < RW; i += 4) {
+        float4 pr;
+        float *pp = &pr.x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ki = 16 * (i >> 2) + 4 * w + j;
+            keep[i + j] = keep[i + j] + kh[ki] * delta;
+            pp[j] = keep[i + j] * qh[ki];
+        }
+        *reinterpret_cast<float4 *>(mine + 16 * (i >> 2)) = pr;
+    }
     if (in)
 #pragma unroll
-        for (int i = 0; i < KF / 4; ++i) {
-            const int ki = w + 4 * i;
-            hs[(int64_t)ki * VD] = S_s[ki][col];
+        for (int i = 0; i < RW; ++i) hs[(int64_t)(16 * (i >> 2) + 4 * w + (i & 3)) * VD] = keep[i];
+    __syncthreads();
+    if (w == 0 && in) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int ki = 0; ki < KF; ki += 4) {
+            const float4 pr = *reinterpret_cast<const float4 *>(prod + col * LD + ki);
+            acc = acc + pr.x;
+            acc = acc + pr.y;
+            acc = acc + pr.z;
+            acc = acc + pr.w;
         }
+        core[(int64_t)h * VD + c0 + col] = acc;
+    }
 }
 
 __global__ __launch_bounds__(64) void delta_net_any_kernel(float *__restrict__ state, const float *__restrict__ q,
