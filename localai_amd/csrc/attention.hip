@@ -131,7 +131,10 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
     constexpr int C = 16 * RF, P = 4 * RF;   // positions per workgroup / per wave
     __shared__ float red_m[4][GT], red_l[4][GT];
     __shared__ __attribute__((aligned(16))) float red_o[4][GT * NV * ATTN_PIECE];
-    const int kh = blockIdx.y, split = blockIdx.x;
+    // kv head = workgroup index mod n_kv: workgroups go to the XCDs round
+    // robin, so with 8 kv heads (or a multiple) each kv head's chunks, and the
+    // merge workgroups of its query heads, share one XCD and its L2
+    const int kh = (int)blockIdx.x % a.n_kv, split = (int)blockIdx.x / a.n_kv;
     const int wave = wave_id(), lane = lane_id(), pg = lane >> 4, c = lane & 15;
     const int hd = a.hd, G = a.G;
     const int64_t row = (int64_t)a.n_kv * hd;
@@ -272,8 +275,8 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
     }
 }
 
-// Merge of the chunks: workgroup (h, b) writes values 64 b .. 64 b + 63 of
-// query head h. With M the largest chunk maximum (base-2 units), out =
+// Merge of the chunks: workgroup (x, b) writes values 64 b .. 64 b + 63 of
+// query head h = (x mod n_kv) G + x / n_kv. With M the largest chunk maximum (base-2 units), out =
 // sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i. The workgroup's waves split
 // the chunks ATTN_MC at a time (wave w: chunks 32 w, 32 (w + nw), ...), so a
 // lane requests its ATTN_MC chunk values and the chunks' (max, l) in one round;
@@ -281,7 +284,8 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
 // and the waves meet in LDS.
 __global__ __launch_bounds__(512) void attn_merge_kernel(AttnArgs a) {
     __shared__ float red_m[8], red_l[8], red_o[8][64];
-    const int h = blockIdx.x, kh = h / a.G, g = h % a.G, hd = a.hd, ns = a.nsplit;
+    // the kv head is the workgroup index mod n_kv, as in the chunk kernel
+    const int kh = (int)blockIdx.x % a.n_kv, g = (int)blockIdx.x / a.n_kv, h = kh * a.G + g, hd = a.hd, ns = a.nsplit;
     const int lane = lane_id(), wave = wave_id(), nw = (int)(blockDim.x >> 6);
     const int d = 64 * blockIdx.y + lane;
     const int64_t rec = hd + 2, stride = (int64_t)a.G * rec;
@@ -371,7 +375,7 @@ int launch_attention_decode(const float *q, const float *k_new, const float *v_n
     a.out = out;
     if (nsplit > 1 && (!ws || ws_bytes < (int64_t)n_kv * nsplit * a.G * (hd + 2) * 4))
         return fail(LOCALAI_EARG, "attention: workspace too small");
-    const dim3 grid((unsigned)nsplit, (unsigned)n_kv);
+    const dim3 grid((unsigned)(nsplit * n_kv));
 #define LQ_ATT(NV, GT)                                                                                        \
     if (nv == NV && gt == GT) {                                                                               \
         hipLaunchKernelGGL((attn_chunk_kernel<NV, GT, attn_rounds(NV, GT)>), grid, dim3(256), 0, s, a);       \
