@@ -401,9 +401,9 @@ int launch_attention_decode(const float *q, const float *k_new, const float *v_n
 // (engine/qwen35.py:224-252). Per head h, with state S [key_dim, value_dim]:
 //   S *= exp(decay[h]);  pred = S^T k;  delta = (v - pred) * beta[h]
 //   S += k delta^T;      core = S^T q
-// The lane that owns column vi of S runs the reference loop's exact
-// float32 operations in its order: each product and each sum rounded on its
-// own (no fused multiply-add), ki ascending, so state and core equal the
+// Column vi of S goes through the reference loop's exact float32
+// operations: each product and each sum rounded on its own (no fused
+// multiply-add), the sums in ki ascending order, so state and core equal the
 // reference loop's bit for bit given the same factor exp(decay). The factor
 // here is the fp64 exponential rounded once to fp32 (correctly rounded); the
 // reference's np.exp on float32 can differ from it in the last bit or two.
